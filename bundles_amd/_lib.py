@@ -1,0 +1,105 @@
+"""ctypes binding of libq36.so, the extern "C" boundary declared in include/q36_abi.h.
+
+The structures below mirror the header field for field; tests check their sizes against the
+library's own sizeof.  Every call raises RuntimeError with q36_last_error() on a non-zero
+return code.  There is no fallback: a missing library is an ImportError-like failure.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libq36.so")
+
+Q36_OK, Q36_EINVAL, Q36_ELAUNCH = 0, 1, 2
+Q36_MOE_INT8, Q36_MOE_FP8 = 0, 1
+
+P = C.c_void_p
+I32 = C.c_int32
+SZ = C.c_size_t
+
+
+class MoeArgs(C.Structure):
+    _fields_ = [("M", I32), ("E", I32), ("H", I32), ("I", I32), ("topk", I32), ("dtype", I32),
+                ("x", P), ("router_w", P), ("router_bias", P), ("positions", P),
+                ("w13", P), ("s13", P), ("w2", P), ("s2", P), ("sw13", P), ("ss13", P), ("sw2", P), ("ss2", P),
+                ("gate_w", P), ("out", P), ("workspace", P), ("workspace_bytes", SZ),
+                ("dbg_acc13", P), ("dbg_acc2", P), ("dbg_h", P)]
+
+
+class MoeWsLayout(C.Structure):
+    _fields_ = [(n, SZ) for n in ("logits", "ids", "wts", "counts", "offsets", "perm", "inv_perm", "active", "ctl",
+                                  "xq", "xs", "h", "y", "total")]
+
+
+class GdnArgs(C.Structure):
+    _fields_ = [("B", I32), ("T", I32), ("mixed", P), ("z", P), ("a", P), ("b", P), ("conv_state", P),
+                ("conv_w", P), ("A_log", P), ("dt_bias", P), ("S0", P), ("norm_w", P), ("eps", C.c_float),
+                ("out", P), ("snaps", P)]
+
+
+class AttnArgs(C.Structure):
+    _fields_ = [("T", I32), ("max_pos", I32), ("x", P), ("wqg", P), ("sqg", P), ("wk", P), ("sk", P), ("wv", P),
+                ("sv", P), ("q_norm_w", P), ("k_norm_w", P), ("eps", C.c_float), ("cos_sin", P),
+                ("positions", P), ("q", P), ("gate", P), ("k", P), ("v", P), ("k8", P), ("v8", P),
+                ("workspace", P), ("workspace_bytes", SZ)]
+
+
+class OprojArgs(C.Structure):
+    _fields_ = [("T", I32), ("attn", P), ("gate", P), ("wo", P), ("so", P), ("out", P), ("workspace", P),
+                ("workspace_bytes", SZ)]
+
+
+class LmheadArgs(C.Structure):
+    _fields_ = [("R", I32), ("H", I32), ("V", I32), ("h", P), ("norm_w", P), ("eps", C.c_float), ("wq", P),
+                ("ws", P), ("ids", P), ("logits", P), ("workspace", P), ("workspace_bytes", SZ)]
+
+
+_lib = None
+
+# (name, restype, argtypes) of every exported symbol; tests check that each one resolves.
+SYMBOLS = [
+    ("q36_abi_version", I32, []),
+    ("q36_last_error", C.c_char_p, []),
+    ("q36_moe_workspace_bytes", SZ, [I32, I32, I32, I32, I32, I32]),
+    ("q36_moe_workspace_layout", I32, [I32, I32, I32, I32, I32, I32, C.POINTER(MoeWsLayout)]),
+    ("q36_moe_route", I32, [C.POINTER(MoeArgs), P]),
+    ("q36_moe_forward", I32, [C.POINTER(MoeArgs), P]),
+    ("q36_quant_rows_i8", I32, [P, C.c_int64, I32, P, P, P]),
+    ("q36_quant_blocks_e4m3", I32, [P, C.c_int64, I32, P, P, P]),
+]
+OPTIONAL_SYMBOLS: list = []
+
+
+def lib():
+    """Load libq36.so (built by bundles_amd.build); raise if it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libq36.so is not built ({LIB_PATH}); run bundles_amd.build.build() first")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in SYMBOLS:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != Q36_OK:
+        msg = lib().q36_last_error().decode(errors="replace")
+        kind = "invalid argument" if rc == Q36_EINVAL else "launch failure"
+        raise RuntimeError(f"{what}: {kind}: {msg}")
+
+
+def ptr(t) -> int | None:
+    """Device (or host) address of a torch tensor, None for None."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(stream=None) -> int | None:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream

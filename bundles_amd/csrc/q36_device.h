@@ -1,0 +1,103 @@
+// Device-side primitives shared by the q36 kernels (gfx950, wave64).
+//
+// Every floating-point step that decides a bit of an integer output (expert ids, quantized
+// activations, argmax ids) is spelled as an explicit IEEE operation: the library is compiled with
+// -ffp-contract=off, fused multiply-adds are written as __builtin_fmaf, and divisions are the
+// correctly rounded '/' (hipcc's default).  The same steps on the host give the same bits.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q36 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// float -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+
+// float -> OCP e4m3fn code: round to nearest even, saturate to +-448, NaN -> 0x7f.
+__device__ __forceinline__ uint32_t f2e4m3(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  float af = __uint_as_float(a);
+  if (af >= 448.f) return sign | 0x7eu;
+  if (af < 0.015625f) return sign | (uint32_t)__builtin_rintf(af * 512.f);
+  int e = (int)((a >> 23) & 0xffu) - 127;
+  uint32_t keep = (a & 0x7fffffu) >> 20, rest = a & 0xfffffu;
+  if (rest > 0x80000u || (rest == 0x80000u && (keep & 1u))) keep++;
+  if (keep == 8u) { keep = 0; e++; }
+  if (e > 8 || (e == 8 && keep > 6u)) return sign | 0x7eu;
+  return sign | ((uint32_t)(e + 7) << 3) | keep;
+}
+__device__ __forceinline__ float e4m3_to_f(uint32_t b) {
+  uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  float v;
+  if (e == 15u && m == 7u) v = __builtin_nanf("");
+  else if (e == 0u) v = __builtin_ldexpf((float)m, -9);
+  else v = __builtin_ldexpf(1.f + (float)m * 0.125f, (int)e - 7);
+  return (b & 0x80u) ? -v : v;
+}
+
+// exp(x): Cody-Waite reduction with ln2 split hi/lo, degree-7 Taylor polynomial by Horner fma,
+// ldexp.  All steps correctly rounded, so host and device agree bit for bit.
+__device__ __forceinline__ float expf_q(float x) {
+  if (x != x) return x;
+  if (x > 88.7228394f) return __builtin_inff();
+  if (x < -103.972084f) return 0.f;
+  float n = __builtin_rintf(x * 1.44269504088896341f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.428606765330187e-06f, r);
+  float p = 1.f / 5040.f;
+  p = __builtin_fmaf(p, r, 1.f / 720.f);
+  p = __builtin_fmaf(p, r, 1.f / 120.f);
+  p = __builtin_fmaf(p, r, 1.f / 24.f);
+  p = __builtin_fmaf(p, r, 1.f / 6.f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.f);
+  p = __builtin_fmaf(p, r, 1.f);
+  return __builtin_ldexpf(p, (int)n);
+}
+__device__ __forceinline__ float sigmoid_q(float z) { return 1.f / (1.f + expf_q(-z)); }
+
+// xor-butterfly over the 64 lanes (offsets 32 .. 1): every lane ends with the same total.
+__device__ __forceinline__ float wave_sum_bfly(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Round half away from zero and clamp to +-127 (the int8 activation / weight rule).
+__device__ __forceinline__ int round_i8(float v) {
+  float r = v >= 0.f ? __builtin_floorf(v + 0.5f) : -__builtin_floorf(0.5f - v);
+  r = fminf(fmaxf(r, -127.f), 127.f);
+  return (int)r;
+}
+
+}  // namespace q36

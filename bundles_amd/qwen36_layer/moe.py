@@ -1,0 +1,161 @@
+"""Decode MoE row batch on libq36 (q36_moe_route / q36_moe_forward).
+
+Mirrors the reference's decode MoE glue (R = qwen36_nodes_kb34, L = R/qwen36_layer):
+  Workspace        <- L/i8x_decode.py:495-526 (persistent per-device scratch, zero on entry)
+  ExpertWeights    <- the i8x expert copy (L/i8x_kernels.py:69-110, L/i8x_reloc.py:193-241):
+                      here either int8 per-channel (W8A8) or e4m3 128x128 block-scaled weights
+  prepare_experts  <- i8x_kernels.make_copy / fill_layer (quantize once at prepare time)
+  route            <- qk_route.route (L/qk_route.cu:1124)
+  moe_row_batch    <- i8x_decode.moe_row_batch (L/i8x_decode.py:528-605)
+All launches go on the current torch stream; nothing allocates inside moe_row_batch except the
+output tensor when the caller passes none (the reference does the same, L/i8x_decode.py:575).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from .. import _lib
+from .._lib import MoeArgs, MoeWsLayout, Q36_MOE_FP8, Q36_MOE_INT8, check, ptr
+
+MAX_TOKENS = 256  # the reference's row-batch limit (L/layer.py:50)
+
+
+@dataclass
+class ExpertWeights:
+    """Quantized routed experts + shared expert of one MoE layer (device tensors)."""
+    dtype: int                  # Q36_MOE_INT8 or Q36_MOE_FP8
+    w13: torch.Tensor           # [E, 2I, H] int8 / uint8 (e4m3 codes)
+    s13: torch.Tensor           # INT8 [E, 2I]; FP8 [E, 2I/128, H/128]
+    w2: torch.Tensor            # [E, H, I]
+    s2: torch.Tensor            # INT8 [E, H]; FP8 [E, H/128, I/128]
+    sw13: torch.Tensor          # [2I, H]
+    ss13: torch.Tensor
+    sw2: torch.Tensor           # [H, I]
+    ss2: torch.Tensor
+
+    @property
+    def E(self) -> int:
+        return self.w13.shape[0]
+
+    @property
+    def H(self) -> int:
+        return self.w13.shape[2]
+
+    @property
+    def I(self) -> int:  # noqa: E743
+        return self.w13.shape[1] // 2
+
+
+def quantize_rows_i8(w: torch.Tensor, stream=None):
+    """Per-row int8 (s = amax/127, round half away): w bf16 [N, K] -> (q int8 [N, K], s fp32 [N])."""
+    w2 = w.reshape(-1, w.shape[-1]).contiguous()
+    N, K = w2.shape
+    q = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    s = torch.empty(N, dtype=torch.float32, device=w.device)
+    check(_lib.lib().q36_quant_rows_i8(ptr(w2), N, K, ptr(q), ptr(s), _lib.stream_handle(stream)),
+          "q36_quant_rows_i8")
+    return q.view(w.shape), s.view(w.shape[:-1])
+
+
+def quantize_blocks_e4m3(w: torch.Tensor, stream=None):
+    """128x128 block e4m3: w bf16 [..., N, K] -> (q uint8 [..., N, K], s fp32 [..., N/128, K/128])."""
+    N, K = w.shape[-2:]
+    lead = w.shape[:-2]
+    w2 = w.reshape(-1, K).contiguous()
+    q = torch.empty(w2.shape, dtype=torch.uint8, device=w.device)
+    s = torch.empty((w2.shape[0] // 128, K // 128), dtype=torch.float32, device=w.device)
+    check(_lib.lib().q36_quant_blocks_e4m3(ptr(w2), w2.shape[0], K, ptr(q), ptr(s), _lib.stream_handle(stream)),
+          "q36_quant_blocks_e4m3")
+    return q.view(w.shape), s.view(*lead, N // 128, K // 128)
+
+
+def prepare_experts(w13: torch.Tensor, w2: torch.Tensor, sw13: torch.Tensor, sw2: torch.Tensor,
+                    dtype: int) -> ExpertWeights:
+    """Quantize bf16 expert weights once (prepare time).  w13 [E,2I,H], w2 [E,H,I], shared [2I,H], [H,I]."""
+    if dtype == Q36_MOE_INT8:
+        q13, s13 = quantize_rows_i8(w13)
+        q2, s2 = quantize_rows_i8(w2)
+        qs13, ss13 = quantize_rows_i8(sw13)
+        qs2, ss2 = quantize_rows_i8(sw2)
+    elif dtype == Q36_MOE_FP8:
+        q13, s13 = quantize_blocks_e4m3(w13)
+        q2, s2 = quantize_blocks_e4m3(w2)
+        qs13, ss13 = quantize_blocks_e4m3(sw13)
+        qs2, ss2 = quantize_blocks_e4m3(sw2)
+    else:
+        raise ValueError(f"unknown MoE dtype {dtype}")
+    return ExpertWeights(dtype, q13, s13, q2, s2, qs13, ss13, qs2, ss2)
+
+
+def workspace_layout(M: int, E: int, H: int, I: int, topk: int, dtype: int) -> MoeWsLayout:  # noqa: E741
+    L = MoeWsLayout()
+    check(_lib.lib().q36_moe_workspace_layout(M, E, H, I, topk, dtype, C.byref(L)), "q36_moe_workspace_layout")
+    return L
+
+
+class Workspace:
+    """Persistent per-device scratch for row batches of up to max_tokens rows (zeroed once)."""
+
+    def __init__(self, E: int, H: int, I: int, topk: int, dtype: int, device, max_tokens: int = MAX_TOKENS):  # noqa: E741
+        self.E, self.H, self.I, self.topk, self.dtype, self.max_tokens = E, H, I, topk, dtype, max_tokens
+        nbytes = _lib.lib().q36_moe_workspace_bytes(max_tokens, E, H, I, topk, dtype)
+        self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+    def views(self, M: int) -> dict:
+        """Typed views of the lists written by the last call with M rows (for tests and callers)."""
+        L = workspace_layout(M, self.E, self.H, self.I, self.topk, self.dtype)
+        b, E, k, S = self.buf, self.E, self.topk, M * self.topk
+
+        def v(off, n, dt):
+            nbytes = n * torch.empty((), dtype=dt).element_size()
+            return b[off:off + nbytes].view(dt)
+        ng = self.H // 128 if self.dtype == Q36_MOE_FP8 else 1
+        return dict(
+            logits=v(L.logits, M * E, torch.float32).view(M, E), ids=v(L.ids, S, torch.int32).view(M, k),
+            wts=v(L.wts, S, torch.float32).view(M, k), counts=v(L.counts, E, torch.int32),
+            offsets=v(L.offsets, E + 1, torch.int32), perm=v(L.perm, S, torch.int32),
+            inv_perm=v(L.inv_perm, S, torch.int32), active=v(L.active, E, torch.int32),
+            ctl=v(L.ctl, 64, torch.int32), xq=v(L.xq, M * self.H, torch.uint8).view(M, self.H),
+            xs=v(L.xs, M * ng, torch.float32).view(M, ng),
+            h=v(L.h, (S + M) * self.I, torch.bfloat16).view(S + M, self.I),
+            y=v(L.y, (S + M) * self.H, torch.bfloat16).view(S + M, self.H))
+
+
+def _args(x, positions, router_w, gate_w, ew, topk, ws: Workspace, out, router_bias, debug):
+    M, H = x.shape
+    if M > ws.max_tokens:
+        raise ValueError(f"moe_row_batch: {M} rows exceed the workspace's {ws.max_tokens}")
+    for name, t in (("x", x), ("router_w", router_w), ("gate_w", gate_w)):
+        if t is not None and (t.dtype != torch.bfloat16 or not t.is_contiguous()):
+            raise ValueError(f"moe_row_batch: {name} must be contiguous bfloat16")
+    if positions is not None and (positions.dtype != torch.int32 or not positions.is_contiguous()):
+        raise ValueError("moe_row_batch: positions must be contiguous int32")
+    if router_bias is not None and (router_bias.dtype != torch.float32 or not router_bias.is_contiguous()):
+        raise ValueError("moe_row_batch: router_bias must be contiguous float32")
+    dbg = debug or {}
+    w = [None] * 8 if ew is None else [ew.w13, ew.s13, ew.w2, ew.s2, ew.sw13, ew.ss13, ew.sw2, ew.ss2]
+    return MoeArgs(M, router_w.shape[0], H, ws.I, topk, ws.dtype, ptr(x), ptr(router_w), ptr(router_bias),
+                   ptr(positions), *(ptr(t) for t in w), ptr(gate_w), ptr(out), ptr(ws.buf), ws.buf.numel(),
+                   ptr(dbg.get("acc13")), ptr(dbg.get("acc2")), ptr(dbg.get("h")))
+
+
+def route(x, positions, router_w, topk: int, ws: Workspace, router_bias=None, stream=None):
+    """Routing only (ids, weights, expert lists and quantized x in the workspace); returns ws.views(M)."""
+    a = _args(x, positions, router_w, None, None, topk, ws, None, router_bias, None)
+    check(_lib.lib().q36_moe_route(C.byref(a), _lib.stream_handle(stream)), "q36_moe_route")
+    return ws.views(x.shape[0])
+
+
+def moe_row_batch(x, positions, router_w, gate_w, ew: ExpertWeights, topk: int, ws: Workspace, out=None,
+                  router_bias=None, debug=None, stream=None):
+    """out[M, H] = shared_gate * shared_expert(x) + sum_j w_j * expert_{id_j}(x)  (bf16)."""
+    if ew.E != router_w.shape[0] or ew.I != ws.I or ew.dtype != ws.dtype or ew.E != ws.E:
+        raise ValueError("moe_row_batch: expert weights, router and workspace disagree on E / I / dtype")
+    if out is None:
+        out = torch.empty_like(x)
+    a = _args(x, positions, router_w, gate_w, ew, topk, ws, out, router_bias, debug)
+    check(_lib.lib().q36_moe_forward(C.byref(a), _lib.stream_handle(stream)), "q36_moe_forward")
+    return out

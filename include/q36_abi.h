@@ -1,0 +1,126 @@
+/* q36 -- MI355X (gfx950) kernel nodes for the qwen36_layer / qwen36_lmhead8 bundle slots.
+ *
+ * The drop-in boundary: a flat extern "C" API over raw device pointers.  Every entry point
+ * validates its arguments, launches on the caller's stream, never allocates, never frees and
+ * never synchronises, so a caller may capture it into a hipGraph.  Return codes: Q36_OK, or
+ * Q36_EINVAL (a shape / alignment / size violation; nothing was launched) or Q36_ELAUNCH (a HIP
+ * error); q36_last_error() gives the thread's last message.  No exception crosses this boundary.
+ *
+ * Reference interfaces replaced (R = qwen36_nodes_kb34, L = R/qwen36_layer, H = R/qwen36_lmhead8):
+ *   q36_moe_route      <- qk_route.route / route48 / route16w     (L/qk_route.cu:1124,1162,1219)
+ *   q36_moe_forward    <- i8x_decode.moe_row_batch: route + fused/up + down + combine
+ *                         (L/i8x_decode.py:528-605; L/qk_moe_up16.cu:915; L/qk_moe_dn16.cu:301;
+ *                          L/qk_route.cu:1270)
+ *   q36_gdn_verify     <- qk_gdn_verify.gdn_verify_fused           (L/qk_gdn_verify.cu:841-849)
+ *   q36_attn_proj      <- qkv_proj + attn_prefill_front            (L/qk_proj_decode.cu:434;
+ *                         L/qk_attn_verify.cu:981)
+ *   q36_attn_oproj     <- o_proj of the gated attention output    (L/attn_fused.py:232-273;
+ *                         gate L/qk_attn_verify.cu:730-737)
+ *   q36_lmhead_argmax  <- lmh8_w8a8x2 / w8a8_linear + the stock greedy sampler
+ *                         (L/qk_proj_decode.cu:1354; H/w8a8.py:116-120; H/node.py:136-151)
+ *   q36_quant_rows_i8  <- lmhead8.quantize_rows / w8a8.quantize_act (H/lmhead8.py:111; H/w8a8.py:77)
+ *   q36_quant_blocks_e4m3 <- (no reference counterpart: the 128x128 block-scaled e4m3 weight
+ *                         format the configuration asks for)
+ */
+#ifndef Q36_ABI_H
+#define Q36_ABI_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q36_ABI_VERSION 1
+#define Q36_OK 0
+#define Q36_EINVAL 1
+#define Q36_ELAUNCH 2
+
+#define Q36_MOE_INT8 0 /* W8A8: per-token int8 x, per-channel int8 weights, fp32 scales */
+#define Q36_MOE_FP8 1  /* OCP e4m3fn: per-token x 128-group x, 128x128 block weight scales */
+
+typedef void* q36_stream_t; /* a hipStream_t (0 = the null stream) */
+
+int q36_abi_version(void);
+const char* q36_last_error(void);
+
+/* ---------------------------------------------------------------------------------------
+ * Decode MoE block (one row batch of M <= 256 tokens).
+ * Layouts (row-major, K innermost):
+ *   x bf16 [M,H]; router_w bf16 [E,H]; router_bias fp32 [E] or NULL (added before the bf16
+ *   rounding of the logits); positions int32 [M] or NULL (rows whose position is 0 are padding:
+ *   no experts, zero output);
+ *   w13 [E,2I,H] (gate rows 0..I-1, up rows I..2I-1), w2 [E,H,I], int8 or e4m3 bytes;
+ *   INT8 scales: s13 fp32 [E,2I], s2 fp32 [E,H]; FP8 scales: s13 [E,2I/128,H/128], s2 [E,H/128,I/128];
+ *   shared expert sw13 [2I,H], sw2 [H,I] with scales of the same form (no E);
+ *   gate_w bf16 [H]; out bf16 [M,H].
+ * Constraints: H % 512 == 0, H <= 8192, I % 128 == 0, I <= 1024, E % 64 == 0, E <= 1024,
+ *   1 <= topk <= min(16, E), 1 <= M <= 256; every pointer 16-byte aligned.
+ * Workspace: q36_moe_workspace_bytes() bytes, 256-byte aligned, ZEROED ONCE after allocation;
+ *   the kernels leave it in the state they need on the next call (self-resetting ticket).
+ *   q36_moe_workspace_layout() gives the byte offset of each list inside it.
+ * Debug outputs (NULL to skip), indexed by sorted position p (routed 0..M*topk-1 in expert order,
+ *   shared M*topk + t): dbg_acc13 int32 [M*topk+M, 2I], dbg_acc2 int32 [M*topk+M, H] (INT8 only:
+ *   the GEMM accumulators before scaling), dbg_h bf16 [M*topk+M, I] (SwiGLU output).
+ * Calls that overlap on one workspace race; distinct workspaces are independent. */
+typedef struct q36_moe_args {
+  int32_t M, E, H, I, topk, dtype;
+  const void* x;
+  const void* router_w;
+  const float* router_bias;
+  const int32_t* positions;
+  const void* w13;
+  const float* s13;
+  const void* w2;
+  const float* s2;
+  const void* sw13;
+  const float* ss13;
+  const void* sw2;
+  const float* ss2;
+  const void* gate_w;
+  void* out;
+  void* workspace;
+  size_t workspace_bytes;
+  int32_t* dbg_acc13;
+  int32_t* dbg_acc2;
+  void* dbg_h;
+} q36_moe_args;
+
+typedef struct q36_moe_ws_layout {
+  size_t logits;   /* fp32 [M,E] bf16-rounded router logits (+bias) */
+  size_t ids;      /* int32 [M,topk], -1 for padding rows */
+  size_t wts;      /* fp32 [M,topk] renormalised routing weights */
+  size_t counts;   /* int32 [E] */
+  size_t offsets;  /* int32 [E+1] exclusive scan of counts */
+  size_t perm;     /* int32 [M*topk] sorted position -> slot t*topk+j (-1 past offsets[E]) */
+  size_t inv_perm; /* int32 [M*topk] slot -> sorted position (-1 for padding) */
+  size_t active;   /* int32 [E] experts with counts > 0, ascending */
+  size_t ctl;      /* int32 [64]: [0] route ticket (kept zero between calls), [1] n_active */
+  size_t xq;       /* quantized x [M,H] */
+  size_t xs;       /* fp32 [M, H/128] (INT8: [M]) */
+  size_t h;        /* bf16 [M*topk+M, I] */
+  size_t y;        /* bf16 [M*topk+M, H] */
+  size_t total;
+} q36_moe_ws_layout;
+
+size_t q36_moe_workspace_bytes(int32_t M, int32_t E, int32_t H, int32_t I, int32_t topk, int32_t dtype);
+int q36_moe_workspace_layout(int32_t M, int32_t E, int32_t H, int32_t I, int32_t topk, int32_t dtype,
+                             q36_moe_ws_layout* out);
+/* Routing only: logits, ids, wts and the expert lists, plus the quantized x. */
+int q36_moe_route(const q36_moe_args* a, q36_stream_t stream);
+/* The whole MoE block: route, routed + shared experts, sigmoid-gated shared add, combine. */
+int q36_moe_forward(const q36_moe_args* a, q36_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Prepare-time weight quantizers (device to device).
+ *   q36_quant_rows_i8:     w bf16 [N,K] -> q int8 [N,K], s fp32 [N]   (s = amax/127, half-away)
+ *   q36_quant_blocks_e4m3: w bf16 [N,K] -> q e4m3 [N,K], s fp32 [N/128, K/128]
+ *                          (s = amax/448, q = e4m3_rn_sat(w * (448/amax)))
+ * K % 128 == 0 (and N % 128 == 0 for blocks). */
+int q36_quant_rows_i8(const void* w, int64_t N, int32_t K, int8_t* q, float* s, q36_stream_t stream);
+int q36_quant_blocks_e4m3(const void* w, int64_t N, int32_t K, uint8_t* q, float* s, q36_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
