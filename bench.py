@@ -1,0 +1,193 @@
+"""Benchmark of the qwen36 kernel nodes on one MI355X.
+
+Headline (the configuration the metric is quoted on): the fp8 e4m3 MoE block at decode batch 64
+(512 experts top-10, intermediate 512 + shared expert, Zipf(1.1)-skewed router), one step = one
+MoE layer over one batch of 64 tokens with every input resident in HBM.  value = tokens/s of that
+layer.  Beside it: the roofline of the dominant kernel (the expert up-projection, HBM-bound), the
+other nodes' step times, and the CPU oracle timed on this host's cores on the same workload.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+
+
+def cpu_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def events_time(fn, steps, torch):
+    """Average ms of fn() over `steps` calls, timed with events on the current stream."""
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def bench_moe(args, torch, dev):
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import moe
+
+    M, E, H, I, K = 64, 512, 2048, 512, 10
+    d = synth.moe_inputs(M, dev, seed=0, E=E, zipf=1.1)
+    ew = moe.prepare_experts(d["w13"], d["w2"], d["sw13"], d["sw2"], moe.Q36_MOE_FP8)
+    del d["w13"], d["w2"]
+    ws = moe.Workspace(E, H, I, K, moe.Q36_MOE_FP8, dev)
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        moe.moe_row_batch(d["x"], None, d["router_w"], d["gate_w"], ew, K, ws, out=out, router_bias=d["router_bias"])
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    U = int(ws.views(M)["ctl"][1].item())
+
+    # the decode step runs as one captured graph (the engine captures the whole verify step)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(max(1, args.warmup)):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        g.replay()
+    torch.cuda.synchronize()
+    ms_graph = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # eager launches, and each phase alone with events on its stream (for the kernel roofline)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_eager = (time.perf_counter() - t0) * 1e3 / args.steps
+    phases = dict(moe.moe_phases(d["x"], None, d["router_w"], d["gate_w"], ew, K, ws, out,
+                                 router_bias=d["router_bias"]))
+    phase_ms = {}
+    for name in ("route", "up", "down", "combine"):
+        others = {"route": [], "up": ["route"], "down": ["route", "up"], "combine": ["route", "up", "down"]}[name]
+        for o in others:
+            phases[o]()
+        phase_ms[name] = events_time(phases[name], args.steps, torch)
+
+    # algorithmic bytes (each weight byte once per unique use, plus activations in and out)
+    S = M * K
+    up_w = 2 * I * H + (2 * I // 128) * (H // 128) * 4
+    dn_w = H * I + (H // 128) * (I // 128) * 4
+    bytes_up = (U + 1) * up_w + M * H + M * (H // 128) * 4 + (S + M) * I * 2
+    bytes_down = (U + 1) * dn_w + (S + M) * I * 2 + (S + M) * H * 2
+    bytes_layer = (U + 1) * (up_w + dn_w) + E * H * 2 + M * H * 2 * 2
+    t_up = phase_ms["up"] * 1e-3
+    res = dict(
+        ms_graph=ms_graph, ms_eager=ms_eager, phase_ms=phase_ms, unique_experts=U,
+        tokens_per_s=M / (ms_graph * 1e-3),
+        bytes_up=bytes_up, bytes_down=bytes_down, bytes_layer=bytes_layer,
+        up_gbs=bytes_up / t_up / 1e9, down_gbs=bytes_down / (phase_ms["down"] * 1e-3) / 1e9,
+        layer_gbs=bytes_layer / (ms_graph * 1e-3) / 1e9,
+    )
+    res["_host"] = (ew, d)
+    return res
+
+
+def cpu_moe_baseline(res, seconds):
+    """The C oracle on this host's cores over the same batch-64 fp8 layer (whole batches)."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+
+    ew, d = res["_host"]
+
+    def h16(t):
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    def hn(t):
+        return t.contiguous().cpu().numpy()
+    hw = [hn(getattr(ew, k)) for k in ("w13", "s13", "w2", "s2", "sw13", "ss13", "sw2", "ss2")]
+    x, wr, gw, bias = h16(d["x"]), h16(d["router_w"]), h16(d["gate_w"]), hn(d["router_bias"])
+    cores = cpu_cores()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.moe(1, x, wr, *hw, gw, 10, bias=bias, n_threads=cores)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 50:
+            break
+    return dict(value=64 * n / el, unit="tokens/s", cores=cores, kind="port",
+                sample=f"{n} full batch-64 fp8 MoE layers (512 experts, top-10, Zipf router) in {el:.1f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the MoE, GDN and lm_head nodes are measured on one "
+                                   "MI355X; multi-GPU sharding is a design note only"}))
+        sys.exit(2)
+
+    import torch
+    from bundles_amd import _lib
+    _lib.lib()  # fails loudly when libq36.so is not built
+    dev = torch.device("cuda:0")
+    print(f"bench: MoE fp8 batch 64, steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
+    moe_res = bench_moe(args, torch, dev)
+    print(f"bench: MoE done ({moe_res['ms_graph'] * 1e3:.1f} us/layer)", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu:
+        print("bench: CPU oracle baseline", file=sys.stderr, flush=True)
+        cpu = cpu_moe_baseline(moe_res, args.cpu_seconds)
+    moe_res.pop("_host")
+
+    up_gbs = moe_res["up_gbs"]
+    line = {
+        "metric": "MoE-layer decode tokens/s @bs64; % HBM/MFMA roofline; GDN-verify us/step",
+        "value": round(moe_res["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(moe_res["ms_graph"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e4m3",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized to e4m3 128x128 blocks)",
+        "config": {"workload": "fp8 MoE block, decode batch 64 (config 2)", "tokens": 64, "hidden": 2048,
+                   "experts": 512, "topk": 10, "intermediate": 512, "shared_experts": 1,
+                   "router_skew": "Zipf(1.1)", "unique_experts": moe_res["unique_experts"]},
+        "roofline": {"bound": "hbm", "kernel": "moe_up_kernel<fp8>", "achieved": round(up_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(up_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+        "moe": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in moe_res.items()},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

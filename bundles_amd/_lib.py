@@ -65,6 +65,9 @@ SYMBOLS = [
     ("q36_moe_workspace_bytes", SZ, [I32, I32, I32, I32, I32, I32]),
     ("q36_moe_workspace_layout", I32, [I32, I32, I32, I32, I32, I32, C.POINTER(MoeWsLayout)]),
     ("q36_moe_route", I32, [C.POINTER(MoeArgs), P]),
+    ("q36_moe_up", I32, [C.POINTER(MoeArgs), P]),
+    ("q36_moe_down", I32, [C.POINTER(MoeArgs), P]),
+    ("q36_moe_combine", I32, [C.POINTER(MoeArgs), P]),
     ("q36_moe_forward", I32, [C.POINTER(MoeArgs), P]),
     ("q36_quant_rows_i8", I32, [P, C.c_int64, I32, P, P, P]),
     ("q36_quant_blocks_e4m3", I32, [P, C.c_int64, I32, P, P, P]),

@@ -899,23 +899,58 @@ extern "C" int q36_moe_route(const q36_moe_args* a, q36_stream_t stream) {
   return launch_route(d, a->dtype, static_cast<hipStream_t>(stream));
 }
 
+namespace q36 {
+namespace {
+int launch_up(const MoeDev& d, int dtype, hipStream_t st) {
+  const int units = 1 + (d.E < d.M * d.k ? d.E : d.M * d.k);
+  if (dtype == Q36_MOE_FP8)
+    moe_up_kernel<Q36_MOE_FP8><<<units * (d.I / 16), 256, 0, st>>>(d);
+  else
+    moe_up_kernel<Q36_MOE_INT8><<<units * (d.I / 16), 256, 0, st>>>(d);
+  return check_launch("q36_moe_up");
+}
+int launch_down(const MoeDev& d, int dtype, hipStream_t st) {
+  const int units = 1 + (d.E < d.M * d.k ? d.E : d.M * d.k);
+  if (dtype == Q36_MOE_FP8)
+    moe_down_kernel<Q36_MOE_FP8><<<units * (d.H / 64), 256, 0, st>>>(d);
+  else
+    moe_down_kernel<Q36_MOE_INT8><<<units * (d.H / 64), 256, 0, st>>>(d);
+  return check_launch("q36_moe_down");
+}
+int launch_combine(const MoeDev& d, hipStream_t st) {
+  moe_combine_kernel<<<d.M, 256, 0, st>>>(d);
+  return check_launch("q36_moe_combine");
+}
+}  // namespace
+}  // namespace q36
+
+extern "C" int q36_moe_up(const q36_moe_args* a, q36_stream_t stream) {
+  MoeDev d;
+  int rc = validate(a, &d, true);
+  return rc ? rc : launch_up(d, a->dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int q36_moe_down(const q36_moe_args* a, q36_stream_t stream) {
+  MoeDev d;
+  int rc = validate(a, &d, true);
+  return rc ? rc : launch_down(d, a->dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int q36_moe_combine(const q36_moe_args* a, q36_stream_t stream) {
+  MoeDev d;
+  int rc = validate(a, &d, true);
+  return rc ? rc : launch_combine(d, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int q36_moe_forward(const q36_moe_args* a, q36_stream_t stream) {
   MoeDev d;
   int rc = validate(a, &d, true);
   if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = launch_route(d, a->dtype, st);
-  if (rc) return rc;
-  const int units = 1 + (d.E < d.M * d.k ? d.E : d.M * d.k);
-  if (a->dtype == Q36_MOE_FP8) {
-    moe_up_kernel<Q36_MOE_FP8><<<units * (d.I / 16), 256, 0, st>>>(d);
-    moe_down_kernel<Q36_MOE_FP8><<<units * (d.H / 64), 256, 0, st>>>(d);
-  } else {
-    moe_up_kernel<Q36_MOE_INT8><<<units * (d.I / 16), 256, 0, st>>>(d);
-    moe_down_kernel<Q36_MOE_INT8><<<units * (d.H / 64), 256, 0, st>>>(d);
-  }
-  moe_combine_kernel<<<d.M, 256, 0, st>>>(d);
-  return check_launch("q36_moe_forward");
+  if ((rc = launch_route(d, a->dtype, st))) return rc;
+  if ((rc = launch_up(d, a->dtype, st))) return rc;
+  if ((rc = launch_down(d, a->dtype, st))) return rc;
+  return launch_combine(d, st);
 }
 
 extern "C" int q36_quant_rows_i8(const void* w, int64_t N, int32_t K, int8_t* q, float* s, q36_stream_t stream) {

@@ -159,3 +159,18 @@ def moe_row_batch(x, positions, router_w, gate_w, ew: ExpertWeights, topk: int, 
     a = _args(x, positions, router_w, gate_w, ew, topk, ws, out, router_bias, debug)
     check(_lib.lib().q36_moe_forward(C.byref(a), _lib.stream_handle(stream)), "q36_moe_forward")
     return out
+
+
+def moe_phases(x, positions, router_w, gate_w, ew: ExpertWeights, topk: int, ws: Workspace, out, router_bias=None,
+               stream=None):
+    """The same block as moe_row_batch as four separately launched phases (route, up, down, combine);
+    returns the list of (name, callable) so a caller can schedule or time each one."""
+    a = _args(x, positions, router_w, gate_w, ew, topk, ws, out, router_bias, None)
+    L = _lib.lib()
+
+    def call(fn, name):
+        def run():
+            check(fn(C.byref(a), _lib.stream_handle(stream)), name)
+        return run
+    return [("route", call(L.q36_moe_route, "q36_moe_route")), ("up", call(L.q36_moe_up, "q36_moe_up")),
+            ("down", call(L.q36_moe_down, "q36_moe_down")), ("combine", call(L.q36_moe_combine, "q36_moe_combine"))]

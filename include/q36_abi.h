@@ -54,7 +54,7 @@ const char* q36_last_error(void);
  *   INT8 scales: s13 fp32 [E,2I], s2 fp32 [E,H]; FP8 scales: s13 [E,2I/128,H/128], s2 [E,H/128,I/128];
  *   shared expert sw13 [2I,H], sw2 [H,I] with scales of the same form (no E);
  *   gate_w bf16 [H]; out bf16 [M,H].
- * Constraints: H % 512 == 0, H <= 8192, I % 128 == 0, I <= 1024, E % 64 == 0, E <= 1024,
+ * Constraints: H == 2048 and I == 512 (this build), E % 64 == 0, 64 <= E <= 1024,
  *   1 <= topk <= min(16, E), 1 <= M <= 256; every pointer 16-byte aligned.
  * Workspace: q36_moe_workspace_bytes() bytes, 256-byte aligned, ZEROED ONCE after allocation;
  *   the kernels leave it in the state they need on the next call (self-resetting ticket).
@@ -108,7 +108,16 @@ int q36_moe_workspace_layout(int32_t M, int32_t E, int32_t H, int32_t I, int32_t
                              q36_moe_ws_layout* out);
 /* Routing only: logits, ids, wts and the expert lists, plus the quantized x. */
 int q36_moe_route(const q36_moe_args* a, q36_stream_t stream);
-/* The whole MoE block: route, routed + shared experts, sigmoid-gated shared add, combine. */
+/* The phases of the block, each one stream-ordered launch set over the same workspace, for
+ * callers that schedule them apart (the reference exposes the same split: up
+ * L/qk_moe_up16.cu:329, down L/qk_moe_dn16.cu:301, combine_norm L/qk_route.cu:1270).
+ *   q36_moe_up:      routed + shared gate/up GEMM and SwiGLU -> h   (needs q36_moe_route first)
+ *   q36_moe_down:    down GEMM x routing weight -> y               (needs q36_moe_up first)
+ *   q36_moe_combine: out = bf16(fma(sigmoid(x . gate_w), y_shared, sum_j y_j)) */
+int q36_moe_up(const q36_moe_args* a, q36_stream_t stream);
+int q36_moe_down(const q36_moe_args* a, q36_stream_t stream);
+int q36_moe_combine(const q36_moe_args* a, q36_stream_t stream);
+/* The whole MoE block: route, up, down, combine. */
 int q36_moe_forward(const q36_moe_args* a, q36_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
