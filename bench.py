@@ -59,7 +59,10 @@ def bench_moe(args, torch, dev):
     for _ in range(max(1, args.warmup)):
         step()
     torch.cuda.synchronize()
-    U = int(ws.views(M)["ctl"][1].item())
+    ids = ws.views(M)["ids"]
+    U = int(torch.unique(ids[ids >= 0]).numel())
+    counts = torch.bincount(ids[ids >= 0].flatten().long(), minlength=E)
+    top_counts = [int(c) for c in torch.sort(counts, descending=True).values[:12].tolist()]
 
     # the decode step runs as one captured graph (the engine captures the whole verify step)
     g = torch.cuda.CUDAGraph()
@@ -99,7 +102,7 @@ def bench_moe(args, torch, dev):
     bytes_layer = (U + 1) * (up_w + dn_w) + E * H * 2 + M * H * 2 * 2
     t_up = phase_ms["up"] * 1e-3
     res = dict(
-        ms_graph=ms_graph, ms_eager=ms_eager, phase_ms=phase_ms, unique_experts=U,
+        ms_graph=ms_graph, ms_eager=ms_eager, phase_ms=phase_ms, unique_experts=U, top_expert_tokens=top_counts,
         tokens_per_s=M / (ms_graph * 1e-3),
         bytes_up=bytes_up, bytes_down=bytes_down, bytes_layer=bytes_layer,
         up_gbs=bytes_up / t_up / 1e9, down_gbs=bytes_down / (phase_ms["down"] * 1e-3) / 1e9,

@@ -19,6 +19,8 @@
 // The shared expert is unit 0 of the up/down grids and covers every token.
 #include <string.h>
 
+#include <type_traits>
+
 #include "q36_device.h"
 #include "q36_host.h"
 
@@ -53,6 +55,9 @@ struct MoeDev {
   int32_t* inv_perm;
   int32_t* active;
   int32_t* ctl;
+  int32_t* ecount;  // tokens per expert, counted by route_topk (zeroed by route_logits)
+  int32_t* eact;    // experts with tokens, in the order route_topk met them; ctl[2] counts them
+  int32_t* elist;   // [E][M] slots of each expert, in the order route_topk met them
   uint8_t* xq;
   float* xs;
   uint16_t* h;
@@ -83,70 +88,93 @@ __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
 // ------------------------------------------------------------------------------------------
 // 1. router logits + activation quantization
 // ------------------------------------------------------------------------------------------
-// Router workgroup (expert group of 16, token tile of 16): wave w owns experts e0 .. e0+3; lane l
-// accumulates the 8-element chunks c = l + 64 j with fma in (j, i) order, the 64 partials meet in
-// an xor butterfly: the fixed reduction order the oracle restates (q36o_dot_canon).
+// Router workgroup = 8 tokens x 16 experts; wave w owns experts e0 .. e0 + 3.  The x tile is staged
+// in LDS; lane l keeps the 8-element chunks c = l + 64 j (j < H/512) of its 4 expert rows in
+// registers and accumulates every (token, expert) dot with fma in (j, i) order.  The 32 lane
+// partials of each output then meet in a recursive-halving reduce-scatter (xor 32 .. 2, then a
+// final xor-1 add): every sum pairs the same two operands as the xor butterfly (offsets 32 .. 1)
+// of q36o_dot_canon, so the logits are bit-identical to the oracle's.
+// One reduce-scatter stage over N values: lanes whose bit O is set keep the upper half.
+template <int N, int O>
+__device__ __forceinline__ void rs_stage(float* v, int lane) {
+  const bool hi = (lane & O) != 0;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float send = hi ? v[i] : v[i + N / 2];
+    const float keep = hi ? v[i + N / 2] : v[i];
+    v[i] = keep + __shfl_xor(send, O);
+  }
+}
+constexpr int kRouteTT = 8;   // tokens per router workgroup
+constexpr int kRouteH = 2048;
 template <int DT>
 __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_router_wg) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int bid = blockIdx.x;
   if (bid < n_router_wg) {
+    constexpr int NJ = kRouteH / 512;
+    __shared__ v4i xt[kRouteTT][kRouteH / 8];
     const int neg = d.E / 16;
     const int eg = bid % neg, tg = bid / neg;
     const int e0 = eg * 16 + wave * 4;
-    const int t0 = tg * 16;
-    const int nt = min(16, d.M - t0);
-    float acc[16][4];
+    const int t0 = tg * kRouteTT;
+    v4i w[4][NJ];
 #pragma unroll
-    for (int t = 0; t < 16; ++t)
+    for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[t][e] = 0.f;
-    const int nj = d.H / 512;
-    for (int j = 0; j < nj; ++j) {
-      const int c = lane + 64 * j;
-      v4i w[4];
+      for (int j = 0; j < NJ; ++j)
+        w[e][j] = ldg16(reinterpret_cast<const uint8_t*>(d.wr + (size_t)(e0 + e) * kRouteH + 8 * (lane + 64 * j)));
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = ldg16(reinterpret_cast<const uint8_t*>(d.wr + (size_t)(e0 + e) * d.H + 8 * c));
-#pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        if (t < nt) {
-          v4i xv = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)(t0 + t) * d.H + 8 * c));
-          float xf[8];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            xf[2 * q] = bf_lo((uint32_t)xv[q]);
-            xf[2 * q + 1] = bf_hi((uint32_t)xv[q]);
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float a = acc[t][e];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              a = __builtin_fmaf(xf[2 * q], bf_lo((uint32_t)w[e][q]), a);
-              a = __builtin_fmaf(xf[2 * q + 1], bf_hi((uint32_t)w[e][q]), a);
-            }
-            acc[t][e] = a;
-          }
-        }
-      }
+    for (int r = 0; r < kRouteTT * kRouteH / 8 / 256; ++r) {
+      const int c = threadIdx.x + 256 * r;
+      const int t = c / (kRouteH / 8), cc = c % (kRouteH / 8);
+      const int tok = min(t0 + t, d.M - 1);
+      xt[t][cc] = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)tok * kRouteH + 8 * cc));
     }
+    __syncthreads();
+    float v[kRouteTT * 4];
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      if (t < nt) {
+    for (int i = 0; i < kRouteTT * 4; ++i) v[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int t = 0; t < kRouteTT; ++t) {
+        const v4i xv = xt[t][lane + 64 * j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float v = wave_sum_bfly(acc[t][e]);
-          if (d.bias) v = v + d.bias[e0 + e];
-          if (lane == e) d.logits[(size_t)(t0 + t) * d.E + e0 + e] = rbf(v);
+          float a = v[t * 4 + e];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            a = __builtin_fmaf(bf_lo((uint32_t)xv[q]), bf_lo((uint32_t)w[e][j][q]), a);
+            a = __builtin_fmaf(bf_hi((uint32_t)xv[q]), bf_hi((uint32_t)w[e][j][q]), a);
+          }
+          v[t * 4 + e] = a;
         }
       }
+    // reduce-scatter: after the stage with offset o a lane keeps the half of its outputs whose
+    // index bit matches its lane bit; 32 outputs over xor 32 .. 2 leave output (lane >> 1).
+    static_assert(kRouteTT * 4 == 32, "the stage list below assumes 32 outputs per wave");
+    rs_stage<32, 32>(v, lane);
+    rs_stage<16, 16>(v, lane);
+    rs_stage<8, 8>(v, lane);
+    rs_stage<4, 4>(v, lane);
+    rs_stage<2, 2>(v, lane);
+    float tot = v[0] + __shfl_xor(v[0], 1);
+    const int idx = lane >> 1;                 // index bits 4..0 = lane bits 5..1
+    const int t = idx >> 2, e = idx & 3;
+    if ((lane & 1) == 0 && t0 + t < d.M) {
+      if (d.bias) tot = tot + d.bias[e0 + e];
+      d.logits[(size_t)(t0 + t) * d.E + e0 + e] = rbf(tot);
     }
     return;
   }
   // Quantization workgroup: one token.  Thread tid owns the 8-element chunks tid + 256 r.
   const int t = bid - n_router_wg;
   const int tid = threadIdx.x;
+  if (t == 0) {
+    for (int e = tid; e < d.E; e += 256) d.ecount[e] = 0;  // route_topk counts into them next
+    if (tid == 0) d.ctl[2] = 0;
+  }
   const int nr = d.H / 2048 > 0 ? d.H / 2048 : 1;
   __shared__ float red[4];
   float xf[4][8];
@@ -198,7 +226,7 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
         const float s = m / 448.f, inv = m > 0.f ? 448.f / m : 0.f;
         uint32_t wd[2] = {0u, 0u};
 #pragma unroll
-        for (int q = 0; q < 8; ++q) wd[q >> 2] |= f2e4m3(xf[r][q] * inv) << (8 * (q & 3));
+        for (int q = 0; q < 8; q += 2) wd[q >> 2] |= f2e4m3x2_hw(xf[r][q] * inv, xf[r][q + 1] * inv) << (8 * (q & 3));
         *reinterpret_cast<uint2*>(d.xq + (size_t)t * d.H + 8 * c) = make_uint2(wd[0], wd[1]);
         if ((c & 15) == 0) d.xs[(size_t)t * ng + c / 16] = s;
       }
@@ -207,35 +235,148 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
 }
 
 // ------------------------------------------------------------------------------------------
-// 2. top-k per token, then the expert lists (last workgroup)
+// 2. top-k per token (one wave per token), and the expert lists
 // ------------------------------------------------------------------------------------------
-__device__ void build_lists(const MoeDev& d) {
-  __shared__ int cnt[kMaxE];
-  __shared__ int off[kMaxE + 1];
-  __shared__ uint32_t mask[kMaxE][kMaxM / 32];
-  __shared__ int wsum[4], wact[4];
+// Order-preserving 32-bit key of a bf16-valued logit and its expert id: (value desc, id asc) is
+// the unsigned order of the key, so one wave max picks the next expert of the top-k.
+__device__ __forceinline__ uint32_t logit_key(float lg, int id) {
+  uint32_t b = __float_as_uint(lg) >> 16;  // the logits hold bf16 values exactly
+  if (b == 0x8000u) b = 0u;                // -0 ties with +0
+  b = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  return (b << 16) | (0xffffu - (uint32_t)id);
+}
+__device__ __forceinline__ float key_logit(uint32_t key) {
+  uint32_t b = key >> 16;
+  b = (b & 0x8000u) ? (b & 0x7fffu) : (~b & 0xffffu);
+  return __uint_as_float(b << 16);
+}
+
+// softmax / top-k / renormalise (L/i8x_decode.py:98-117)
+__global__ __launch_bounds__(256) void route_topk_kernel(MoeDev d) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= d.M) return;
+  const int E = d.E, k = d.k, nm = E / 64;
+  const bool valid = d.pos == nullptr || d.pos[t] != 0;
+  if (!valid) {
+    if (lane < k) {
+      d.ids[t * k + lane] = -1;
+      d.wts[t * k + lane] = 0.f;
+    }
+    return;
+  }
+  float lg[16];
+  uint32_t key[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) lg[m] = d.logits[(size_t)t * E + lane + 64 * (m < nm ? m : nm - 1)];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) key[m] = m < nm ? logit_key(lg[m], lane + 64 * m) : 0u;
+  float mx = 0.f, vj[16];
+  int idj[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (j < k) {
+      uint32_t lb = 0u;
+#pragma unroll
+      for (int m = 0; m < 16; ++m) lb = max(lb, key[m]);
+      const uint32_t win = wave_max_u32(lb);
+      const int id = (int)(0xffffu - (win & 0xffffu));
+      const float v = key_logit(win);
+      if (j == 0) mx = v;
+      vj[j] = v;
+      idj[j] = id;
+#pragma unroll
+      for (int m = 0; m < 16; ++m)
+        if (lane + 64 * m == id) key[m] = 0u;
+    }
+  }
+  float part = 0.f;
+#pragma unroll
+  for (int m = 0; m < 16; ++m)
+    if (m < nm) part = part + expf_q(lg[m] - mx);
+  const float sum = wave_sum_bfly(part);
+  float wsum = 0.f, my_p = 0.f;
+  int my_id = -1;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (j < k) {
+      const float p = expf_q(vj[j] - mx) / sum;
+      wsum = wsum + p;
+      if (lane == j) {
+        my_p = p;
+        my_id = idj[j];
+      }
+    }
+  }
+  const float div = wsum > 0.f ? wsum : 1.f;
+  if (lane < k) {
+    d.ids[t * k + lane] = my_id;
+    d.wts[t * k + lane] = my_p / div;
+    // the expert's slot list and the active-expert list, for the expert kernels (their order
+    // follows the atomics; every output element is computed from its own row, so the results do
+    // not depend on it)
+    const int pos = atomicAdd(&d.ecount[my_id], 1);
+    d.elist[(size_t)my_id * d.M + pos] = t * k + lane;
+    if (pos == 0) d.eact[atomicAdd(&d.ctl[2], 1)] = my_id;
+  }
+}
+
+// Expert lists in LDS, in canonical order (expert asc, token asc, j asc): counts, exclusive
+// offsets, the active experts, and perm (sorted position -> slot t*k + j).  Every workgroup of
+// the expert kernels builds them from ids in its prologue (a 256-thread pass over M*k ids), so
+// no workgroup waits on another; with `publish` the workgroup also writes them to the workspace.
+struct Lists {
+  int* cnt;      // [E]
+  int* off;      // [E+1]
+  int* active;   // [E]
+  uint32_t* mask;  // [E][mw]
+  int* perm;     // [M*k]
+  int* misc;     // [0] n_active, [1..4] wave count totals, [5..8] wave active totals
+};
+__host__ __device__ inline size_t lists_lds_bytes(int E, int M, int k) {
+  const int mw = (M + 31) / 32;
+  return sizeof(int) * ((size_t)E + (E + 1) + E + (size_t)E * mw + (size_t)M * k + 16);
+}
+__device__ __forceinline__ Lists lists_carve(char* base, int E, int M, int k) {
+  Lists L;
+  const int mw = (M + 31) / 32;
+  int* p = reinterpret_cast<int*>(base);
+  L.cnt = p;
+  p += E;
+  L.off = p;
+  p += E + 1;
+  L.active = p;
+  p += E;
+  L.mask = reinterpret_cast<uint32_t*>(p);
+  p += E * mw;
+  L.perm = p;
+  p += M * k;
+  L.misc = p;
+  return L;
+}
+__device__ void lists_build(const MoeDev& d, const Lists& L, bool publish) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int E = d.E, S = d.M * d.k, mw = (d.M + 31) / 32;
+  const int E = d.E, M = d.M, k = d.k, S = M * k, mw = (M + 31) / 32;
   for (int e = tid; e < E; e += 256) {
-    cnt[e] = 0;
-    for (int w = 0; w < mw; ++w) mask[e][w] = 0u;
+    L.cnt[e] = 0;
+    for (int w = 0; w < mw; ++w) L.mask[e * mw + w] = 0u;
   }
   __syncthreads();
   for (int s = tid; s < S; s += 256) {
-    const int e = __hip_atomic_load(d.ids + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int e = d.ids[s];
     if (e >= 0) {
-      const int t = s / d.k;
-      atomicAdd(&cnt[e], 1);
-      atomicOr(&mask[e][t >> 5], 1u << (t & 31));
+      const int t = s / k;
+      atomicAdd(&L.cnt[e], 1);
+      atomicOr(&L.mask[e * mw + (t >> 5)], 1u << (t & 31));
     }
   }
   __syncthreads();
-  // Exclusive scan of counts and of the active flags: thread tid owns experts 4 tid .. 4 tid + 3.
+  // exclusive scans of counts and active flags: thread tid owns experts 4 tid .. 4 tid + 3
   int c4[4], csum = 0, asum = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = 4 * tid + i;
-    c4[i] = e < E ? cnt[e] : 0;
+    c4[i] = e < E ? L.cnt[e] : 0;
     csum += c4[i];
     asum += c4[i] > 0;
   }
@@ -243,352 +384,352 @@ __device__ void build_lists(const MoeDev& d) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const int cn = __shfl_up(ci, o), an = __shfl_up(ai, o);
-    if (lane >= o) { ci += cn; ai += an; }
+    if (lane >= o) {
+      ci += cn;
+      ai += an;
+    }
   }
-  if (lane == 63) { wsum[wave] = ci; wact[wave] = ai; }
+  if (lane == 63) {
+    L.misc[1 + wave] = ci;
+    L.misc[5 + wave] = ai;
+  }
   __syncthreads();
-  int cbase = 0, abase = 0;
-  for (int w = 0; w < wave; ++w) { cbase += wsum[w]; abase += wact[w]; }
-  int ce = cbase + ci - csum, ae = abase + ai - asum;
+  int ce = ci - csum, ae = ai - asum;
+  for (int w = 0; w < wave; ++w) {
+    ce += L.misc[1 + w];
+    ae += L.misc[5 + w];
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = 4 * tid + i;
     if (e < E) {
-      off[e] = ce;
-      d.offsets[e] = ce;
-      d.counts[e] = c4[i];
-      if (c4[i] > 0) d.active[ae++] = e;
+      L.off[e] = ce;
+      if (c4[i] > 0) L.active[ae++] = e;
       ce += c4[i];
     }
   }
   if (tid == 255) {
-    off[E] = ce;
-    d.offsets[E] = ce;
-    d.ctl[1] = ae;
+    L.off[E] = ce;
+    L.misc[0] = ae;
   }
   __syncthreads();
   for (int s = tid; s < S; s += 256) {
-    const int e = __hip_atomic_load(d.ids + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (e < 0) {
-      d.inv_perm[s] = -1;
-      continue;
+    const int e = d.ids[s];
+    int p = -1;
+    if (e >= 0) {
+      const int t = s / k, tw = t >> 5;
+      int rank = __popc(L.mask[e * mw + tw] & ((1u << (t & 31)) - 1u));
+      for (int w = 0; w < tw; ++w) rank += __popc(L.mask[e * mw + w]);
+      p = L.off[e] + rank;
+      L.perm[p] = s;
     }
-    const int t = s / d.k, tw = t >> 5;
-    int rank = __popc(mask[e][tw] & ((1u << (t & 31)) - 1u));
-    for (int w = 0; w < tw; ++w) rank += __popc(mask[e][w]);
-    const int p = off[e] + rank;
-    d.perm[p] = s;
-    d.inv_perm[s] = p;
+    if (publish) {
+      d.inv_perm[s] = p;
+      if (p >= 0) d.perm[p] = s;
+    }
   }
-  for (int p = off[E] + tid; p < S; p += 256) d.perm[p] = -1;
-  if (tid == 0) d.ctl[0] = 0;  // reset the ticket for the next call
+  if (publish) {
+    for (int p = L.off[E] + tid; p < S; p += 256) d.perm[p] = -1;
+    for (int e = tid; e < E; e += 256) {
+      d.counts[e] = L.cnt[e];
+      d.offsets[e] = L.off[e];
+    }
+    const int na = L.misc[0];
+    for (int u = tid; u < na; u += 256) d.active[u] = L.active[u];
+    if (tid == 0) {
+      d.offsets[E] = L.off[E];
+      d.ctl[1] = na;
+    }
+  }
+  __syncthreads();
 }
 
-__global__ __launch_bounds__(256) void route_topk_kernel(MoeDev d) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + wave;
-  if (t < d.M) {
-    const bool valid = d.pos == nullptr || d.pos[t] != 0;
-    if (!valid) {
-      if (lane < d.k) {
-        d.ids[t * d.k + lane] = -1;
-        d.wts[t * d.k + lane] = 0.f;
-      }
+// Lists alone (q36_moe_route): one workgroup builds and publishes them.
+__global__ __launch_bounds__(256) void route_lists_kernel(MoeDev d) {
+  extern __shared__ __align__(16) char dyn_lds[];
+  const Lists L = lists_carve(dyn_lds, d.E, d.M, d.k);
+  lists_build(d, L, true);
+}
+
+// ------------------------------------------------------------------------------------------
+// Expert work: token lists, MFMA fragments
+// ------------------------------------------------------------------------------------------
+// The expert kernels find an expert's tokens from ids directly: thread t (< M) scans token t's k
+// ids, and a ballot compaction lists the matching slots s = t*k + j in token order (the shared
+// expert lists slot M*k + t of every non-padding token).  h and y are indexed by slot, so no
+// sorted-position lists sit on the forward path (q36_moe_route still publishes them).
+__device__ __forceinline__ int expert_slots(const MoeDev& d, int e_or_shared, int* slots, int* wtot) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int my = -1;
+  if (tid < d.M) {
+    if (e_or_shared < 0) {
+      if (d.pos == nullptr || d.pos[tid] != 0) my = d.M * d.k + tid;
     } else {
-      const int nm = d.E / 64;
-      float lg[16];
-      float mx = -__builtin_inff();
-#pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        lg[m] = m < nm ? d.logits[(size_t)t * d.E + lane + 64 * m] : -__builtin_inff();
-        mx = fmaxf(mx, lg[m]);
-      }
-      mx = wave_max(mx);
-      float part = 0.f;
-#pragma unroll
-      for (int m = 0; m < 16; ++m)
-        if (m < nm) part = part + expf_q(lg[m] - mx);
-      const float sum = wave_sum_bfly(part);
-      uint32_t taken = 0u;
-      float wsum = 0.f, my_p = 0.f;
-      int my_id = -1;
-      for (int j = 0; j < d.k; ++j) {
-        float bv = -__builtin_inff();
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-          const int id = lane + 64 * m;
-          if (m < nm && !((taken >> m) & 1u) && (lg[m] > bv || (lg[m] == bv && id < bi))) {
-            bv = lg[m];
-            bi = id;
-          }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-          const float ov = __shfl_xor(bv, o);
-          const int oi = __shfl_xor(bi, o);
-          if (ov > bv || (ov == bv && oi < bi)) {
-            bv = ov;
-            bi = oi;
-          }
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        const float p = expf_q(bv - mx) / sum;
-        wsum = wsum + p;
-        if (lane == j) {
-          my_p = p;
-          my_id = bi;
-        }
-      }
-      const float div = wsum > 0.f ? wsum : 1.f;
-      if (lane < d.k) {
-        d.ids[t * d.k + lane] = my_id;
-        d.wts[t * d.k + lane] = my_p / div;
-      }
+      for (int j = 0; j < d.k; ++j)
+        if (d.ids[tid * d.k + j] == e_or_shared) my = tid * d.k + j;
     }
   }
-  __shared__ int last;
+  const unsigned long long b = __ballot(my >= 0);
+  const int below = __popcll(b & ((1ull << lane) - 1ull));
+  if (lane == 0) wtot[wave] = __popcll(b);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    const int old = atomicAdd(d.ctl, 1);
-    last = old == (int)gridDim.x - 1;
+  int base = 0, tot = 0;
+  for (int w = 0; w < 4; ++w) {
+    base += w < wave ? wtot[w] : 0;
+    tot += wtot[w];
   }
+  if (my >= 0) slots[base + below] = my;
   __syncthreads();
-  if (!last) return;
-  __threadfence();
-  build_lists(d);
+  return tot;
 }
+// Unit u of an expert kernel: 0 is the shared expert (slots M*k + t of the non-padding tokens),
+// u >= 1 the (u-1)-th entry of the active list.  Fills slots[] in LDS and returns the count
+// (0: nothing to do).  *e_out is the expert (-1 for shared).
+__device__ __forceinline__ int unit_slots(const MoeDev& d, int unit, int* slots, int* wtot, int* e_out) {
+  if (unit == 0) {
+    *e_out = -1;
+    return expert_slots(d, -1, slots, wtot);
+  }
+  if (unit - 1 >= d.ctl[2]) {
+    *e_out = -1;
+    return 0;
+  }
+  const int e = d.eact[unit - 1];
+  const int cnt = d.ecount[e];
+  for (int i = threadIdx.x; i < cnt; i += blockDim.x) slots[i] = d.elist[(size_t)e * d.M + i];
+  __syncthreads();
+  *e_out = e;
+  return cnt;
+}
+__device__ __forceinline__ int slot_token(const MoeDev& d, int s) {
+  const int S = d.M * d.k;
+  return s >= S ? s - S : s / d.k;
+}
+
+constexpr int kMoeH = 2048, kMoeI = 512;
 
 // ------------------------------------------------------------------------------------------
 // 3. up GEMM + SwiGLU
 // ------------------------------------------------------------------------------------------
-// Workgroup = (unit, chunk of 16 gate rows + the matching 16 up rows); unit 0 is the shared
-// expert over all M tokens, unit u >= 1 the (u-1)-th active expert.  Wave w owns K range
-// [w H/4, (w+1) H/4); its weight fragments are loaded once and reused for every 16-token tile.
-// MFMA operands: src0 = activation tile (lane -> token row l%16), src1 = weight rows (lane ->
-// row l%16); lane group l/16 carries the same K bytes of both, so the products pair up; the
-// 16x16 result gives lane l column l%16 (weight row) and rows 4(l/16)+r (tokens).
+// Workgroup = (unit, group of 4 chunks); unit 0 is the shared expert, unit 1 + e expert e (the
+// workgroup returns at once when e has no tokens).  Each wave owns one chunk: 16 gate rows and
+// the matching 16 up rows over the whole K = H, streamed from HBM in 16 stages of 128 bytes per
+// row with kUpD stages in flight; no reduction across waves.  The activation rows of up to 64
+// tokens (4 tiles of 16) are shared by the four waves through LDS, one K half at a time.
+// Per stage a lane holds 32 contiguous bytes of its row (row = lane % 16, bytes 32 (lane / 16))
+// of both operands -- one e4m3 16x16x128 MFMA, or two int8 16x16x64 MFMAs on the two 16-byte
+// halves (their K pairing is the same for src0 and src1, so the int32 sums are exact).  The
+// 16x16 result gives lane l weight row l%16 and token rows 4(l/16)+r; SwiGLU happens in the
+// lane.  For e4m3 the block terms (block sum * xs * ws) are added in increasing block order from
+// zero, the order of the block dequant sum.
+constexpr int kUpD = 4;                    // weight stages in flight per wave
+constexpr int kUpKH = kMoeH / 2;           // K bytes per LDS activation half
+constexpr int kUpRow = kUpKH + 16;         // padded LDS row (spreads the 16 rows over the banks)
+constexpr int kUpGroups = kMoeI / 16 / 4;  // workgroups per unit (4 chunks each)
 template <int DT>
 __global__ __launch_bounds__(256) void moe_up_kernel(MoeDev d) {
-  constexpr int H = 2048;
-  constexpr int KW = H / 4;                        // K per wave
-  constexpr int NS = DT == Q36_MOE_FP8 ? KW / 128 : KW / 64;  // MFMA K steps per wave
-  const int I = d.I;
-  const int nch = I / 16;
-  const int ug = blockIdx.x / nch, ch = blockIdx.x % nch;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int lr = lane & 15, lgp = lane >> 4;
-  const bool shared = ug == 0;
-  const uint8_t* W;
-  const float* S;
-  int p0, cnt;
-  if (shared) {
-    W = d.sw13;
-    S = d.ss13;
-    p0 = d.M * d.k;
-    cnt = d.M;
-  } else {
-    const int u = ug - 1;
-    if (u >= d.ctl[1]) return;
-    const int e = d.active[u];
-    W = d.w13 + (size_t)e * 2 * I * H;
-    S = d.s13 + (DT == Q36_MOE_FP8 ? (size_t)e * (2 * I / 128) * (H / 128) : (size_t)e * 2 * I);
-    p0 = d.offsets[e];
-    cnt = d.counts[e];
-  }
-  const int ng = ch * 16 + lr;  // this lane's gate row (its up row is I + ng)
-  const int kw0 = wave * KW;
-  constexpr int FB = DT == Q36_MOE_FP8 ? 32 : 16;  // fragment bytes per lane per step
-  constexpr int KS = DT == Q36_MOE_FP8 ? 128 : 64;
-  const uint8_t* bg = W + (size_t)ng * H + kw0 + lgp * FB;
-  const uint8_t* bu = W + (size_t)(I + ng) * H + kw0 + lgp * FB;
-  v4i Bg[NS][FB / 16], Bu[NS][FB / 16];
+  constexpr int H = kMoeH, I = kMoeI, NSTG = H / 128, NT = 4;
+  extern __shared__ __align__(16) char up_lds[];
+  uint8_t* a_l = reinterpret_cast<uint8_t*>(up_lds);                     // [64][kUpRow]
+  float* xs_l = reinterpret_cast<float*>(up_lds + 64 * kUpRow);           // [64][NSTG]
+  float* ws_l = xs_l + 64 * NSTG;                                         // [2I/128][NSTG]
+  int* slots = reinterpret_cast<int*>(ws_l + (2 * I / 128) * NSTG);       // [kMaxM]
+  int* wtot = slots + kMaxM;                                              // [4]
+  const int unit = blockIdx.x / kUpGroups, grp = blockIdx.x % kUpGroups;
+  const bool shared = unit == 0;
+  if (!shared && unit - 1 >= d.ctl[2]) return;
+  const int e = shared ? -1 : d.eact[unit - 1];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
+  const uint8_t* W = shared ? d.sw13 : d.w13 + (size_t)e * 2 * I * H;
+  const float* S = shared ? d.ss13
+                          : d.s13 + (DT == Q36_MOE_FP8 ? (size_t)e * (2 * I / 128) * NSTG : (size_t)e * 2 * I);
+  const int ch = grp * 4 + wave;
+  const int ng = ch * 16 + lr;
+  const uint8_t* bg = W + (size_t)ng * H + lgp * 32;
+  const uint8_t* bu = W + (size_t)(I + ng) * H + lgp * 32;
+  v4i Bq[kUpD][4];
+  auto issue = [&](int s, int q) {
+    Bq[q][0] = ldg16_nt(bg + s * 128);
+    Bq[q][1] = ldg16_nt(bg + s * 128 + 16);
+    Bq[q][2] = ldg16_nt(bu + s * 128);
+    Bq[q][3] = ldg16_nt(bu + s * 128 + 16);
+  };
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
+  for (int s = 0; s < kUpD; ++s) issue(s, s);  // the first weight stages, before the token list
+  int e_chk;
+  const int cnt = unit_slots(d, unit, slots, wtot, &e_chk);
+  if (cnt == 0) return;
+  if constexpr (DT == Q36_MOE_FP8)
+    for (int i = tid; i < (2 * I / 128) * NSTG; i += 256) ws_l[i] = S[i];
+  using Acc = typename std::conditional<DT == Q36_MOE_FP8, v4f, v4i>::type;
+  for (int g0 = 0; g0 < cnt; g0 += 64) {
+    const int nt = min(NT, (cnt - g0 + 15) / 16);
+    if (g0 > 0) {
 #pragma unroll
-    for (int h2 = 0; h2 < FB / 16; ++h2) {
-      Bg[s][h2] = ldg16_nt(bg + s * KS + 16 * h2);
-      Bu[s][h2] = ldg16_nt(bu + s * KS + 16 * h2);
+      for (int s = 0; s < kUpD; ++s) issue(s, s);
     }
-  // Per-lane weight scales.
-  float wsg[NS], wsu[NS];
-  if constexpr (DT == Q36_MOE_FP8) {
-    const int nkb = H / 128;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      wsg[s] = S[(size_t)(ng / 128) * nkb + kw0 / 128 + s];
-      wsu[s] = S[(size_t)((I + ng) / 128) * nkb + kw0 / 128 + s];
+    for (int i = tid; i < 64 * NSTG; i += 256) {
+      const int ti = g0 + i / NSTG;
+      if constexpr (DT == Q36_MOE_FP8)
+        xs_l[i] = ti < cnt ? d.xs[(size_t)slot_token(d, slots[ti]) * NSTG + i % NSTG] : 0.f;
+      else
+        xs_l[i] = (ti < cnt && i % NSTG == 0) ? d.xs[slot_token(d, slots[ti])] : 0.f;
     }
-  }
-  __shared__ int red[4][2][64][4];                          // INT8: per-wave int32 partials
-  __shared__ float redf[4][DT == Q36_MOE_FP8 ? NS : 1][2][64][4];  // FP8: one term per 128-block
-  for (int t0 = 0; t0 < cnt; t0 += 16) {
-    // activation rows of this tile
-    const int ti = t0 + lr;
-    int tok = -1;
-    if (ti < cnt) tok = shared ? ti : d.perm[p0 + ti] / d.k;
-    v4i A[NS][FB / 16];
+    Acc ag[NT], au[NT];
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int h2 = 0; h2 < FB / 16; ++h2) {
-        if (tok >= 0) A[s][h2] = ldg16(d.xq + (size_t)tok * H + kw0 + s * KS + lgp * FB + 16 * h2);
-        else A[s][h2] = v4i{0, 0, 0, 0};
-      }
-    if constexpr (DT == Q36_MOE_FP8) {
-      // tokens of this lane's 4 output rows
-      float xsv[4][NS];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tr = t0 + 4 * lgp + r;
-        int tk = -1;
-        if (tr < cnt) tk = shared ? tr : d.perm[p0 + tr] / d.k;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) xsv[r][s] = tk >= 0 ? d.xs[(size_t)tk * (H / 128) + kw0 / 128 + s] : 0.f;
-      }
-      // Each 128-block term (block sum * xs * ws) goes to LDS; the epilogue adds the H/128 terms
-      // in increasing block order from zero, the order of the block dequant sum.
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const v8i a8 = cat8(A[s][0], A[s][1]);
-        const v4f rg = mfma_fp8(a8, cat8(Bg[s][0], Bg[s][1]));
-        const v4f ru = mfma_fp8(a8, cat8(Bu[s][0], Bu[s][1]));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          redf[wave][s][0][lane][r] = (rg[r] * xsv[r][s]) * wsg[s];
-          redf[wave][s][1][lane][r] = (ru[r] * xsv[r][s]) * wsu[s];
-        }
-      }
-    } else {
-      v4i ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        ag = mfma_i8(A[s][0], Bg[s][0], ag);
-        au = mfma_i8(A[s][0], Bu[s][0], au);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        red[wave][0][lane][r] = ag[r];
-        red[wave][1][lane][r] = au[r];
-      }
+    for (int tt = 0; tt < NT; ++tt) {
+      ag[tt] = Acc{0, 0, 0, 0};
+      au[tt] = Acc{0, 0, 0, 0};
     }
-    __syncthreads();
-    {
-      // epilogue: thread -> (lane' = tid % 64, r = tid / 64): token row 4 (lane'/16) + r, column lane' % 16
-      const int l2 = threadIdx.x & 63, r = threadIdx.x >> 6;
-      const int row = 4 * (l2 >> 4) + r, col = l2 & 15;
-      const int ti2 = t0 + row;
-      if (ti2 < cnt) {
-        const int p = p0 + ti2;
-        const int n = ch * 16 + col;
-        float g, u;
-        if constexpr (DT == Q36_MOE_FP8) {
-          g = 0.f;
-          u = 0.f;
 #pragma unroll
-          for (int w = 0; w < 4; ++w)
+    for (int half = 0; half < 2; ++half) {
+      // this half's activation rows into LDS: thread -> (row tid/4, 256 bytes at 256 (tid%4))
+      __syncthreads();
+      {
+        const int rr = tid >> 2, seg = tid & 3;
+        const int ti = g0 + rr;
+        const bool ok = ti < cnt && rr < 16 * nt;
+        const uint8_t* src = d.xq + (size_t)slot_token(d, slots[ok ? ti : 0]) * H + half * kUpKH + seg * 256;
+        v4i v[16];
 #pragma unroll
-            for (int s = 0; s < NS; ++s) {
-              g = g + redf[w][s][0][l2][r];
-              u = u + redf[w][s][1][l2][r];
+        for (int c = 0; c < 16; ++c) v[c] = ok ? ldg16(src + 16 * c) : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 16; ++c) *reinterpret_cast<v4i*>(a_l + rr * kUpRow + seg * 256 + 16 * c) = v[c];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int sh = 0; sh < NSTG / 2; ++sh) {
+        const int s = half * (NSTG / 2) + sh;
+        const int q = s % kUpD;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+          if (tt < nt) {
+            const uint8_t* ap = a_l + (tt * 16 + lr) * kUpRow + sh * 128 + lgp * 32;
+            const v4i a0 = *reinterpret_cast<const v4i*>(ap);
+            const v4i a1 = *reinterpret_cast<const v4i*>(ap + 16);
+            if constexpr (DT == Q36_MOE_FP8) {
+              const v8i a8 = cat8(a0, a1);
+              const v4f rg = mfma_fp8(a8, cat8(Bq[q][0], Bq[q][1]));
+              const v4f ru = mfma_fp8(a8, cat8(Bq[q][2], Bq[q][3]));
+              const float wg = ws_l[(ng / 128) * NSTG + s], wu = ws_l[((I + ng) / 128) * NSTG + s];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float xsr = xs_l[(tt * 16 + 4 * lgp + r) * NSTG + s];
+                float g = ag[tt][r] + (rg[r] * xsr) * wg;
+                float u = au[tt][r] + (ru[r] * xsr) * wu;
+                // pin the running sums here: left alone, the compiler sinks the whole chain below
+                // the loop and keeps every stage's MFMA result live
+                asm volatile("" : "+v"(g), "+v"(u));
+                ag[tt][r] = g;
+                au[tt][r] = u;
+              }
+            } else {
+              ag[tt] = mfma_i8(a0, Bq[q][0], ag[tt]);
+              ag[tt] = mfma_i8(a1, Bq[q][1], ag[tt]);
+              au[tt] = mfma_i8(a0, Bq[q][2], au[tt]);
+              au[tt] = mfma_i8(a1, Bq[q][3], au[tt]);
             }
-        } else {
-          const int ai = red[0][0][l2][r] + red[1][0][l2][r] + red[2][0][l2][r] + red[3][0][l2][r];
-          const int au = red[0][1][l2][r] + red[1][1][l2][r] + red[2][1][l2][r] + red[3][1][l2][r];
-          if (d.dbg_acc13) {
-            d.dbg_acc13[(size_t)p * 2 * I + n] = ai;
-            d.dbg_acc13[(size_t)p * 2 * I + I + n] = au;
           }
-          const int tk = shared ? ti2 : d.perm[p] / d.k;
-          const float xsc = d.xs[tk];
-          g = ((float)ai * xsc) * S[n];
-          u = ((float)au * xsc) * S[I + n];
         }
-        g = rbf(g);
-        u = rbf(u);
-        const uint32_t hb = f2bf((g / (1.f + expf_q(-g))) * u);
-        d.h[(size_t)p * I + n] = (uint16_t)hb;
-        if (d.dbg_h) d.dbg_h[(size_t)p * I + n] = (uint16_t)hb;
+        if (s + kUpD < NSTG) issue(s + kUpD, q);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __syncthreads();
+    const int n = ch * 16 + lr;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ti = g0 + tt * 16 + 4 * lgp + r;
+        if (tt < nt && ti < cnt) {
+          const int s = slots[ti];
+          float g, u;
+          if constexpr (DT == Q36_MOE_FP8) {
+            g = ag[tt][r];
+            u = au[tt][r];
+          } else {
+            if (d.dbg_acc13) {
+              d.dbg_acc13[(size_t)s * 2 * I + n] = ag[tt][r];
+              d.dbg_acc13[(size_t)s * 2 * I + I + n] = au[tt][r];
+            }
+            const float xsc = xs_l[(tt * 16 + 4 * lgp + r) * NSTG];
+            g = ((float)ag[tt][r] * xsc) * S[n];
+            u = ((float)au[tt][r] * xsc) * S[I + n];
+          }
+          g = rbf(g);
+          u = rbf(u);
+          const uint32_t hb = f2bf((g / (1.f + expf_q(-g))) * u);
+          d.h[(size_t)s * I + n] = (uint16_t)hb;
+          if (d.dbg_h) d.dbg_h[(size_t)s * I + n] = (uint16_t)hb;
+        }
+      }
   }
 }
+constexpr size_t kUpLds = 64 * kUpRow + sizeof(float) * (64 * (kMoeH / 128) + (2 * kMoeI / 128) * (kMoeH / 128)) +
+                          sizeof(int) * (kMaxM + 4);
 
 // ------------------------------------------------------------------------------------------
 // 4. down GEMM x routing weight
 // ------------------------------------------------------------------------------------------
-// Workgroup = (unit, chunk of 64 output rows).  Per 16-token tile the tile's h rows are loaded
-// and quantized into LDS (int8 per row over I, e4m3 per 128-group); wave w owns K block
-// [w I/4, (w+1) I/4) = one 128-group, four 16-row MFMA column tiles.
+// Workgroup = (unit, group of 4 x 32 output rows); each wave owns 32 rows (two 16-row MFMA
+// column tiles) over the whole K = I (4 stages of 128 bytes), loaded before the token scan.  Per
+// 16-token tile the workgroup quantizes the tile's h rows once into LDS (e4m3 per 128-group,
+// int8 per row) and every wave reads its MFMA operand from there.
+constexpr int kDnRows = 32;
+constexpr int kDnGroups = kMoeH / (4 * kDnRows);
 template <int DT>
 __global__ __launch_bounds__(256) void moe_down_kernel(MoeDev d) {
-  constexpr int H = 2048, I = 512;
-  constexpr int KW = I / 4;                                   // 128
-  constexpr int NS = DT == Q36_MOE_FP8 ? KW / 128 : KW / 64;  // 1 or 2
-  constexpr int FB = DT == Q36_MOE_FP8 ? 32 : 16;
-  constexpr int KS = DT == Q36_MOE_FP8 ? 128 : 64;
-  constexpr int nch = H / 64;
-  const int ug = blockIdx.x / nch, ch = blockIdx.x % nch;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int lr = lane & 15, lgp = lane >> 4;
-  const bool shared = ug == 0;
-  const uint8_t* W;
-  const float* S;
-  int p0, cnt;
-  if (shared) {
-    W = d.sw2;
-    S = d.ss2;
-    p0 = d.M * d.k;
-    cnt = d.M;
-  } else {
-    const int u = ug - 1;
-    if (u >= d.ctl[1]) return;
-    const int e = d.active[u];
-    W = d.w2 + (size_t)e * H * I;
-    S = d.s2 + (DT == Q36_MOE_FP8 ? (size_t)e * (H / 128) * (I / 128) : (size_t)e * H);
-    p0 = d.offsets[e];
-    cnt = d.counts[e];
-  }
-  const int kw0 = wave * KW;
-  v4i B[4][NS][FB / 16];
+  constexpr int H = kMoeH, I = kMoeI, NSTG = I / 128;
+  __shared__ int slots[kMaxM];
+  __shared__ int wtot[4];
+  __shared__ __align__(16) uint8_t hq[16][I];
+  __shared__ float hs[16][NSTG];
+  const int unit = blockIdx.x / kDnGroups, grp = blockIdx.x % kDnGroups;
+  const bool shared = unit == 0;
+  if (!shared && unit - 1 >= d.ctl[2]) return;
+  const int e = shared ? -1 : d.eact[unit - 1];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
+  const uint8_t* W = shared ? d.sw2 : d.w2 + (size_t)e * H * I;
+  const float* S =
+      shared ? d.ss2 : d.s2 + (DT == Q36_MOE_FP8 ? (size_t)e * (H / 128) * NSTG : (size_t)e * H);
+  const int n0 = (grp * 4 + wave) * kDnRows;
+  v4i B[2][NSTG][2];
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const uint8_t* b = W + (size_t)(ch * 64 + nt * 16 + lr) * I + kw0 + lgp * FB;
+  for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int h2 = 0; h2 < FB / 16; ++h2) B[nt][s][h2] = ldg16_nt(b + s * KS + 16 * h2);
-  }
-  float wsc[4];
+    for (int s = 0; s < NSTG; ++s) {
+      const uint8_t* src = W + (size_t)(n0 + ct * 16 + lr) * I + s * 128 + lgp * 32;
+      B[ct][s][0] = ldg16_nt(src);
+      B[ct][s][1] = ldg16_nt(src + 16);
+    }
+  int e_chk;
+  const int cnt = unit_slots(d, unit, slots, wtot, &e_chk);
+  if (cnt == 0) return;
+  float wsc[2][NSTG];
   if constexpr (DT == Q36_MOE_FP8) {
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) wsc[nt] = S[(size_t)((ch * 64 + nt * 16) / 128) * (I / 128) + wave];
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int s = 0; s < NSTG; ++s) wsc[ct][s] = S[(size_t)((n0 + ct * 16) / 128) * NSTG + s];
   }
-  __shared__ __align__(16) uint8_t hq[16][I];
-  __shared__ float hs[16][4];
-  __shared__ float red[4][4][64][4];
   for (int t0 = 0; t0 < cnt; t0 += 16) {
     {
-      // quantize the tile's h rows: thread -> (row tid/16, 32 elements at 32 (tid%16))
+      // quantize the tile: thread -> (row tid/16, values 32 (tid%16) .. +31); a 128-group is
+      // four neighbouring threads, a row sixteen
       const int tr = tid >> 4, q16 = tid & 15;
+      const bool ok = t0 + tr < cnt;
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(d.h + (size_t)slots[ok ? t0 + tr : 0] * I) + q16 * 64;
+      v4i raw[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) raw[v] = ldg16(src + 16 * v);
       float hv[32];
-      if (t0 + tr < cnt) {
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(d.h + (size_t)(p0 + t0 + tr) * I + q16 * 32);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const v4i raw = ldg16(src + 16 * v);
+      for (int v = 0; v < 4; ++v)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            hv[8 * v + 2 * q] = bf_lo((uint32_t)raw[q]);
-            hv[8 * v + 2 * q + 1] = bf_hi((uint32_t)raw[q]);
-          }
+        for (int q = 0; q < 4; ++q) {
+          hv[8 * v + 2 * q] = ok ? bf_lo((uint32_t)raw[v][q]) : 0.f;
+          hv[8 * v + 2 * q + 1] = ok ? bf_hi((uint32_t)raw[v][q]) : 0.f;
         }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 32; ++v) hv[v] = 0.f;
-      }
       float m = 0.f;
 #pragma unroll
       for (int v = 0; v < 32; ++v) m = fmaxf(m, fabsf(hv[v]));
@@ -596,73 +737,70 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeDev d) {
       if constexpr (DT == Q36_MOE_FP8) {
         m = fmaxf(m, __shfl_xor(m, 1));
         m = fmaxf(m, __shfl_xor(m, 2));
-        const float s = m / 448.f, inv = m > 0.f ? 448.f / m : 0.f;
+        const float inv = m > 0.f ? 448.f / m : 0.f;
 #pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          wd[v] = 0u;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) wd[v] |= f2e4m3(hv[4 * v + q] * inv) << (8 * q);
-        }
-        if ((q16 & 3) == 0) hs[tr][q16 >> 2] = s;
+        for (int v = 0; v < 8; ++v)
+          wd[v] = f2e4m3x2_hw(hv[4 * v] * inv, hv[4 * v + 1] * inv) |
+                  (f2e4m3x2_hw(hv[4 * v + 2] * inv, hv[4 * v + 3] * inv) << 16);
+        if ((q16 & 3) == 0) hs[tr][q16 >> 2] = m / 448.f;
       } else {
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-        const float s = m / 127.f, safe = m > 0.f ? s : 1.f;
+        const float sc = m / 127.f, safe = m > 0.f ? sc : 1.f;
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
           wd[v] = 0u;
 #pragma unroll
           for (int q = 0; q < 4; ++q) wd[v] |= ((uint32_t)round_i8(hv[4 * v + q] / safe) & 0xffu) << (8 * q);
         }
-        if (q16 == 0) hs[tr][0] = s;
+        if (q16 == 0) hs[tr][0] = sc;
       }
       uint4* dst = reinterpret_cast<uint4*>(&hq[tr][q16 * 32]);
       dst[0] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
       dst[1] = make_uint4(wd[4], wd[5], wd[6], wd[7]);
     }
     __syncthreads();
-    v4i A[NS][FB / 16];
+    v4i A[NSTG][2];
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
+    for (int s = 0; s < NSTG; ++s) {
+      A[s][0] = *reinterpret_cast<const v4i*>(&hq[lr][s * 128 + lgp * 32]);
+      A[s][1] = *reinterpret_cast<const v4i*>(&hq[lr][s * 128 + lgp * 32 + 16]);
+    }
 #pragma unroll
-      for (int h2 = 0; h2 < FB / 16; ++h2)
-        A[s][h2] = *reinterpret_cast<const v4i*>(&hq[lr][kw0 + s * KS + lgp * FB + 16 * h2]);
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
+    for (int ct = 0; ct < 2; ++ct) {
+      const int n = n0 + ct * 16 + lr;
+      float yv[4];
       if constexpr (DT == Q36_MOE_FP8) {
-        const v4f rr = mfma_fp8(cat8(A[0][0], A[0][1]), cat8(B[nt][0][0], B[nt][0][1]));
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave][nt][lane][r] = (rr[r] * hs[4 * lgp + r][wave]) * wsc[nt];
+        for (int s = 0; s < NSTG; ++s) {
+          const v4f rr = mfma_fp8(cat8(A[s][0], A[s][1]), cat8(B[ct][s][0], B[ct][s][1]));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = acc[r] + (rr[r] * hs[4 * lgp + r][s]) * wsc[ct][s];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yv[r] = acc[r];
       } else {
         v4i acc = {0, 0, 0, 0};
 #pragma unroll
-        for (int s = 0; s < NS; ++s) acc = mfma_i8(A[s][0], B[nt][s][0], acc);
+        for (int s = 0; s < NSTG; ++s) {
+          acc = mfma_i8(A[s][0], B[ct][s][0], acc);
+          acc = mfma_i8(A[s][1], B[ct][s][1], acc);
+        }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave][nt][lane][r] = __int_as_float(acc[r]);
+        for (int r = 0; r < 4; ++r) {
+          const int ti2 = t0 + 4 * lgp + r;
+          if (ti2 < cnt && d.dbg_acc2) d.dbg_acc2[(size_t)slots[ti2] * H + n] = acc[r];
+          yv[r] = ((float)acc[r] * hs[4 * lgp + r][0]) * S[n];
+        }
       }
-    }
-    __syncthreads();
-    {
-      const int nt = tid >> 6, l2 = tid & 63;
-      const int n = ch * 64 + nt * 16 + (l2 & 15);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 4 * (l2 >> 4) + r;
-        const int ti2 = t0 + row;
+        const int ti2 = t0 + 4 * lgp + r;
         if (ti2 < cnt) {
-          const int p = p0 + ti2;
-          const float wt = shared ? 1.f : d.wts[d.perm[p]];
-          float yv;
-          if constexpr (DT == Q36_MOE_FP8) {
-            const float acc = (((0.f + red[0][nt][l2][r]) + red[1][nt][l2][r]) + red[2][nt][l2][r]) + red[3][nt][l2][r];
-            yv = acc * wt;
-          } else {
-            const int ai = __float_as_int(red[0][nt][l2][r]) + __float_as_int(red[1][nt][l2][r]) +
-                           __float_as_int(red[2][nt][l2][r]) + __float_as_int(red[3][nt][l2][r]);
-            if (d.dbg_acc2) d.dbg_acc2[(size_t)p * H + n] = ai;
-            yv = (((float)ai * hs[row][0]) * S[n]) * wt;
-          }
-          d.y[(size_t)p * H + n] = (uint16_t)f2bf(yv);
+          const int s = slots[ti2];
+          const float wt = shared ? 1.f : d.wts[s];
+          d.y[(size_t)s * H + n] = (uint16_t)f2bf(yv[r] * wt);
         }
       }
     }
@@ -673,11 +811,17 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeDev d) {
 // ------------------------------------------------------------------------------------------
 // 5. combine
 // ------------------------------------------------------------------------------------------
+// One workgroup per token; every y row of the token (its k routed slots t*k + j and the shared
+// slot M*k + t) is loaded before any is added, then
+// out = bf16(fma(gate, y_shared, ((0 + y_0) + y_1) ... + y_{k-1})).
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
   const int t = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool valid = d.pos == nullptr || d.pos[t] != 0;
+  const int S = d.M * d.k;
   __shared__ float gate_s;
+  __shared__ int prow[17];
+  if (tid <= d.k) prow[tid] = tid < d.k ? t * d.k + tid : S + t;
   if (valid && wave == 0) {
     float acc = 0.f;
     for (int j = 0; j < d.H / 512; ++j) {
@@ -694,23 +838,30 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
     if (lane == 0) gate_s = sigmoid_q(acc);
   }
   __syncthreads();
-  const int S = d.M * d.k;
   for (int c = tid; 8 * c < d.H; c += 256) {
     uint4 o = make_uint4(0u, 0u, 0u, 0u);
     if (valid) {
+      v4i yv[17];
+#pragma unroll
+      for (int j = 0; j < 17; ++j)
+        yv[j] = ldg16(reinterpret_cast<const uint8_t*>(d.y + (size_t)prow[j <= d.k ? j : d.k] * d.H + 8 * c));
       float acc[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc[q] = 0.f;
-      for (int j = 0; j < d.k; ++j) {
-        const int p = d.inv_perm[t * d.k + j];
-        const v4i yv = ldg16(reinterpret_cast<const uint8_t*>(d.y + (size_t)p * d.H + 8 * c));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          acc[2 * q] = acc[2 * q] + bf_lo((uint32_t)yv[q]);
-          acc[2 * q + 1] = acc[2 * q + 1] + bf_hi((uint32_t)yv[q]);
+      for (int j = 0; j < 16; ++j) {
+        if (j < d.k) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[2 * q] = acc[2 * q] + bf_lo((uint32_t)yv[j][q]);
+            acc[2 * q + 1] = acc[2 * q + 1] + bf_hi((uint32_t)yv[j][q]);
+          }
         }
       }
-      const v4i sv = ldg16(reinterpret_cast<const uint8_t*>(d.y + (size_t)(S + t) * d.H + 8 * c));
+      v4i sv = yv[0];
+#pragma unroll
+      for (int j = 1; j < 17; ++j)
+        if (j == d.k) sv = yv[j];
       const float g = gate_s;
       uint32_t w[4];
 #pragma unroll
@@ -790,7 +941,7 @@ __global__ __launch_bounds__(256) void quant_blocks_e4m3_kernel(const uint16_t* 
     for (int i = 0; i < 4; ++i) {
       wd[i] = 0u;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) wd[i] |= f2e4m3(v[16 * c + 4 * i + b] * inv) << (8 * b);
+      for (int b = 0; b < 4; b += 2) wd[i] |= f2e4m3x2_hw(v[16 * c + 4 * i + b] * inv, v[16 * c + 4 * i + b + 1] * inv) << (8 * b);
     }
     *reinterpret_cast<uint4*>(dst + 16 * c) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
   }
@@ -808,7 +959,6 @@ int layout(int M, int E, int H, int I, int k, int dtype, q36_moe_ws_layout* L) {
     return r;
   };
   const size_t S = (size_t)M * k;
-  // ctl first: its offset must not depend on M, so the ticket stays zero across calls of any size
   L->ctl = take(sizeof(int32_t) * 64);
   L->logits = take(sizeof(float) * (size_t)M * E);
   L->ids = take(sizeof(int32_t) * S);
@@ -818,6 +968,9 @@ int layout(int M, int E, int H, int I, int k, int dtype, q36_moe_ws_layout* L) {
   L->perm = take(sizeof(int32_t) * S);
   L->inv_perm = take(sizeof(int32_t) * S);
   L->active = take(sizeof(int32_t) * E);
+  L->ecount = take(sizeof(int32_t) * E);
+  L->eact = take(sizeof(int32_t) * E);
+  L->elist = take(sizeof(int32_t) * (size_t)E * M);
   L->xq = take((size_t)M * H);
   L->xs = take(sizeof(float) * (size_t)M * (dtype == Q36_MOE_FP8 ? H / 128 : 1));
   L->h = take(sizeof(uint16_t) * (S + M) * I);
@@ -858,21 +1011,78 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
               reinterpret_cast<float*>(ws + L.wts), reinterpret_cast<int32_t*>(ws + L.counts),
               reinterpret_cast<int32_t*>(ws + L.offsets), reinterpret_cast<int32_t*>(ws + L.perm),
               reinterpret_cast<int32_t*>(ws + L.inv_perm), reinterpret_cast<int32_t*>(ws + L.active),
-              reinterpret_cast<int32_t*>(ws + L.ctl), reinterpret_cast<uint8_t*>(ws + L.xq),
+              reinterpret_cast<int32_t*>(ws + L.ctl), reinterpret_cast<int32_t*>(ws + L.ecount),
+              reinterpret_cast<int32_t*>(ws + L.eact), reinterpret_cast<int32_t*>(ws + L.elist),
+              reinterpret_cast<uint8_t*>(ws + L.xq),
               reinterpret_cast<float*>(ws + L.xs), reinterpret_cast<uint16_t*>(ws + L.h),
               reinterpret_cast<uint16_t*>(ws + L.y), a->dbg_acc13, a->dbg_acc2,
               static_cast<uint16_t*>(a->dbg_h)};
   return Q36_OK;
 }
 
+// Raise a kernel's dynamic-LDS limit (once per device and kernel) when a launch needs more than
+// the 64 KiB default; gfx950 has 160 KiB per CU.
+int ensure_lds(const void* fn, size_t bytes, const char* what) {
+  if (bytes <= 65536) return Q36_OK;
+  static const void* done[64][8] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  for (int i = 0; i < 8; ++i)
+    if (done[dev][i] == fn) return Q36_OK;
+  if (bytes > 160 * 1024) {
+    set_error("%s: %zu bytes of LDS exceed the 160 KiB of a CU", what, bytes);
+    return Q36_EINVAL;
+  }
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+    set_error("%s: hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed", what);
+    return Q36_ELAUNCH;
+  }
+  for (int i = 0; i < 8; ++i)
+    if (done[dev][i] == nullptr) {
+      done[dev][i] = fn;
+      break;
+    }
+  return Q36_OK;
+}
+
 int launch_route(const MoeDev& d, int dtype, hipStream_t st) {
-  const int n_router = (d.E / 16) * ((d.M + 15) / 16);
+  const int n_router = (d.E / 16) * ((d.M + kRouteTT - 1) / kRouteTT);
   if (dtype == Q36_MOE_FP8)
     route_logits_kernel<Q36_MOE_FP8><<<n_router + d.M, 256, 0, st>>>(d, n_router);
   else
     route_logits_kernel<Q36_MOE_INT8><<<n_router + d.M, 256, 0, st>>>(d, n_router);
   route_topk_kernel<<<(d.M + 3) / 4, 256, 0, st>>>(d);
   return check_launch("q36_moe_route");
+}
+int launch_lists(const MoeDev& d, hipStream_t st) {
+  const size_t lds = lists_lds_bytes(d.E, d.M, d.k);
+  int rc = ensure_lds(reinterpret_cast<const void*>(&route_lists_kernel), lds, "q36_moe_route");
+  if (rc) return rc;
+  route_lists_kernel<<<1, 256, lds, st>>>(d);
+  return check_launch("q36_moe_route");
+}
+
+template <int DT>
+int launch_up_t(const MoeDev& d, hipStream_t st) {
+  int rc = ensure_lds(reinterpret_cast<const void*>(&moe_up_kernel<DT>), kUpLds, "q36_moe_up");
+  if (rc) return rc;
+  moe_up_kernel<DT><<<(d.E + 1) * kUpGroups, 256, kUpLds, st>>>(d);
+  return check_launch("q36_moe_up");
+}
+template <int DT>
+int launch_down_t(const MoeDev& d, hipStream_t st) {
+  moe_down_kernel<DT><<<(d.E + 1) * kDnGroups, 256, 0, st>>>(d);
+  return check_launch("q36_moe_down");
+}
+int launch_up(const MoeDev& d, int dtype, hipStream_t st) {
+  return dtype == Q36_MOE_FP8 ? launch_up_t<Q36_MOE_FP8>(d, st) : launch_up_t<Q36_MOE_INT8>(d, st);
+}
+int launch_down(const MoeDev& d, int dtype, hipStream_t st) {
+  return dtype == Q36_MOE_FP8 ? launch_down_t<Q36_MOE_FP8>(d, st) : launch_down_t<Q36_MOE_INT8>(d, st);
+}
+int launch_combine(const MoeDev& d, hipStream_t st) {
+  moe_combine_kernel<<<d.M, 256, 0, st>>>(d);
+  return check_launch("q36_moe_combine");
 }
 
 }  // namespace
@@ -896,33 +1106,10 @@ extern "C" int q36_moe_route(const q36_moe_args* a, q36_stream_t stream) {
   MoeDev d;
   int rc = validate(a, &d, false);
   if (rc) return rc;
-  return launch_route(d, a->dtype, static_cast<hipStream_t>(stream));
+  rc = launch_route(d, a->dtype, static_cast<hipStream_t>(stream));
+  return rc ? rc : launch_lists(d, static_cast<hipStream_t>(stream));
 }
 
-namespace q36 {
-namespace {
-int launch_up(const MoeDev& d, int dtype, hipStream_t st) {
-  const int units = 1 + (d.E < d.M * d.k ? d.E : d.M * d.k);
-  if (dtype == Q36_MOE_FP8)
-    moe_up_kernel<Q36_MOE_FP8><<<units * (d.I / 16), 256, 0, st>>>(d);
-  else
-    moe_up_kernel<Q36_MOE_INT8><<<units * (d.I / 16), 256, 0, st>>>(d);
-  return check_launch("q36_moe_up");
-}
-int launch_down(const MoeDev& d, int dtype, hipStream_t st) {
-  const int units = 1 + (d.E < d.M * d.k ? d.E : d.M * d.k);
-  if (dtype == Q36_MOE_FP8)
-    moe_down_kernel<Q36_MOE_FP8><<<units * (d.H / 64), 256, 0, st>>>(d);
-  else
-    moe_down_kernel<Q36_MOE_INT8><<<units * (d.H / 64), 256, 0, st>>>(d);
-  return check_launch("q36_moe_down");
-}
-int launch_combine(const MoeDev& d, hipStream_t st) {
-  moe_combine_kernel<<<d.M, 256, 0, st>>>(d);
-  return check_launch("q36_moe_combine");
-}
-}  // namespace
-}  // namespace q36
 
 extern "C" int q36_moe_up(const q36_moe_args* a, q36_stream_t stream) {
   MoeDev d;

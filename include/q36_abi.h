@@ -56,12 +56,12 @@ const char* q36_last_error(void);
  *   gate_w bf16 [H]; out bf16 [M,H].
  * Constraints: H == 2048 and I == 512 (this build), E % 64 == 0, 64 <= E <= 1024,
  *   1 <= topk <= min(16, E), 1 <= M <= 256; every pointer 16-byte aligned.
- * Workspace: q36_moe_workspace_bytes() bytes, 256-byte aligned, ZEROED ONCE after allocation;
- *   the kernels leave it in the state they need on the next call (self-resetting ticket).
- *   q36_moe_workspace_layout() gives the byte offset of each list inside it.
- * Debug outputs (NULL to skip), indexed by sorted position p (routed 0..M*topk-1 in expert order,
- *   shared M*topk + t): dbg_acc13 int32 [M*topk+M, 2I], dbg_acc2 int32 [M*topk+M, H] (INT8 only:
- *   the GEMM accumulators before scaling), dbg_h bf16 [M*topk+M, I] (SwiGLU output).
+ * Workspace: q36_moe_workspace_bytes() bytes, 256-byte aligned, no initial contents required
+ *   (every call writes what it reads).  q36_moe_workspace_layout() gives the byte offset of each
+ *   list inside it.
+ * Debug outputs (NULL to skip), indexed by slot (routed t*topk + j, shared M*topk + t):
+ *   dbg_acc13 int32 [M*topk+M, 2I], dbg_acc2 int32 [M*topk+M, H] (INT8 only: the GEMM
+ *   accumulators before scaling), dbg_h bf16 [M*topk+M, I] (SwiGLU output).
  * Calls that overlap on one workspace race; distinct workspaces are independent. */
 typedef struct q36_moe_args {
   int32_t M, E, H, I, topk, dtype;
@@ -95,11 +95,14 @@ typedef struct q36_moe_ws_layout {
   size_t perm;     /* int32 [M*topk] sorted position -> slot t*topk+j (-1 past offsets[E]) */
   size_t inv_perm; /* int32 [M*topk] slot -> sorted position (-1 for padding) */
   size_t active;   /* int32 [E] experts with counts > 0, ascending */
-  size_t ctl;      /* int32 [64]: [0] route ticket (kept zero between calls), [1] n_active */
+  size_t ctl;      /* int32 [64]: [1] n_active (published by q36_moe_route) */
   size_t xq;       /* quantized x [M,H] */
   size_t xs;       /* fp32 [M, H/128] (INT8: [M]) */
-  size_t h;        /* bf16 [M*topk+M, I] */
-  size_t y;        /* bf16 [M*topk+M, H] */
+  size_t h;        /* bf16 [M*topk+M, I] by slot (t*topk + j; shared M*topk + t) */
+  size_t y;        /* bf16 [M*topk+M, H] by slot, routing weight applied */
+  size_t ecount;   /* int32 [E] tokens per expert (route-internal) */
+  size_t eact;     /* int32 [E] experts with tokens, unordered (route-internal; ctl[2] counts) */
+  size_t elist;    /* int32 [E, M] slots of each expert, unordered (route-internal) */
   size_t total;
 } q36_moe_ws_layout;
 

@@ -390,15 +390,15 @@ int q36o_moe(const q36o_moe_args* a) {
   size_t es13 = a->mode == 0 ? (size_t)2 * I : (size_t)(2 * I / 128) * (H / 128);
   size_t es2 = a->mode == 0 ? (size_t)H : (size_t)(H / 128) * (I / 128);
 #pragma omp parallel for schedule(dynamic, 1)
-  for (int p = 0; p < S + M; ++p) {
+  for (int p = 0; p < S + M; ++p) {  /* p = slot: t*k + j routed, S + t shared */
     int t, e;
     float wt;
     expert_t ex = {a->mode, H, I, 0, 0, 0, 0};
     if (p < S) {
-      if (perm[p] < 0) continue;
-      t = perm[p] / k;
-      e = a->ids[perm[p]];
-      wt = a->wts[perm[p]];
+      if (a->ids[p] < 0) continue;
+      t = p / k;
+      e = a->ids[p];
+      wt = a->wts[p];
       ex.w13 = (const char*)a->w13 + (size_t)e * eb13;
       ex.s13 = a->s13 + (size_t)e * es13;
       ex.w2 = (const char*)a->w2 + (size_t)e * eb2;
@@ -426,7 +426,7 @@ int q36o_moe(const q36o_moe_args* a) {
     const uint16_t* ysh = y + (size_t)(S + t) * H;
     for (int n = 0; n < H; ++n) {
       float acc = 0.f;
-      for (int j = 0; j < k; ++j) acc = acc + q36o_bf16_to_f32(y[(size_t)inv[t * k + j] * H + n]);
+      for (int j = 0; j < k; ++j) acc = acc + q36o_bf16_to_f32(y[(size_t)(t * k + j) * H + n]);
       o[n] = q36o_f32_to_bf16(fmaf(gate, q36o_bf16_to_f32(ysh[n]), acc));
     }
   }

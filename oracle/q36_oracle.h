@@ -42,7 +42,7 @@ int q36o_route(const uint16_t* x, const uint16_t* wr, const float* bias, const i
 /* ---- MoE block (routed experts + shared expert + sigmoid gate + combine) ----
  * mode 0: int8 W8A8 (per-token / per-slot int8 activations, per-channel fp32 weight scales)
  * mode 1: fp8 e4m3 (per-token x 128-group activations, 128x128 block weight scales)
- * Optional debug outputs, indexed by sorted position p (routed 0..M*k-1, shared M*k + t):
+ * Optional debug outputs, indexed by slot (routed t*k + j, shared M*k + t):
  *   acc13 int32 [M*k+M, 2I] and acc2 int32 [M*k+M, H] (mode 0 only), h bf16 [M*k+M, I]. */
 typedef struct {
   int mode, M, E, H, I, k;
