@@ -112,6 +112,33 @@ def bench_moe(args, torch, dev):
     return res
 
 
+def bench_gdn(args, torch, dev):
+    """Config 3: GDN verify step, 32 sequences x (1 + 4) positions."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import gdn_fused
+
+    B, T = 32, 5
+    d = synth.gdn_inputs(B, T, dev, seed=0)
+    out = torch.empty((B * T, 4096), dtype=torch.bfloat16, device=dev)
+    snaps = torch.empty((B, T, 32, 128, 128), dtype=torch.float32, device=dev)
+    cso = torch.empty_like(d["conv_state"])
+
+    def step():
+        gdn_fused.gdn_verify_fused(d["mixed"], d["z"], d["a"], d["b"], d["conv_state"], d["conv_w"], d["A_log"],
+                                   d["dt_bias"], d["S0"], d["norm_w"], 1e-6, T=T, out=out, snaps=snaps,
+                                   conv_state_out=cso)
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    ms = events_time(step, args.steps, torch)
+    R = B * T
+    state = B * 32 * 128 * 128 * 4
+    algo = (state + T * state + R * 8192 * 2 + R * 4096 * 2 + 2 * R * 32 * 2 + 2 * B * 8192 * 3 * 2
+            + 8192 * 4 * 2 + R * 4096 * 2)
+    return dict(us_per_step=ms * 1e3, bytes=algo, gbs=algo / (ms * 1e-3) / 1e9, sequences=B, positions=T)
+
+
 def cpu_moe_baseline(res, seconds):
     """The C oracle on this host's cores over the same batch-64 fp8 layer (whole batches)."""
     import numpy as np
@@ -160,6 +187,10 @@ def main():
     moe_res = bench_moe(args, torch, dev)
     print(f"bench: MoE done ({moe_res['ms_graph'] * 1e3:.1f} us/layer)", file=sys.stderr, flush=True)
 
+    print("bench: GDN verify 32 x 5", file=sys.stderr, flush=True)
+    gdn_res = bench_gdn(args, torch, dev)
+    print(f"bench: GDN done ({gdn_res['us_per_step']:.1f} us/step)", file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu:
         print("bench: CPU oracle baseline", file=sys.stderr, flush=True)
@@ -188,6 +219,10 @@ def main():
                      "traffic": None},
         "cpu_baseline": cpu,
         "moe": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in moe_res.items()},
+        "gdn_verify": {"us_per_step": round(gdn_res["us_per_step"], 2), "bytes": gdn_res["bytes"],
+                       "achieved_gbs": round(gdn_res["gbs"], 1), "frac_hbm": round(gdn_res["gbs"] / HBM_PEAK_GBS, 4),
+                       "workload": "32 sequences x (1+4) positions, 16 QK / 32 V heads x 128, fp32 state + "
+                                   "per-position snapshots"},
     }
     print(json.dumps(line), flush=True)
 

@@ -35,8 +35,8 @@ class MoeWsLayout(C.Structure):
 
 class GdnArgs(C.Structure):
     _fields_ = [("B", I32), ("T", I32), ("mixed", P), ("z", P), ("a", P), ("b", P), ("conv_state", P),
-                ("conv_w", P), ("A_log", P), ("dt_bias", P), ("S0", P), ("norm_w", P), ("eps", C.c_float),
-                ("out", P), ("snaps", P)]
+                ("conv_state_out", P), ("conv_w", P), ("A_log", P), ("dt_bias", P), ("S0", P), ("norm_w", P),
+                ("eps", C.c_float), ("out", P), ("snaps", P)]
 
 
 class AttnArgs(C.Structure):
@@ -69,6 +69,7 @@ SYMBOLS = [
     ("q36_moe_down", I32, [C.POINTER(MoeArgs), P]),
     ("q36_moe_combine", I32, [C.POINTER(MoeArgs), P]),
     ("q36_moe_forward", I32, [C.POINTER(MoeArgs), P]),
+    ("q36_gdn_verify", I32, [C.POINTER(GdnArgs), P]),
     ("q36_quant_rows_i8", I32, [P, C.c_int64, I32, P, P, P]),
     ("q36_quant_blocks_e4m3", I32, [P, C.c_int64, I32, P, P, P]),
 ]

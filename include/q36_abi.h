@@ -124,6 +124,37 @@ int q36_moe_combine(const q36_moe_args* a, q36_stream_t stream);
 int q36_moe_forward(const q36_moe_args* a, q36_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
+ * GDN speculative-verify step (L/qk_gdn_verify.cu:841-849 gdn_verify_fused), fixed head
+ * geometry: 16 key heads x 128, 32 value heads x 128 (value head h reads key head h/2).
+ *   mixed bf16 [B*T, 8192] = q (16x128) | k (16x128) | v (32x128), row b*T + t
+ *   z bf16 [B*T, 4096]; a, b bf16 [B*T, 32]
+ *   conv_state bf16 [B, 8192, 3] (taps oldest first, read only); conv_state_out bf16 [B, 8192, 3]
+ *     receives the state after the T positions (the last three inputs); must not alias conv_state
+ *   conv_w bf16 [8192, 4]; A_log, dt_bias fp32 [32]; norm_w bf16 [128]
+ *   S0 fp32 [B, 32, 128 (v), 128 (k)] (read only)
+ *   out bf16 [B*T, 4096] = gated RMSNorm of o_t = S_t q_t
+ *   snaps fp32 [B, T, 32, 128, 128]: S_t after position t (the rollback states)
+ * 1 <= T <= 8; S0 and snaps 16-byte aligned. */
+typedef struct q36_gdn_args {
+  int32_t B, T;
+  const void* mixed;
+  const void* z;
+  const void* a;
+  const void* b;
+  const void* conv_state;
+  void* conv_state_out;
+  const void* conv_w;
+  const float* A_log;
+  const float* dt_bias;
+  const float* S0;
+  const void* norm_w;
+  float eps;
+  void* out;
+  float* snaps;
+} q36_gdn_args;
+int q36_gdn_verify(const q36_gdn_args* a, q36_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
  * Prepare-time weight quantizers (device to device).
  *   q36_quant_rows_i8:     w bf16 [N,K] -> q int8 [N,K], s fp32 [N]   (s = amax/127, half-away)
  *   q36_quant_blocks_e4m3: w bf16 [N,K] -> q e4m3 [N,K], s fp32 [N/128, K/128]
