@@ -139,6 +139,37 @@ def bench_gdn(args, torch, dev):
     return dict(us_per_step=ms * 1e3, bytes=algo, gbs=algo / (ms * 1e-3) / 1e9, sequences=B, positions=T)
 
 
+def bench_attn(args, torch, dev):
+    """Config 4: fused gated attention projections at 128 tokens (proj + norm/RoPE, then o_proj)."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import attn_fused
+
+    T = 128
+    d = synth.attn_inputs(T, dev, seed=0)
+    w = attn_fused.prepare_weights(d["wqg"], d["wk"], d["wv"], d["wo"])
+    ws = attn_fused.Workspace(T, dev)
+    o = attn_fused.attn_proj(d["x"], w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"], ws)
+    out = torch.empty((T, 2048), dtype=torch.bfloat16, device=dev)
+    gate = o["gate"].reshape(T, 4096)
+
+    def proj():
+        attn_fused.attn_proj(d["x"], w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"], ws, out=o)
+
+    def oproj():
+        attn_fused.attn_oproj(d["attn"], gate, w, ws, out=out)
+
+    for _ in range(max(1, args.warmup)):
+        proj()
+        oproj()
+    torch.cuda.synchronize()
+    ms_p = events_time(proj, args.steps, torch)
+    ms_o = events_time(oproj, args.steps, torch)
+    wbytes = 9216 * 2048 + 72 * 16 * 4 + 2048 * 4096 + 16 * 32 * 4
+    abytes = T * 2048 * 2 + T * (8192 + 1024) * 2 + T * 1024 + 2 * T * 4096 * 2 + T * 2048 * 2
+    tot = wbytes + abytes
+    return dict(us_proj=ms_p * 1e3, us_oproj=ms_o * 1e3, bytes=tot, gbs=tot / ((ms_p + ms_o) * 1e-3) / 1e9)
+
+
 def cpu_moe_baseline(res, seconds):
     """The C oracle on this host's cores over the same batch-64 fp8 layer (whole batches)."""
     import numpy as np
@@ -191,6 +222,9 @@ def main():
     gdn_res = bench_gdn(args, torch, dev)
     print(f"bench: GDN done ({gdn_res['us_per_step']:.1f} us/step)", file=sys.stderr, flush=True)
 
+    print("bench: attention projections 128 tokens", file=sys.stderr, flush=True)
+    attn_res = bench_attn(args, torch, dev)
+
     cpu = None
     if not args.no_cpu:
         print("bench: CPU oracle baseline", file=sys.stderr, flush=True)
@@ -219,6 +253,10 @@ def main():
                      "traffic": None},
         "cpu_baseline": cpu,
         "moe": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in moe_res.items()},
+        "attn_proj": {"us_proj": round(attn_res["us_proj"], 2), "us_oproj": round(attn_res["us_oproj"], 2),
+                      "bytes": attn_res["bytes"], "achieved_gbs": round(attn_res["gbs"], 1),
+                      "frac_hbm": round(attn_res["gbs"] / HBM_PEAK_GBS, 4),
+                      "workload": "128 tokens, e4m3 128x128-block qkv [9216,2048] + o_proj [2048,4096]"},
         "gdn_verify": {"us_per_step": round(gdn_res["us_per_step"], 2), "bytes": gdn_res["bytes"],
                        "achieved_gbs": round(gdn_res["gbs"], 1), "frac_hbm": round(gdn_res["gbs"] / HBM_PEAK_GBS, 4),
                        "workload": "32 sequences x (1+4) positions, 16 QK / 32 V heads x 128, fp32 state + "

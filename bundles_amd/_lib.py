@@ -40,10 +40,9 @@ class GdnArgs(C.Structure):
 
 
 class AttnArgs(C.Structure):
-    _fields_ = [("T", I32), ("max_pos", I32), ("x", P), ("wqg", P), ("sqg", P), ("wk", P), ("sk", P), ("wv", P),
-                ("sv", P), ("q_norm_w", P), ("k_norm_w", P), ("eps", C.c_float), ("cos_sin", P),
-                ("positions", P), ("q", P), ("gate", P), ("k", P), ("v", P), ("k8", P), ("v8", P),
-                ("workspace", P), ("workspace_bytes", SZ)]
+    _fields_ = [("T", I32), ("max_pos", I32), ("x", P), ("wqkv", P), ("sqkv", P), ("q_norm_w", P),
+                ("k_norm_w", P), ("eps", C.c_float), ("cos_sin", P), ("positions", P), ("q", P), ("gate", P),
+                ("k", P), ("v", P), ("k8", P), ("v8", P), ("workspace", P), ("workspace_bytes", SZ)]
 
 
 class OprojArgs(C.Structure):
@@ -70,6 +69,10 @@ SYMBOLS = [
     ("q36_moe_combine", I32, [C.POINTER(MoeArgs), P]),
     ("q36_moe_forward", I32, [C.POINTER(MoeArgs), P]),
     ("q36_gdn_verify", I32, [C.POINTER(GdnArgs), P]),
+    ("q36_attn_workspace_bytes", SZ, [I32]),
+    ("q36_oproj_workspace_bytes", SZ, [I32]),
+    ("q36_attn_proj", I32, [C.POINTER(AttnArgs), P]),
+    ("q36_attn_oproj", I32, [C.POINTER(OprojArgs), P]),
     ("q36_quant_rows_i8", I32, [P, C.c_int64, I32, P, P, P]),
     ("q36_quant_blocks_e4m3", I32, [P, C.c_int64, I32, P, P, P]),
 ]

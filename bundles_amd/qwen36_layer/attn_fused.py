@@ -1,0 +1,78 @@
+"""Fused gated full-attention projections on libq36 (q36_attn_proj, q36_attn_oproj).
+
+Mirrors the reference's attention glue (R = qwen36_nodes_kb34, L = R/qwen36_layer): the fused
+qkv projection + q/k norm + partial RoPE + e4m3 KV write (L/attn_fused.py:232-273,
+L/qk_attn_verify.cu:765-797 attn_prefill_front) and the gated o_proj input
+(L/qk_attn_verify.cu:730-737).  Weights are e4m3 with 128x128 block scales (prepare_weights).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from .. import _lib
+from .._lib import AttnArgs, OprojArgs, check, ptr
+from .moe import quantize_blocks_e4m3
+
+N_Q_HEADS, N_KV_HEADS, HEAD_DIM, HIDDEN = 16, 2, 256, 2048
+QKV_ROWS = 2 * N_Q_HEADS * HEAD_DIM + 2 * N_KV_HEADS * HEAD_DIM  # 9216
+
+
+@dataclass
+class AttnWeights:
+    wqkv: torch.Tensor   # e4m3 codes [9216, 2048]
+    sqkv: torch.Tensor   # fp32 [72, 16]
+    wo: torch.Tensor     # e4m3 codes [2048, 4096]
+    so: torch.Tensor     # fp32 [16, 32]
+
+
+def prepare_weights(wqg: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor, wo: torch.Tensor) -> AttnWeights:
+    """bf16 Wqg [8192,2048] (q/gate interleaved per head), Wk/Wv [512,2048], Wo [2048,4096] -> e4m3 blocks."""
+    qkv = torch.cat([wqg, wk, wv], dim=0).contiguous()
+    q, s = quantize_blocks_e4m3(qkv)
+    qo, so = quantize_blocks_e4m3(wo.contiguous())
+    return AttnWeights(q, s, qo, so)
+
+
+def rope_cos_sin(max_pos: int, theta: float = 1e7, rot_dim: int = 64, device="cpu") -> torch.Tensor:
+    inv = theta ** (-torch.arange(0, rot_dim, 2, dtype=torch.float64) / rot_dim)
+    ang = torch.arange(max_pos, dtype=torch.float64)[:, None] * inv[None, :]
+    return torch.cat([ang.cos(), ang.sin()], dim=1).to(torch.float32).to(device)
+
+
+class Workspace:
+    def __init__(self, T_max: int, device):
+        L = _lib.lib()
+        self.T_max = T_max
+        self.proj = torch.empty(L.q36_attn_workspace_bytes(T_max), dtype=torch.uint8, device=device)
+        self.oproj = torch.empty(L.q36_oproj_workspace_bytes(T_max), dtype=torch.uint8, device=device)
+
+
+def attn_proj(x, w: AttnWeights, q_norm_w, k_norm_w, eps, cos_sin, positions, ws: Workspace, out=None, stream=None):
+    """Returns dict(q, gate, k, v, k8, v8) for tokens x bf16 [T, 2048]."""
+    T = x.shape[0]
+    if T > ws.T_max:
+        raise ValueError(f"attn_proj: {T} tokens exceed the workspace's {ws.T_max}")
+    dev = x.device
+    o = out or dict(q=torch.empty((T, N_Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=dev),
+                    gate=torch.empty((T, N_Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=dev),
+                    k=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=dev),
+                    v=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=dev),
+                    k8=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.uint8, device=dev),
+                    v8=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.uint8, device=dev))
+    a = AttnArgs(T, cos_sin.shape[0], ptr(x), ptr(w.wqkv), ptr(w.sqkv), ptr(q_norm_w), ptr(k_norm_w), eps,
+                 ptr(cos_sin), ptr(positions), ptr(o["q"]), ptr(o["gate"]), ptr(o["k"]), ptr(o["v"]), ptr(o["k8"]),
+                 ptr(o["v8"]), ptr(ws.proj), ws.proj.numel())
+    check(_lib.lib().q36_attn_proj(C.byref(a), _lib.stream_handle(stream)), "q36_attn_proj")
+    return o
+
+
+def attn_oproj(attn, gate, w: AttnWeights, ws: Workspace, out=None, stream=None):
+    """out bf16 [T, 2048] = o_proj(bf16(attn * sigmoid(gate))), attn / gate bf16 [T, 4096]."""
+    T = attn.shape[0]
+    out = torch.empty((T, HIDDEN), dtype=torch.bfloat16, device=attn.device) if out is None else out
+    a = OprojArgs(T, ptr(attn), ptr(gate), ptr(w.wo), ptr(w.so), ptr(out), ptr(ws.oproj), ws.oproj.numel())
+    check(_lib.lib().q36_attn_oproj(C.byref(a), _lib.stream_handle(stream)), "q36_attn_oproj")
+    return out

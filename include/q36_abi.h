@@ -155,6 +155,53 @@ typedef struct q36_gdn_args {
 int q36_gdn_verify(const q36_gdn_args* a, q36_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Fused gated full-attention projections (16 q heads x 256 with an output gate per head,
+ * 2 KV heads x 256, hidden 2048), e4m3 weights with fp32 128x128 block scales.
+ *   q36_attn_proj:  x bf16 [T, 2048] -> e4m3 activations (per token x 128 channels) ->
+ *     qkv = x . wqkv^T with wqkv e4m3 [9216, 2048] = rows [q(256) gate(256)] x 16 | k 2x256 | v 2x256
+ *     (the reference's fused qkv layout, L/attn_fused.py:209), sqkv fp32 [72, 16], rounded to bf16;
+ *     then per head: Gemma RMSNorm on q and k (q_norm_w, k_norm_w bf16 [256], eps), neox RoPE on
+ *     dims 0..63 with cos_sin fp32 [max_pos, 64] (cos 0..31 | sin 0..31) at positions int32 [T]
+ *     (L/qk_attn_verify.cu:156-208).  Outputs: q bf16 [T,16,256], gate bf16 [T,16,256],
+ *     k, v bf16 [T,2,256], k8, v8 e4m3 [T,2,256] (the cache write, satfinite, no scale).
+ *   q36_attn_oproj: out bf16 [T, 2048] = (bf16(attn * sigmoid(gate)) in e4m3) . wo^T with
+ *     attn, gate bf16 [T, 4096], wo e4m3 [2048, 4096], so fp32 [16, 32] (L/qk_attn_verify.cu:730-737).
+ * Workspaces: q36_attn_workspace_bytes(T), q36_oproj_workspace_bytes(T), 256-byte aligned. */
+typedef struct q36_attn_args {
+  int32_t T, max_pos;
+  const void* x;
+  const void* wqkv;
+  const float* sqkv;
+  const void* q_norm_w;
+  const void* k_norm_w;
+  float eps;
+  const float* cos_sin;
+  const int32_t* positions;
+  void* q;
+  void* gate;
+  void* k;
+  void* v;
+  void* k8;
+  void* v8;
+  void* workspace;
+  size_t workspace_bytes;
+} q36_attn_args;
+typedef struct q36_oproj_args {
+  int32_t T;
+  const void* attn;
+  const void* gate;
+  const void* wo;
+  const float* so;
+  void* out;
+  void* workspace;
+  size_t workspace_bytes;
+} q36_oproj_args;
+size_t q36_attn_workspace_bytes(int32_t T);
+size_t q36_oproj_workspace_bytes(int32_t T);
+int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream);
+int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
  * Prepare-time weight quantizers (device to device).
  *   q36_quant_rows_i8:     w bf16 [N,K] -> q int8 [N,K], s fp32 [N]   (s = amax/127, half-away)
  *   q36_quant_blocks_e4m3: w bf16 [N,K] -> q e4m3 [N,K], s fp32 [N/128, K/128]

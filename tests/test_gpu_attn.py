@@ -1,0 +1,67 @@
+"""GPU parity of the fused attention projections (libq36 through the C-ABI) against the CPU oracle.
+
+Bar: bf16 outputs (q, gate, k, v, o_proj out) within 1e-2 relative (per-row norm); the e4m3 cache
+rows decode to values within the same bar."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bf16_close, bits16, bits8, np_
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def attn():
+    from bundles_amd import _lib
+    _lib.lib()
+    from bundles_amd.qwen36_layer import attn_fused
+    return attn_fused
+
+
+def _setup(attn, dev, T, seed):
+    from bundles_amd import synth
+    d = synth.attn_inputs(T, dev, seed=seed)
+    w = attn.prepare_weights(d["wqg"], d["wk"], d["wv"], d["wo"])
+    d["positions"][0] = 0
+    d["positions"][-1] = 32767
+    return d, w
+
+
+def _oracle_weights(w):
+    q, s = np_(w.wqkv).astype(np.uint8), np_(w.sqkv)
+    return dict(wqg=q[:8192], sqg=s[:64], wk=q[8192:8704], sk=s[64:68], wv=q[8704:], sv=s[68:72])
+
+
+@pytest.mark.parametrize("T", [1, 37, 128])
+def test_attn_proj_parity(attn, oracle_mod, dev, T):
+    O = oracle_mod
+    print(f"attn_proj T={T}", flush=True)
+    d, w = _setup(attn, dev, T, seed=T)
+    ws = attn.Workspace(T, dev)
+    o = attn.attn_proj(d["x"], w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"], ws)
+    torch.cuda.synchronize()
+    ow = _oracle_weights(w)
+    r = O.attn_proj(bits16(d["x"]), ow["wqg"], ow["sqg"], ow["wk"], ow["sk"], ow["wv"], ow["sv"],
+                    bits16(d["q_norm_w"]), bits16(d["k_norm_w"]), 1e-6, np_(d["cos_sin"]), np_(d["positions"]))
+    for key in ("q", "gate", "k", "v"):
+        wr, ar, er = assert_bf16_close(bits16(o[key]).reshape(T, -1), r[key].reshape(T, -1), 1e-2, key)
+        print(f"{key}: row err {wr:.2e} elem {ar:.2e} exact {er:.4f}", flush=True)
+    for key in ("k8", "v8"):
+        got = O.e4m3_to_f32(bits8(o[key]).reshape(T, -1))
+        ref = O.e4m3_to_f32(r[key].reshape(T, -1))
+        assert_bf16_close(O.f32_to_bf16(got), O.f32_to_bf16(ref), 1e-2, key)
+        print(f"{key}: exact codes {np.mean(bits8(o[key]).reshape(T, -1) == r[key].reshape(T, -1)):.4f}")
+
+
+@pytest.mark.parametrize("T", [1, 128])
+def test_attn_oproj_parity(attn, oracle_mod, dev, T):
+    O = oracle_mod
+    d, w = _setup(attn, dev, T, seed=100 + T)
+    ws = attn.Workspace(T, dev)
+    gate = (torch.randn((T, 4096), device=dev) * 2).to(torch.bfloat16)
+    out = attn.attn_oproj(d["attn"], gate, w, ws)
+    torch.cuda.synchronize()
+    r = O.attn_oproj(bits16(d["attn"]), bits16(gate), np_(w.wo).astype(np.uint8), np_(w.so))
+    wr, ar, er = assert_bf16_close(bits16(out), r, 1e-2, "oproj")
+    print(f"oproj: row err {wr:.2e} elem {ar:.2e} exact {er:.4f}", flush=True)
