@@ -170,6 +170,32 @@ def bench_attn(args, torch, dev):
     return dict(us_proj=ms_p * 1e3, us_oproj=ms_o * 1e3, bytes=tot, gbs=tot / ((ms_p + ms_o) * 1e-3) / 1e9)
 
 
+MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8, published
+
+
+def bench_lmhead(args, torch, dev):
+    """Config 5 head: int8 lm_head + argmax over 2048 rows (256 sequences x 8 positions) x 151936."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_lmhead8 import lmhead8
+
+    R, V = 2048, 151936
+    d = synth.lmhead_inputs(R, V, dev, seed=0)
+    q, s = lmhead8.quantize_rows(d["w"])
+    del d["w"]
+    ws = lmhead8.Workspace(R, dev)
+    ids = torch.empty(R, dtype=torch.int32, device=dev)
+
+    def step():
+        lmhead8.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=d["norm_w"], eps=1e-6, ids=ids)
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    ms = events_time(step, max(5, args.steps // 2), torch)
+    ops = 2.0 * R * V * 2048
+    return dict(us_per_step=ms * 1e3, ops=ops, tops=ops / (ms * 1e-3) / 1e12, rows=R, vocab=V)
+
+
 def cpu_moe_baseline(res, seconds):
     """The C oracle on this host's cores over the same batch-64 fp8 layer (whole batches)."""
     import numpy as np
@@ -222,6 +248,8 @@ def main():
     gdn_res = bench_gdn(args, torch, dev)
     print(f"bench: GDN done ({gdn_res['us_per_step']:.1f} us/step)", file=sys.stderr, flush=True)
 
+    print("bench: lm_head + argmax 2048 x 151936", file=sys.stderr, flush=True)
+    lmh_res = bench_lmhead(args, torch, dev)
     print("bench: attention projections 128 tokens", file=sys.stderr, flush=True)
     attn_res = bench_attn(args, torch, dev)
 
@@ -253,6 +281,10 @@ def main():
                      "traffic": None},
         "cpu_baseline": cpu,
         "moe": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in moe_res.items()},
+        "lmhead_argmax": {"us_per_step": round(lmh_res["us_per_step"], 2), "ops": lmh_res["ops"],
+                          "achieved_tops": round(lmh_res["tops"], 1), "peak_tops": MFMA_I8_PEAK_TOPS,
+                          "frac_mfma": round(lmh_res["tops"] / MFMA_I8_PEAK_TOPS, 4),
+                          "workload": "2048 rows x 151936 vocab x 2048, int8 W8A8 + final RMSNorm + argmax"},
         "attn_proj": {"us_proj": round(attn_res["us_proj"], 2), "us_oproj": round(attn_res["us_oproj"], 2),
                       "bytes": attn_res["bytes"], "achieved_gbs": round(attn_res["gbs"], 1),
                       "frac_hbm": round(attn_res["gbs"] / HBM_PEAK_GBS, 4),

@@ -73,6 +73,8 @@ SYMBOLS = [
     ("q36_oproj_workspace_bytes", SZ, [I32]),
     ("q36_attn_proj", I32, [C.POINTER(AttnArgs), P]),
     ("q36_attn_oproj", I32, [C.POINTER(OprojArgs), P]),
+    ("q36_lmhead_workspace_bytes", SZ, [I32]),
+    ("q36_lmhead_argmax", I32, [C.POINTER(LmheadArgs), P]),
     ("q36_quant_rows_i8", I32, [P, C.c_int64, I32, P, P, P]),
     ("q36_quant_blocks_e4m3", I32, [P, C.c_int64, I32, P, P, P]),
 ]

@@ -1,0 +1,45 @@
+"""Int8 lm_head with fused greedy argmax on libq36 (q36_lmhead_argmax, q36_quant_rows_i8).
+
+Mirrors the reference's lm_head glue (R = qwen36_nodes_kb34, H = R/qwen36_lmhead8):
+  quantize_rows       <- H/lmhead8.py:111 (per-row int8, fp32 scale amax/127, round half away)
+  w8a8_lmhead_argmax  <- H/w8a8.py:116-120 w8a8_linear, with the greedy argmax of the stock sampler
+                         (H/node.py:136-151) fused in; logits are returned only when asked for.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from .. import _lib
+from .._lib import LmheadArgs, check, ptr
+
+
+def quantize_rows(w: torch.Tensor, stream=None):
+    """bf16 [N, K] -> (int8 [N, K], fp32 scale [N])."""
+    from ..qwen36_layer.moe import quantize_rows_i8
+    return quantize_rows_i8(w, stream=stream)
+
+
+class Workspace:
+    def __init__(self, R_max: int, device):
+        self.R_max = R_max
+        self.buf = torch.empty(_lib.lib().q36_lmhead_workspace_bytes(R_max), dtype=torch.uint8, device=device)
+
+
+def w8a8_lmhead_argmax(h, q, scale, ws: Workspace, norm_w=None, eps: float = 1e-6, want_logits: bool = False,
+                       ids=None, stream=None):
+    """h bf16 [R, 2048] -> ids int32 [R] (and bf16 logits [R, V] when want_logits)."""
+    R, H = h.shape
+    V = q.shape[0]
+    if R > ws.R_max:
+        raise ValueError(f"w8a8_lmhead_argmax: {R} rows exceed the workspace's {ws.R_max}")
+    for name, t, dt in (("h", h, torch.bfloat16), ("q", q, torch.int8), ("scale", scale, torch.float32)):
+        if t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"w8a8_lmhead_argmax: {name} must be contiguous {dt}")
+    ids = torch.empty(R, dtype=torch.int32, device=h.device) if ids is None else ids
+    logits = torch.empty((R, V), dtype=torch.bfloat16, device=h.device) if want_logits else None
+    a = LmheadArgs(R, H, V, ptr(h), ptr(norm_w), eps, ptr(q), ptr(scale), ptr(ids), ptr(logits), ptr(ws.buf),
+                   ws.buf.numel())
+    check(_lib.lib().q36_lmhead_argmax(C.byref(a), _lib.stream_handle(stream)), "q36_lmhead_argmax")
+    return (ids, logits) if want_logits else ids

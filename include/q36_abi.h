@@ -202,6 +202,28 @@ int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream);
 int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Int8 lm_head fused with greedy argmax (H/w8a8.py:116-120 w8a8_linear + the stock argmax,
+ * H/node.py:136-151).  h bf16 [R, H] (H = 2048) -> optional final Gemma RMSNorm (norm_w bf16 [H],
+ * NULL to skip; y = bf16((h * rstd) * (1 + w))) -> per-row int8 (s = amax/127, half away) ->
+ * acc = xq . wq^T (int32, wq int8 [V, H], ws fp32 [V]) -> logit = bf16((acc * xs) * ws) ->
+ * ids int32 [R] = first index of the row's largest logit.  logits bf16 [R, V] is optional (NULL
+ * skips the store).  V % 16 == 0.  Workspace: q36_lmhead_workspace_bytes(R), 256-byte aligned. */
+typedef struct q36_lmhead_args {
+  int32_t R, H, V;
+  const void* h;
+  const void* norm_w;
+  float eps;
+  const int8_t* wq;
+  const float* ws;
+  int32_t* ids;
+  void* logits;
+  void* workspace;
+  size_t workspace_bytes;
+} q36_lmhead_args;
+size_t q36_lmhead_workspace_bytes(int32_t R);
+int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
  * Prepare-time weight quantizers (device to device).
  *   q36_quant_rows_i8:     w bf16 [N,K] -> q int8 [N,K], s fp32 [N]   (s = amax/127, half-away)
  *   q36_quant_blocks_e4m3: w bf16 [N,K] -> q e4m3 [N,K], s fp32 [N/128, K/128]

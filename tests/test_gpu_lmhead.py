@@ -1,0 +1,78 @@
+"""GPU parity of the int8 lm_head + argmax (libq36 through the C-ABI) against the CPU oracle.
+
+Bar: int8 activations, logits (exact: int32 accumulation and two IEEE products) and argmax ids
+bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits16, np_
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def lmh():
+    from bundles_amd import _lib
+    _lib.lib()
+    from bundles_amd.qwen36_lmhead8 import lmhead8
+    return lmhead8
+
+
+def _setup(lmh, dev, R, V, seed):
+    from bundles_amd import synth
+    d = synth.lmhead_inputs(R, V, dev, seed=seed)
+    q, s = lmh.quantize_rows(d["w"])
+    return d, q, s
+
+
+@pytest.mark.parametrize("R,V,norm", [(1, 2048, True), (37, 4096, True), (256, 8192, False), (300, 4112, True)])
+def test_lmhead_logits_and_ids_exact(lmh, oracle_mod, dev, R, V, norm):
+    O = oracle_mod
+    print(f"lmhead R={R} V={V} norm={norm}", flush=True)
+    d, q, s = _setup(lmh, dev, R, V, seed=R + V)
+    ws = lmh.Workspace(R, dev)
+    nw = d["norm_w"] if norm else None
+    ids, logits = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=nw, eps=1e-6, want_logits=True)
+    torch.cuda.synchronize()
+    rid, rlog = O.lmhead(bits16(d["h"]), bits16(nw) if norm else None, 1e-6, np_(q), np_(s), want_logits=True)
+    assert np.array_equal(bits16(logits), rlog), "logits differ"
+    assert np.array_equal(np_(ids), rid), "argmax ids differ"
+
+
+def test_lmhead_full_vocab(lmh, oracle_mod, dev):
+    O = oracle_mod
+    R, V = 64, 151936
+    d, q, s = _setup(lmh, dev, R, V, seed=5)
+    ws = lmh.Workspace(R, dev)
+    ids = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=d["norm_w"], eps=1e-6)
+    torch.cuda.synchronize()
+    rid, _ = O.lmhead(bits16(d["h"]), bits16(d["norm_w"]), 1e-6, np_(q), np_(s))
+    assert np.array_equal(np_(ids), rid)
+
+
+def test_lmhead_config5_rows_subset(lmh, oracle_mod, dev):
+    """Config 5: 2048 rows (256 sequences x 8 positions) x 151936; 64 rows checked on the CPU."""
+    O = oracle_mod
+    R, V = 2048, 151936
+    d, q, s = _setup(lmh, dev, R, V, seed=0)
+    ws = lmh.Workspace(R, dev)
+    ids = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=d["norm_w"], eps=1e-6)
+    torch.cuda.synchronize()
+    rows = np.concatenate([np.arange(0, 8), np.arange(R - 8, R), np.random.default_rng(0).choice(R, 48, False)])
+    rid, _ = O.lmhead(np.ascontiguousarray(bits16(d["h"])[rows]), bits16(d["norm_w"]), 1e-6, np_(q), np_(s))
+    assert np.array_equal(np_(ids)[rows], rid)
+
+
+def test_lmhead_ties_pick_first_index(lmh, dev):
+    R, V = 8, 2048
+    d, q, s = _setup(lmh, dev, R, V, seed=9)
+    q[1000] = q[17]
+    s[1000] = s[17]
+    q[2047] = q[17]
+    s[2047] = s[17]
+    ws = lmh.Workspace(R, dev)
+    ids, logits = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, want_logits=True)
+    torch.cuda.synchronize()
+    lg = logits.float().cpu().numpy()
+    assert np.array_equal(np_(ids), lg.argmax(axis=1))  # numpy argmax = first maximal index
