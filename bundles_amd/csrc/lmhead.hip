@@ -103,22 +103,23 @@ __global__ __launch_bounds__(256) void lmh_prep_kernel(LmhDev d) {
 // (chunk kc of eight consecutive rows) touch eight distinct 16-byte bank windows.
 __device__ __forceinline__ int bswz(int c, int kc) { return c * kBK + ((kc ^ ((c >> 1) & 3)) << 4); }
 
-__device__ __forceinline__ unsigned long long logit_key64(float lg, int col) {
-  uint32_t b = __float_as_uint(lg) >> 16;  // bf16 value
-  if (b == 0x8000u) b = 0u;
-  b = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
-  return ((unsigned long long)b << 32) | (unsigned long long)(0xffffffffu - (uint32_t)col);
-}
-
 template <int N>
 using ic = std::integral_constant<int, N>;
+
+// x rounded to bf16 (round to nearest even), returned as the float it represents: one
+// v_cvt_pk_bf16_f32 with a zero low half.
+__device__ __forceinline__ float round_bf16(float x) {
+  typedef float v2f __attribute__((ext_vector_type(2)));
+  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(float, __builtin_convertvector((v2f){0.f, x}, v2bf));
+}
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lmh_gemm_kernel(LmhDev d) {
   // Four LDS stages per operand, one object each: the compiler tracks the buffer-to-LDS loads of
   // each object separately and waits only for those of the stage being read.
   __shared__ __align__(1024) int8_t a_s0[kBM * kBK], a_s1[kBM * kBK], a_s2[kBM * kBK], a_s3[kBM * kBK];
   __shared__ __align__(1024) int8_t b_s0[kBN * kBK], b_s1[kBN * kBK], b_s2[kBN * kBK], b_s3[kBN * kBK];
-  __shared__ unsigned long long rkey[2][kBM];
+  __shared__ uint32_t rkey[2][kBM];
   auto a_st = [&](auto st) -> int8_t* {
     if constexpr (decltype(st)::value == 0) return a_s0;
     else if constexpr (decltype(st)::value == 1) return a_s1;
@@ -205,44 +206,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     body(ks + 3, ic<3>{}, ic<2>{}, std::false_type{});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  // epilogue: lane holds columns v0 + wn*128 + ni*16 + lr and rows r0 + wm*128 + mi*16 + 4 lgp + q
+  // Epilogue: lane holds columns cb + ni*16 + lr and rows r0 + wm*128 + mi*16 + 4 lgp + q.  Each
+  // logit is rounded to bf16 once (hardware round-to-nearest-even); the lane keeps the first
+  // largest of its eight columns per row by a float compare (-0 == +0 as in the bf16 argmax); the
+  // 16 lanes of a row then combine a 32-bit key (order-preserving bf16 bits << 16 | 0xffff - column
+  // in the tile) by DPP max, the two column waves through LDS, and the tile through one 64-bit
+  // atomic max per row.  Column groups past V (V % 16 == 0) are wave-uniform and skipped.
+  const int cb = v0 + wn * 128;
+  const int nv = min(8, (d.V - cb) / 16);
   float wsv[8];
 #pragma unroll
-  for (int ni = 0; ni < 8; ++ni) {
-    const int col = v0 + wn * 128 + ni * 16 + lr;
-    wsv[ni] = col < d.V ? d.ws[col] : 0.f;
-  }
+  for (int ni = 0; ni < 8; ++ni) wsv[ni] = ni < nv ? d.ws[cb + ni * 16 + lr] : 0.f;
+  auto epilogue = [&](auto store) {
 #pragma unroll
-  for (int mi = 0; mi < 8; ++mi) {
+    for (int mi = 0; mi < 8; ++mi) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int rl = wm * 128 + mi * 16 + 4 * lgp + q;
-      const int row = r0 + rl;
-      const float xsr = row < d.R ? d.xs[row] : 0.f;
-      unsigned long long best = 0ull;
+      for (int q = 0; q < 4; ++q) {
+        const int rl = wm * 128 + mi * 16 + 4 * lgp + q;
+        const int row = r0 + rl;
+        const float xsr = row < d.R ? d.xs[row] : 0.f;
+        float best = -__builtin_inff();
+        int bi = 0;
 #pragma unroll
-      for (int ni = 0; ni < 8; ++ni) {
-        const int col = v0 + wn * 128 + ni * 16 + lr;
-        const float lg = rbf(((float)acc[mi][ni][q] * xsr) * wsv[ni]);
-        if (col < d.V) {
-          const unsigned long long k = logit_key64(lg, col);
-          best = k > best ? k : best;
-          if (d.logits && row < d.R) d.logits[(size_t)row * d.V + col] = (uint16_t)f2bf(lg);
+        for (int ni = 0; ni < 8; ++ni) {
+          const float lg = round_bf16(((float)acc[mi][ni][q] * xsr) * wsv[ni]);
+          if (ni < nv) {
+            if (lg > best) {
+              best = lg;
+              bi = ni;
+            }
+            if constexpr (decltype(store)::value)
+              if (row < d.R) d.logits[(size_t)row * d.V + cb + ni * 16 + lr] = (uint16_t)(__float_as_uint(lg) >> 16);
+          }
         }
+        uint32_t b16 = __float_as_uint(best + 0.f) >> 16;
+        b16 = (b16 & 0x8000u) ? (~b16 & 0xffffu) : (b16 | 0x8000u);
+        const uint32_t key = row16_max_u32((b16 << 16) | (0xffffu - (uint32_t)(wn * 128 + bi * 16 + lr)));
+        if (lr == 0) rkey[wn][rl] = key;
       }
-      // max over the 16 lanes of this row (lanes sharing lgp)
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) {
-        const unsigned long long other = __shfl_xor(best, o);
-        best = other > best ? other : best;
-      }
-      if (lr == 0) rkey[wn][rl] = best;
     }
-  }
+  };
+  if (d.logits)
+    epilogue(std::true_type{});
+  else
+    epilogue(std::false_type{});
   __syncthreads();
   if (r0 + tid < d.R) {
-    const unsigned long long k = rkey[0][tid] > rkey[1][tid] ? rkey[0][tid] : rkey[1][tid];
-    atomicMax(&d.keys[r0 + tid], k);
+    const uint32_t k = max(rkey[0][tid], rkey[1][tid]);
+    const uint32_t col = (uint32_t)v0 + (0xffffu - (k & 0xffffu));
+    atomicMax(&d.keys[r0 + tid], ((unsigned long long)(k >> 16) << 32) | (unsigned long long)(0xffffffffu - col));
   }
 }
 

@@ -120,6 +120,15 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return max(max(a, b), max(c, d));
 }
 
+// Unsigned max over each row of 16 lanes (every lane of the row gets the row's maximum).
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  v = max(v, dpp_u32<0x140>(v));
+  return v;
+}
+
 // Round half away from zero and clamp to +-127 (the int8 activation / weight rule).
 __device__ __forceinline__ int round_i8(float v) {
   float r = v >= 0.f ? __builtin_floorf(v + 0.5f) : -__builtin_floorf(0.5f - v);
