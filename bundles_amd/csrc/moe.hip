@@ -1022,29 +1022,6 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
 
 // Raise a kernel's dynamic-LDS limit (once per device and kernel) when a launch needs more than
 // the 64 KiB default; gfx950 has 160 KiB per CU.
-int ensure_lds(const void* fn, size_t bytes, const char* what) {
-  if (bytes <= 65536) return Q36_OK;
-  static const void* done[64][8] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  for (int i = 0; i < 8; ++i)
-    if (done[dev][i] == fn) return Q36_OK;
-  if (bytes > 160 * 1024) {
-    set_error("%s: %zu bytes of LDS exceed the 160 KiB of a CU", what, bytes);
-    return Q36_EINVAL;
-  }
-  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
-    set_error("%s: hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed", what);
-    return Q36_ELAUNCH;
-  }
-  for (int i = 0; i < 8; ++i)
-    if (done[dev][i] == nullptr) {
-      done[dev][i] = fn;
-      break;
-    }
-  return Q36_OK;
-}
-
 int launch_route(const MoeDev& d, int dtype, hipStream_t st) {
   const int n_router = (d.E / 16) * ((d.M + kRouteTT - 1) / kRouteTT);
   if (dtype == Q36_MOE_FP8)

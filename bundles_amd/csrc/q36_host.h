@@ -11,6 +11,9 @@ namespace q36 {
 
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 
+// Allow kernel fn `bytes` of dynamic LDS (above 64 KiB: raises the kernel's limit once per device).
+int ensure_lds(const void* fn, size_t bytes, const char* what);
+
 inline bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 

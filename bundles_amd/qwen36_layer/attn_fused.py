@@ -22,10 +22,20 @@ QKV_ROWS = 2 * N_Q_HEADS * HEAD_DIM + 2 * N_KV_HEADS * HEAD_DIM  # 9216
 
 @dataclass
 class AttnWeights:
-    wqkv: torch.Tensor   # e4m3 codes [9216, 2048]
+    wqkv: torch.Tensor   # e4m3 codes [9216, 2048] (row-major)
     sqkv: torch.Tensor   # fp32 [72, 16]
-    wo: torch.Tensor     # e4m3 codes [2048, 4096]
+    wo: torch.Tensor     # e4m3 codes [2048, 4096] (row-major)
     so: torch.Tensor     # fp32 [16, 32]
+    wqkv_p: torch.Tensor = None  # the same codes in MFMA fragment order (what the kernels read)
+    wo_p: torch.Tensor = None
+
+
+def pack_frag(q: torch.Tensor, stream=None) -> torch.Tensor:
+    """e4m3 codes [N, K] row-major -> the MFMA fragment order of q36_pack_frag_e4m3 (same bytes)."""
+    N, K = q.shape
+    out = torch.empty_like(q)
+    check(_lib.lib().q36_pack_frag_e4m3(ptr(q), N, K, ptr(out), _lib.stream_handle(stream)), "q36_pack_frag_e4m3")
+    return out
 
 
 def prepare_weights(wqg: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor, wo: torch.Tensor) -> AttnWeights:
@@ -33,7 +43,7 @@ def prepare_weights(wqg: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor, wo: t
     qkv = torch.cat([wqg, wk, wv], dim=0).contiguous()
     q, s = quantize_blocks_e4m3(qkv)
     qo, so = quantize_blocks_e4m3(wo.contiguous())
-    return AttnWeights(q, s, qo, so)
+    return AttnWeights(q, s, qo, so, pack_frag(q), pack_frag(qo))
 
 
 def rope_cos_sin(max_pos: int, theta: float = 1e7, rot_dim: int = 64, device="cpu") -> torch.Tensor:
@@ -62,7 +72,7 @@ def attn_proj(x, w: AttnWeights, q_norm_w, k_norm_w, eps, cos_sin, positions, ws
                     v=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=dev),
                     k8=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.uint8, device=dev),
                     v8=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.uint8, device=dev))
-    a = AttnArgs(T, cos_sin.shape[0], ptr(x), ptr(w.wqkv), ptr(w.sqkv), ptr(q_norm_w), ptr(k_norm_w), eps,
+    a = AttnArgs(T, cos_sin.shape[0], ptr(x), ptr(w.wqkv_p), ptr(w.sqkv), ptr(q_norm_w), ptr(k_norm_w), eps,
                  ptr(cos_sin), ptr(positions), ptr(o["q"]), ptr(o["gate"]), ptr(o["k"]), ptr(o["v"]), ptr(o["k8"]),
                  ptr(o["v8"]), ptr(ws.proj), ws.proj.numel())
     check(_lib.lib().q36_attn_proj(C.byref(a), _lib.stream_handle(stream)), "q36_attn_proj")
@@ -73,6 +83,6 @@ def attn_oproj(attn, gate, w: AttnWeights, ws: Workspace, out=None, stream=None)
     """out bf16 [T, 2048] = o_proj(bf16(attn * sigmoid(gate))), attn / gate bf16 [T, 4096]."""
     T = attn.shape[0]
     out = torch.empty((T, HIDDEN), dtype=torch.bfloat16, device=attn.device) if out is None else out
-    a = OprojArgs(T, ptr(attn), ptr(gate), ptr(w.wo), ptr(w.so), ptr(out), ptr(ws.oproj), ws.oproj.numel())
+    a = OprojArgs(T, ptr(attn), ptr(gate), ptr(w.wo_p), ptr(w.so), ptr(out), ptr(ws.oproj), ws.oproj.numel())
     check(_lib.lib().q36_attn_oproj(C.byref(a), _lib.stream_handle(stream)), "q36_attn_oproj")
     return out

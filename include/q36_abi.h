@@ -21,6 +21,8 @@
  *   q36_quant_rows_i8  <- lmhead8.quantize_rows / w8a8.quantize_act (H/lmhead8.py:111; H/w8a8.py:77)
  *   q36_quant_blocks_e4m3 <- (no reference counterpart: the 128x128 block-scaled e4m3 weight
  *                         format the configuration asks for)
+ *   q36_pack_frag_e4m3 <- (no reference counterpart: a prepare-time reordering of those weights
+ *                         into the operand order of the gfx950 MFMA)
  */
 #ifndef Q36_ABI_H
 #define Q36_ABI_H
@@ -159,13 +161,15 @@ int q36_gdn_verify(const q36_gdn_args* a, q36_stream_t stream);
  * 2 KV heads x 256, hidden 2048), e4m3 weights with fp32 128x128 block scales.
  *   q36_attn_proj:  x bf16 [T, 2048] -> e4m3 activations (per token x 128 channels) ->
  *     qkv = x . wqkv^T with wqkv e4m3 [9216, 2048] = rows [q(256) gate(256)] x 16 | k 2x256 | v 2x256
- *     (the reference's fused qkv layout, L/attn_fused.py:209), sqkv fp32 [72, 16], rounded to bf16;
+ *     (the reference's fused qkv layout, L/attn_fused.py:209) passed in fragment order
+ *     (q36_pack_frag_e4m3), sqkv fp32 [72, 16], rounded to bf16;
  *     then per head: Gemma RMSNorm on q and k (q_norm_w, k_norm_w bf16 [256], eps), neox RoPE on
  *     dims 0..63 with cos_sin fp32 [max_pos, 64] (cos 0..31 | sin 0..31) at positions int32 [T]
  *     (L/qk_attn_verify.cu:156-208).  Outputs: q bf16 [T,16,256], gate bf16 [T,16,256],
  *     k, v bf16 [T,2,256], k8, v8 e4m3 [T,2,256] (the cache write, satfinite, no scale).
  *   q36_attn_oproj: out bf16 [T, 2048] = (bf16(attn * sigmoid(gate)) in e4m3) . wo^T with
- *     attn, gate bf16 [T, 4096], wo e4m3 [2048, 4096], so fp32 [16, 32] (L/qk_attn_verify.cu:730-737).
+ *     attn, gate bf16 [T, 4096], wo e4m3 [2048, 4096] in fragment order, so fp32 [16, 32]
+ *     (L/qk_attn_verify.cu:730-737).
  * Workspaces: q36_attn_workspace_bytes(T), q36_oproj_workspace_bytes(T), 256-byte aligned. */
 typedef struct q36_attn_args {
   int32_t T, max_pos;
@@ -228,9 +232,14 @@ int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream);
  *   q36_quant_rows_i8:     w bf16 [N,K] -> q int8 [N,K], s fp32 [N]   (s = amax/127, half-away)
  *   q36_quant_blocks_e4m3: w bf16 [N,K] -> q e4m3 [N,K], s fp32 [N/128, K/128]
  *                          (s = amax/448, q = e4m3_rn_sat(w * (448/amax)))
- * K % 128 == 0 (and N % 128 == 0 for blocks). */
+ *   q36_pack_frag_e4m3:    q e4m3 [N,K] row-major -> packed, the MFMA fragment order the
+ *                          attention kernels read: for row tile r = n / 16 and block b = k / 128,
+ *                          2048 bytes at (r * K/128 + b) * 2048; inside, byte h*1024 + 16*l + j
+ *                          holds q[16 r + l % 16][128 b + 32 (l / 16) + 16 h + j] (h < 2, l < 64).
+ * K % 128 == 0 (and N % 128 == 0 for blocks, N % 16 == 0 for the packing). */
 int q36_quant_rows_i8(const void* w, int64_t N, int32_t K, int8_t* q, float* s, q36_stream_t stream);
 int q36_quant_blocks_e4m3(const void* w, int64_t N, int32_t K, uint8_t* q, float* s, q36_stream_t stream);
+int q36_pack_frag_e4m3(const uint8_t* q, int64_t N, int32_t K, uint8_t* packed, q36_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -65,3 +65,21 @@ def test_attn_oproj_parity(attn, oracle_mod, dev, T):
     r = O.attn_oproj(bits16(d["attn"]), bits16(gate), np_(w.wo).astype(np.uint8), np_(w.so))
     wr, ar, er = assert_bf16_close(bits16(out), r, 1e-2, "oproj")
     print(f"oproj: row err {wr:.2e} elem {ar:.2e} exact {er:.4f}", flush=True)
+
+
+def test_pack_frag_layout(attn, dev):
+    """q36_pack_frag_e4m3 against the documented byte map, on a ragged-looking shape."""
+    N, K = 48, 384
+    q = torch.randint(0, 256, (N, K), dtype=torch.uint8, device=dev)
+    got = np_(attn.pack_frag(q))
+    src = np_(q)
+    ref = np.empty(N * K, np.uint8)
+    nkb = K // 128
+    for r in range(N // 16):
+        for b in range(nkb):
+            base = (r * nkb + b) * 2048
+            for h in range(2):
+                for l in range(64):
+                    row, col = 16 * r + l % 16, 128 * b + 32 * (l // 16) + 16 * h
+                    ref[base + h * 1024 + 16 * l: base + h * 1024 + 16 * l + 16] = src[row, col:col + 16]
+    assert np.array_equal(got.reshape(-1), ref)
