@@ -6,7 +6,7 @@ MoE layer over one batch of 64 tokens with every input resident in HBM.  value =
 layer.  Beside it: the roofline of the dominant kernel (the expert up-projection, HBM-bound), the
 other nodes' step times, and the CPU oracle timed on this host's cores on the same workload.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only moe,gdn,lmhead,attn] [--copy-calib]
 """
 from __future__ import annotations
 
@@ -28,6 +28,18 @@ def cpu_cores() -> int:
     except AttributeError:
         n = os.cpu_count() or 1
     return max(1, min(n, 16))
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter runs (profiles/hbm_traffic.json:
+    FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the counter reads for a plain copy
+    of known size), or None when that file does not list the kernel."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
+            t = json.load(f)[kernel]
+        return int(t["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def events_time(fn, steps, torch):
@@ -162,12 +174,22 @@ def bench_attn(args, torch, dev):
         proj()
         oproj()
     torch.cuda.synchronize()
+    # as in the engine's captured verify step: one graph per projection, replayed
     ms_p = events_time(proj, args.steps, torch)
     ms_o = events_time(oproj, args.steps, torch)
+    gp, go = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gp):
+        proj()
+    with torch.cuda.graph(go):
+        oproj()
+    torch.cuda.synchronize()
+    ms_pg = events_time(gp.replay, args.steps, torch)
+    ms_og = events_time(go.replay, args.steps, torch)
     wbytes = 9216 * 2048 + 72 * 16 * 4 + 2048 * 4096 + 16 * 32 * 4
     abytes = T * 2048 * 2 + T * (8192 + 1024) * 2 + T * 1024 + 2 * T * 4096 * 2 + T * 2048 * 2
     tot = wbytes + abytes
-    return dict(us_proj=ms_p * 1e3, us_oproj=ms_o * 1e3, bytes=tot, gbs=tot / ((ms_p + ms_o) * 1e-3) / 1e9)
+    return dict(us_proj=ms_p * 1e3, us_oproj=ms_o * 1e3, us_proj_graph=ms_pg * 1e3, us_oproj_graph=ms_og * 1e3,
+                bytes=tot, gbs=tot / ((ms_p + ms_o) * 1e-3) / 1e9)
 
 
 MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8, published
@@ -217,7 +239,7 @@ def cpu_moe_baseline(res, seconds):
         O.moe(1, x, wr, *hw, gw, 10, bias=bias, n_threads=cores)
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 50:
+        if el >= seconds or n >= 400:
             break
     return dict(value=64 * n / el, unit="tokens/s", cores=cores, kind="port",
                 sample=f"{n} full batch-64 fp8 MoE layers (512 experts, top-10, Zipf router) in {el:.1f} s")
@@ -230,6 +252,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="moe,gdn,lmhead,attn",
+                    help="comma list of the nodes to run (the headline needs moe)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run a plain 256 MiB device copy (the reference kernel for HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the MoE, GDN and lm_head nodes are measured on one "
@@ -240,18 +266,28 @@ def main():
     from bundles_amd import _lib
     _lib.lib()  # fails loudly when libq36.so is not built
     dev = torch.device("cuda:0")
+    only = set(args.only.split(","))
     print(f"bench: MoE fp8 batch 64, steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
     moe_res = bench_moe(args, torch, dev)
     print(f"bench: MoE done ({moe_res['ms_graph'] * 1e3:.1f} us/layer)", file=sys.stderr, flush=True)
-
-    print("bench: GDN verify 32 x 5", file=sys.stderr, flush=True)
-    gdn_res = bench_gdn(args, torch, dev)
-    print(f"bench: GDN done ({gdn_res['us_per_step']:.1f} us/step)", file=sys.stderr, flush=True)
-
-    print("bench: lm_head + argmax 2048 x 151936", file=sys.stderr, flush=True)
-    lmh_res = bench_lmhead(args, torch, dev)
-    print("bench: attention projections 128 tokens", file=sys.stderr, flush=True)
-    attn_res = bench_attn(args, torch, dev)
+    gdn_res = lmh_res = attn_res = None
+    if "gdn" in only:
+        print("bench: GDN verify 32 x 5", file=sys.stderr, flush=True)
+        gdn_res = bench_gdn(args, torch, dev)
+        print(f"bench: GDN done ({gdn_res['us_per_step']:.1f} us/step)", file=sys.stderr, flush=True)
+    if "lmhead" in only:
+        print("bench: lm_head + argmax 2048 x 151936", file=sys.stderr, flush=True)
+        lmh_res = bench_lmhead(args, torch, dev)
+    if "attn" in only:
+        print("bench: attention projections 128 tokens", file=sys.stderr, flush=True)
+        attn_res = bench_attn(args, torch, dev)
+    if args.copy_calib:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     cpu = None
     if not args.no_cpu:
@@ -278,22 +314,29 @@ def main():
                    "router_skew": "Zipf(1.1)", "unique_experts": moe_res["unique_experts"]},
         "roofline": {"bound": "hbm", "kernel": "moe_up_kernel<fp8>", "achieved": round(up_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(up_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic("moe_up_kernel<fp8>")},
         "cpu_baseline": cpu,
         "moe": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in moe_res.items()},
-        "lmhead_argmax": {"us_per_step": round(lmh_res["us_per_step"], 2), "ops": lmh_res["ops"],
-                          "achieved_tops": round(lmh_res["tops"], 1), "peak_tops": MFMA_I8_PEAK_TOPS,
-                          "frac_mfma": round(lmh_res["tops"] / MFMA_I8_PEAK_TOPS, 4),
-                          "workload": "2048 rows x 151936 vocab x 2048, int8 W8A8 + final RMSNorm + argmax"},
-        "attn_proj": {"us_proj": round(attn_res["us_proj"], 2), "us_oproj": round(attn_res["us_oproj"], 2),
-                      "bytes": attn_res["bytes"], "achieved_gbs": round(attn_res["gbs"], 1),
-                      "frac_hbm": round(attn_res["gbs"] / HBM_PEAK_GBS, 4),
-                      "workload": "128 tokens, e4m3 128x128-block qkv [9216,2048] + o_proj [2048,4096]"},
-        "gdn_verify": {"us_per_step": round(gdn_res["us_per_step"], 2), "bytes": gdn_res["bytes"],
-                       "achieved_gbs": round(gdn_res["gbs"], 1), "frac_hbm": round(gdn_res["gbs"] / HBM_PEAK_GBS, 4),
-                       "workload": "32 sequences x (1+4) positions, 16 QK / 32 V heads x 128, fp32 state + "
-                                   "per-position snapshots"},
     }
+    if lmh_res:
+        line["lmhead_argmax"] = {
+            "us_per_step": round(lmh_res["us_per_step"], 2), "ops": lmh_res["ops"],
+            "achieved_tops": round(lmh_res["tops"], 1), "peak_tops": MFMA_I8_PEAK_TOPS,
+            "frac_mfma": round(lmh_res["tops"] / MFMA_I8_PEAK_TOPS, 4),
+            "workload": "2048 rows x 151936 vocab x 2048, int8 W8A8 + final RMSNorm + argmax"}
+    if attn_res:
+        line["attn_proj"] = {
+            "us_proj": round(attn_res["us_proj"], 2), "us_oproj": round(attn_res["us_oproj"], 2),
+            "us_proj_graph": round(attn_res["us_proj_graph"], 2), "us_oproj_graph": round(attn_res["us_oproj_graph"], 2),
+            "bytes": attn_res["bytes"], "achieved_gbs": round(attn_res["gbs"], 1),
+            "frac_hbm": round(attn_res["gbs"] / HBM_PEAK_GBS, 4),
+            "workload": "128 tokens, e4m3 128x128-block qkv [9216,2048] + o_proj [2048,4096] (eager back-to-back "
+                        "launches; *_graph: one captured graph per call, replayed)"}
+    if gdn_res:
+        line["gdn_verify"] = {
+            "us_per_step": round(gdn_res["us_per_step"], 2), "bytes": gdn_res["bytes"],
+            "achieved_gbs": round(gdn_res["gbs"], 1), "frac_hbm": round(gdn_res["gbs"] / HBM_PEAK_GBS, 4),
+            "workload": "32 sequences x (1+4) positions, 16 QK / 32 V heads x 128, fp32 state + per-position snapshots"}
     print(json.dumps(line), flush=True)
 
 
