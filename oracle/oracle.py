@@ -115,6 +115,13 @@ def e4m3_lut() -> np.ndarray:
     return np.array([L.q36o_e4m3_to_f32(i) for i in range(256)], dtype=np.float32)
 
 
+def f32_to_e4m3(x: np.ndarray) -> np.ndarray:
+    """Element-wise q36o_f32_to_e4m3 (RNE, satfinite); for small arrays."""
+    enc = lib().q36o_f32_to_e4m3
+    x = np.asarray(x, np.float32)
+    return np.fromiter((enc(float(v)) for v in x.reshape(-1)), np.uint8, x.size).reshape(x.shape)
+
+
 def e4m3_to_f32(b: np.ndarray) -> np.ndarray:
     return e4m3_lut()[np.asarray(b, dtype=np.uint8)]
 
