@@ -8,14 +8,19 @@
 //   combine          L/i8x_decode.py:424-443; L/qk_route.cu:630-722
 //
 // Launch sequence on the caller's stream (no host synchronisation, graph-capturable):
-//   1. route_logits  router GEMV (bf16 logits) + per-token activation quantization
-//   2. route_topk    softmax / top-k / renormalise per token; the last workgroup (ticket) builds
-//                    the expert lists (counts, offsets, perm, inv_perm, active) in canonical order
-//   3. moe_up        one workgroup per (active expert, 16 gate + 16 up rows): weights streamed once
-//                    into registers, MFMA over every 16-token tile of the expert, SwiGLU -> h
-//   4. moe_down      one workgroup per (active expert, 64 output rows): h re-quantized in LDS,
-//                    MFMA, x routing weight -> y per sorted position
-//   5. moe_combine   out = bf16(fma(sigmoid(x . gate_w), y_shared, sum_j y_j))
+//   1. route_logits  router GEMV (bf16 logits, canonical reduction order) + per-token activation
+//                    quantization; also clears the per-expert counters for step 2
+//   2. route_topk    softmax / top-k / renormalise, one wave per token; each pick appends its slot
+//                    (t * k + j) to its expert's slot list through an atomic counter (the order
+//                    inside a list changes no output: every result is stored by slot)
+//      route_lists   (q36_moe_route only) the canonical maps: counts, offsets, perm, inv_perm and
+//                    active, expert ascending, then token, then pick
+//   3. moe_up        one workgroup per (unit, 64 gate + 64 up rows): each wave streams its 16 + 16
+//                    weight rows over the whole K once, MFMA against every 16-token tile of the
+//                    unit's tokens (staged in LDS), SwiGLU -> h per slot
+//   4. moe_down      one workgroup per (unit, 128 output rows): the unit's h rows re-quantized
+//                    once in LDS, MFMA, x routing weight -> y per slot
+//   5. moe_combine   out = bf16(fma(sigmoid(x . gate_w), y_shared, sum_j y_j)), j in pick order
 // The shared expert is unit 0 of the up/down grids and covers every token.
 #include <string.h>
 
