@@ -77,7 +77,7 @@ SYMBOLS = [
     ("q36_lmhead_argmax", I32, [C.POINTER(LmheadArgs), P]),
     ("q36_quant_rows_i8", I32, [P, C.c_int64, I32, P, P, P]),
     ("q36_quant_blocks_e4m3", I32, [P, C.c_int64, I32, P, P, P]),
-    ("q36_pack_frag_e4m3", I32, [P, C.c_int64, I32, P, P]),
+    ("q36_pack_frag8", I32, [P, C.c_int64, I32, P, P]),
 ]
 OPTIONAL_SYMBOLS: list = []
 

@@ -317,7 +317,7 @@ void launch_gemm(const GemmDev& g, hipStream_t st) {
   fp8_gemm_kernel<RT, TPW, NKB><<<grid, 256, 0, st>>>(g);
 }
 
-// e4m3 [N, K] row-major -> fragment order; thread = one 16-byte chunk of the output
+// 8-bit codes (e4m3 or int8) [N, K] row-major -> fragment order; thread = one 16-byte chunk of the output
 __global__ __launch_bounds__(256) void pack_frag_kernel(const uint8_t* q, int64_t N, int K, uint8_t* out) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // output chunk
   const int64_t total = N * K / 16;
@@ -392,12 +392,13 @@ extern "C" int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream) {
   return check_launch("q36_attn_oproj");
 }
 
-extern "C" int q36_pack_frag_e4m3(const uint8_t* q, int64_t N, int32_t K, uint8_t* packed, q36_stream_t stream) {
-  Q36_REQUIRE(q && packed, "q36_pack_frag_e4m3: null pointer");
-  Q36_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 128 == 0, "q36_pack_frag_e4m3: N=%lld K=%d must be multiples of 16 and 128",
+extern "C" int q36_pack_frag8(const void* q, int64_t N, int32_t K, void* packed, q36_stream_t stream) {
+  Q36_REQUIRE(q && packed, "q36_pack_frag8: null pointer");
+  Q36_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 128 == 0, "q36_pack_frag8: N=%lld K=%d must be multiples of 16 and 128",
               (long long)N, K);
-  Q36_REQUIRE(aligned16(q) && aligned16(packed), "q36_pack_frag_e4m3: pointers must be 16-byte aligned");
+  Q36_REQUIRE(aligned16(q) && aligned16(packed), "q36_pack_frag8: pointers must be 16-byte aligned");
   const int64_t chunks = N * K / 16;
-  pack_frag_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(q, N, K, packed);
-  return check_launch("q36_pack_frag_e4m3");
+  pack_frag_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint8_t*>(q), N, K, static_cast<uint8_t*>(packed));
+  return check_launch("q36_pack_frag8");
 }

@@ -521,8 +521,8 @@ constexpr int kMoeH = 2048, kMoeI = 512;
 // the matching 16 up rows over the whole K = H, streamed from HBM in 16 stages of 128 bytes per
 // row with kUpD stages in flight; no reduction across waves.  The activation rows of up to 64
 // tokens (4 tiles of 16) are shared by the four waves through LDS, one K half at a time.
-// Per stage a lane holds 32 contiguous bytes of its row (row = lane % 16, bytes 32 (lane / 16))
-// of both operands -- one e4m3 16x16x128 MFMA, or two int8 16x16x64 MFMAs on the two 16-byte
+// Weights are stored in MFMA fragment order (q36_pack_frag8).  Per stage a lane holds 32 bytes of
+// its row (row = lane % 16, bytes 32 (lane / 16) of the 128-byte stage) of both operands -- one e4m3 16x16x128 MFMA, or two int8 16x16x64 MFMAs on the two 16-byte
 // halves (their K pairing is the same for src0 and src1, so the int32 sums are exact).  The
 // 16x16 result gives lane l weight row l%16 and token rows 4(l/16)+r; SwiGLU happens in the
 // lane.  For e4m3 the block terms (block sum * xs * ws) are added in increasing block order from
@@ -550,14 +550,16 @@ __global__ __launch_bounds__(256) void moe_up_kernel(MoeDev d) {
                           : d.s13 + (DT == Q36_MOE_FP8 ? (size_t)e * (2 * I / 128) * NSTG : (size_t)e * 2 * I);
   const int ch = grp * 4 + wave;
   const int ng = ch * 16 + lr;
-  const uint8_t* bg = W + (size_t)ng * H + lgp * 32;
-  const uint8_t* bu = W + (size_t)(I + ng) * H + lgp * 32;
+  // weights in fragment order: 16-row tile t, stage s at (t * NSTG + s) * 2048, the lane's two
+  // 16-byte halves at 16 lane and 1024 + 16 lane (one 1 KB contiguous load per half per wave)
+  const uint8_t* bg = W + ((size_t)ch * NSTG << 11) + lane * 16;
+  const uint8_t* bu = W + ((size_t)(I / 16 + ch) * NSTG << 11) + lane * 16;
   v4i Bq[kUpD][4];
   auto issue = [&](int s, int q) {
-    Bq[q][0] = ldg16_nt(bg + s * 128);
-    Bq[q][1] = ldg16_nt(bg + s * 128 + 16);
-    Bq[q][2] = ldg16_nt(bu + s * 128);
-    Bq[q][3] = ldg16_nt(bu + s * 128 + 16);
+    Bq[q][0] = ldg16_nt(bg + s * 2048);
+    Bq[q][1] = ldg16_nt(bg + s * 2048 + 1024);
+    Bq[q][2] = ldg16_nt(bu + s * 2048);
+    Bq[q][3] = ldg16_nt(bu + s * 2048 + 1024);
   };
 #pragma unroll
   for (int s = 0; s < kUpD; ++s) issue(s, s);  // the first weight stages, before the token list
@@ -703,9 +705,9 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeDev d) {
   for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
     for (int s = 0; s < NSTG; ++s) {
-      const uint8_t* src = W + (size_t)(n0 + ct * 16 + lr) * I + s * 128 + lgp * 32;
+      const uint8_t* src = W + ((size_t)((n0 >> 4) + ct) * NSTG << 11) + (s << 11) + lane * 16;  // fragment order
       B[ct][s][0] = ldg16_nt(src);
-      B[ct][s][1] = ldg16_nt(src + 16);
+      B[ct][s][1] = ldg16_nt(src + 1024);
     }
   int e_chk;
   const int cnt = unit_slots(d, unit, slots, wtot, &e_chk);

@@ -31,10 +31,10 @@ class AttnWeights:
 
 
 def pack_frag(q: torch.Tensor, stream=None) -> torch.Tensor:
-    """e4m3 codes [N, K] row-major -> the MFMA fragment order of q36_pack_frag_e4m3 (same bytes)."""
+    """e4m3 codes [N, K] row-major -> the MFMA fragment order of q36_pack_frag8 (same bytes)."""
     N, K = q.shape
     out = torch.empty_like(q)
-    check(_lib.lib().q36_pack_frag_e4m3(ptr(q), N, K, ptr(out), _lib.stream_handle(stream)), "q36_pack_frag_e4m3")
+    check(_lib.lib().q36_pack_frag8(ptr(q), N, K, ptr(out), _lib.stream_handle(stream)), "q36_pack_frag8")
     return out
 
 

@@ -27,6 +27,8 @@ MAX_TOKENS = 256  # the reference's row-batch limit (L/layer.py:50)
 class ExpertWeights:
     """Quantized routed experts + shared expert of one MoE layer (device tensors)."""
     dtype: int                  # Q36_MOE_INT8 or Q36_MOE_FP8
+    # the code tensors (w13, w2, sw13, sw2) hold their bytes in MFMA fragment order (pack_frag8);
+    # unpack_frag8_np gives the row-major view
     w13: torch.Tensor           # [E, 2I, H] int8 / uint8 (e4m3 codes)
     s13: torch.Tensor           # INT8 [E, 2I]; FP8 [E, 2I/128, H/128]
     w2: torch.Tensor            # [E, H, I]
@@ -72,9 +74,30 @@ def quantize_blocks_e4m3(w: torch.Tensor, stream=None):
     return q.view(w.shape), s.view(*lead, N // 128, K // 128)
 
 
+def pack_frag8(q: torch.Tensor, stream=None) -> torch.Tensor:
+    """8-bit codes [..., N, K] row-major -> the MFMA fragment order of q36_pack_frag8 (same shape and
+    bytes, reordered): 16-row tile t, 128-byte block b at (t * K/128 + b) * 2048; inside, byte
+    h*1024 + 16*l + j holds row 16 t + l % 16, column 128 b + 32 (l / 16) + 16 h + j."""
+    K = q.shape[-1]
+    N = q.numel() // K
+    out = torch.empty_like(q)
+    check(_lib.lib().q36_pack_frag8(ptr(q), N, K, ptr(out), _lib.stream_handle(stream)), "q36_pack_frag8")
+    return out
+
+
+def unpack_frag8_np(p):
+    """Host inverse of pack_frag8 (numpy array [..., N, K] in fragment order -> row-major)."""
+    shape = p.shape
+    K = shape[-1]
+    N = p.size // K
+    a = p.reshape(N // 16, K // 128, 2, 4, 16, 16)  # tile, block, half h, lane group, lane row, byte
+    return a.transpose(0, 4, 1, 3, 2, 5).reshape(shape)
+
+
 def prepare_experts(w13: torch.Tensor, w2: torch.Tensor, sw13: torch.Tensor, sw2: torch.Tensor,
                     dtype: int) -> ExpertWeights:
-    """Quantize bf16 expert weights once (prepare time).  w13 [E,2I,H], w2 [E,H,I], shared [2I,H], [H,I]."""
+    """Quantize bf16 expert weights once (prepare time) and store the codes in MFMA fragment order.
+    w13 [E,2I,H], w2 [E,H,I], shared [2I,H], [H,I]."""
     if dtype == Q36_MOE_INT8:
         q13, s13 = quantize_rows_i8(w13)
         q2, s2 = quantize_rows_i8(w2)
@@ -87,7 +110,7 @@ def prepare_experts(w13: torch.Tensor, w2: torch.Tensor, sw13: torch.Tensor, sw2
         qs2, ss2 = quantize_blocks_e4m3(sw2)
     else:
         raise ValueError(f"unknown MoE dtype {dtype}")
-    return ExpertWeights(dtype, q13, s13, q2, s2, qs13, ss13, qs2, ss2)
+    return ExpertWeights(dtype, pack_frag8(q13), s13, pack_frag8(q2), s2, pack_frag8(qs13), ss13, pack_frag8(qs2), ss2)
 
 
 def workspace_layout(M: int, E: int, H: int, I: int, topk: int, dtype: int) -> MoeWsLayout:  # noqa: E741

@@ -21,8 +21,8 @@
  *   q36_quant_rows_i8  <- lmhead8.quantize_rows / w8a8.quantize_act (H/lmhead8.py:111; H/w8a8.py:77)
  *   q36_quant_blocks_e4m3 <- (no reference counterpart: the 128x128 block-scaled e4m3 weight
  *                         format the configuration asks for)
- *   q36_pack_frag_e4m3 <- (no reference counterpart: a prepare-time reordering of those weights
- *                         into the operand order of the gfx950 MFMA)
+ *   q36_pack_frag8     <- (no reference counterpart: a prepare-time reordering of the 8-bit
+ *                         weights into the operand order of the gfx950 MFMA)
  */
 #ifndef Q36_ABI_H
 #define Q36_ABI_H
@@ -52,7 +52,8 @@ const char* q36_last_error(void);
  *   x bf16 [M,H]; router_w bf16 [E,H]; router_bias fp32 [E] or NULL (added before the bf16
  *   rounding of the logits); positions int32 [M] or NULL (rows whose position is 0 are padding:
  *   no experts, zero output);
- *   w13 [E,2I,H] (gate rows 0..I-1, up rows I..2I-1), w2 [E,H,I], int8 or e4m3 bytes;
+ *   w13 [E,2I,H] (gate rows 0..I-1, up rows I..2I-1), w2 [E,H,I], int8 or e4m3 bytes, each
+ *   (and the shared expert's) in MFMA fragment order (q36_pack_frag8 of the row-major codes);
  *   INT8 scales: s13 fp32 [E,2I], s2 fp32 [E,H]; FP8 scales: s13 [E,2I/128,H/128], s2 [E,H/128,I/128];
  *   shared expert sw13 [2I,H], sw2 [H,I] with scales of the same form (no E);
  *   gate_w bf16 [H]; out bf16 [M,H].
@@ -162,7 +163,7 @@ int q36_gdn_verify(const q36_gdn_args* a, q36_stream_t stream);
  *   q36_attn_proj:  x bf16 [T, 2048] -> e4m3 activations (per token x 128 channels) ->
  *     qkv = x . wqkv^T with wqkv e4m3 [9216, 2048] = rows [q(256) gate(256)] x 16 | k 2x256 | v 2x256
  *     (the reference's fused qkv layout, L/attn_fused.py:209) passed in fragment order
- *     (q36_pack_frag_e4m3), sqkv fp32 [72, 16], rounded to bf16;
+ *     (q36_pack_frag8), sqkv fp32 [72, 16], rounded to bf16;
  *     then per head: Gemma RMSNorm on q and k (q_norm_w, k_norm_w bf16 [256], eps), neox RoPE on
  *     dims 0..63 with cos_sin fp32 [max_pos, 64] (cos 0..31 | sin 0..31) at positions int32 [T]
  *     (L/qk_attn_verify.cu:156-208).  Outputs: q bf16 [T,16,256], gate bf16 [T,16,256],
@@ -232,14 +233,15 @@ int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream);
  *   q36_quant_rows_i8:     w bf16 [N,K] -> q int8 [N,K], s fp32 [N]   (s = amax/127, half-away)
  *   q36_quant_blocks_e4m3: w bf16 [N,K] -> q e4m3 [N,K], s fp32 [N/128, K/128]
  *                          (s = amax/448, q = e4m3_rn_sat(w * (448/amax)))
- *   q36_pack_frag_e4m3:    q e4m3 [N,K] row-major -> packed, the MFMA fragment order the
- *                          attention kernels read: for row tile r = n / 16 and block b = k / 128,
+ *   q36_pack_frag8:        8-bit codes (e4m3 or int8) [N,K] row-major -> packed, the MFMA
+ *                          fragment order the MoE and attention kernels read: for row tile
+ *                          r = n / 16 and block b = k / 128,
  *                          2048 bytes at (r * K/128 + b) * 2048; inside, byte h*1024 + 16*l + j
  *                          holds q[16 r + l % 16][128 b + 32 (l / 16) + 16 h + j] (h < 2, l < 64).
  * K % 128 == 0 (and N % 128 == 0 for blocks, N % 16 == 0 for the packing). */
 int q36_quant_rows_i8(const void* w, int64_t N, int32_t K, int8_t* q, float* s, q36_stream_t stream);
 int q36_quant_blocks_e4m3(const void* w, int64_t N, int32_t K, uint8_t* q, float* s, q36_stream_t stream);
-int q36_pack_frag_e4m3(const uint8_t* q, int64_t N, int32_t K, uint8_t* packed, q36_stream_t stream);
+int q36_pack_frag8(const void* q, int64_t N, int32_t K, void* packed, q36_stream_t stream);
 
 #ifdef __cplusplus
 }

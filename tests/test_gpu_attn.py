@@ -68,7 +68,7 @@ def test_attn_oproj_parity(attn, oracle_mod, dev, T):
 
 
 def test_pack_frag_layout(attn, dev):
-    """q36_pack_frag_e4m3 against the documented byte map, on a ragged-looking shape."""
+    """q36_pack_frag8 against the documented byte map, on a ragged-looking shape."""
     N, K = 48, 384
     q = torch.randint(0, 256, (N, K), dtype=torch.uint8, device=dev)
     got = np_(attn.pack_frag(q))

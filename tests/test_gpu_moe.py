@@ -21,7 +21,12 @@ def q36():
 
 
 def _host_weights(ew):
-    return {k: np_(getattr(ew, k)) for k in ("w13", "s13", "w2", "s2", "sw13", "ss13", "sw2", "ss2")}
+    """Host copies for the oracle: the code tensors back in row-major order."""
+    from bundles_amd.qwen36_layer.moe import unpack_frag8_np
+    hw = {k: np_(getattr(ew, k)) for k in ("w13", "s13", "w2", "s2", "sw13", "ss13", "sw2", "ss2")}
+    for k in ("w13", "w2", "sw13", "sw2"):
+        hw[k] = unpack_frag8_np(hw[k])
+    return hw
 
 
 def test_quant_rows_i8_matches_oracle(q36, oracle_mod, dev):
@@ -167,3 +172,14 @@ def test_moe_repeat_deterministic(q36, dev):
     torch.cuda.synchronize()
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
     assert torch.equal(outs[0].view(torch.int16), outs[2].view(torch.int16))
+
+
+def test_pack_frag8_round_trip(q36, dev):
+    """pack_frag8 then the host inverse gives the codes back, for int8 and e4m3 shapes of the experts."""
+    from bundles_amd.qwen36_layer.moe import pack_frag8, unpack_frag8_np
+    for shape in ((3, 1024, 2048), (2, 2048, 512), (48, 384)):
+        q = torch.randint(-128, 128, shape, dtype=torch.int8, device=dev)
+        p = pack_frag8(q)
+        torch.cuda.synchronize()
+        assert not torch.equal(p, q)
+        assert np.array_equal(unpack_frag8_np(np_(p)), np_(q))
