@@ -531,13 +531,19 @@ constexpr int kUpD = 4;                    // weight stages in flight per wave
 constexpr int kUpKH = kMoeH / 2;           // K bytes per LDS activation half
 constexpr int kUpRow = kUpKH + 16;         // padded LDS row (spreads the 16 rows over the banks)
 constexpr int kUpGroups = kMoeI / 16 / 4;  // workgroups per unit (4 chunks each)
+// Buffer load of 16 bytes per lane straight into LDS (lane l writes lds + 16 l); offsets past the
+// buffer's size read as zero.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds, 16, voff, 0, 0, 0);
+}
+
 template <int DT>
-__global__ __launch_bounds__(256) void moe_up_kernel(MoeDev d) {
-  constexpr int H = kMoeH, I = kMoeI, NSTG = H / 128, NT = 4;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void moe_up_kernel(MoeDev d) {
+  constexpr int H = kMoeH, I = kMoeI, NSTG = H / 128, TG = 64;
   extern __shared__ __align__(16) char up_lds[];
-  uint8_t* a_l = reinterpret_cast<uint8_t*>(up_lds);                     // [64][kUpRow]
-  float* xs_l = reinterpret_cast<float*>(up_lds + 64 * kUpRow);           // [64][NSTG]
-  float* ws_l = xs_l + 64 * NSTG;                                         // [2I/128][NSTG]
+  uint8_t* a_l = reinterpret_cast<uint8_t*>(up_lds);                     // [TG][kUpRow]
+  float* xs_t = reinterpret_cast<float*>(up_lds + TG * kUpRow);           // [NSTG][TG] (token fastest)
+  float* ws_l = xs_t + TG * NSTG;                                         // [2I/128][NSTG]
   int* slots = reinterpret_cast<int*>(ws_l + (2 * I / 128) * NSTG);       // [kMaxM]
   int* wtot = slots + kMaxM;                                              // [4]
   const int unit = blockIdx.x / kUpGroups, grp = blockIdx.x % kUpGroups;
@@ -552,14 +558,21 @@ __global__ __launch_bounds__(256) void moe_up_kernel(MoeDev d) {
   const int ng = ch * 16 + lr;
   // weights in fragment order: 16-row tile t, stage s at (t * NSTG + s) * 2048, the lane's two
   // 16-byte halves at 16 lane and 1024 + 16 lane (one 1 KB contiguous load per half per wave)
-  const uint8_t* bg = W + ((size_t)ch * NSTG << 11) + lane * 16;
-  const uint8_t* bu = W + ((size_t)(I / 16 + ch) * NSTG << 11) + lane * 16;
+  // Buffer loads: the stage offset goes in the scalar offset, so the unrolled stages share one
+  // address register (global loads would need a 64-bit address per stage: the 2 KB steps
+  // overflow their immediate offset).
+  const int chu = __builtin_amdgcn_readfirstlane(ch);
+  const __amdgpu_buffer_rsrc_t grs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(W + ((size_t)chu * NSTG << 11)), (short)0, NSTG << 11, 0x00020000);
+  const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W + ((size_t)(I / 16 + chu) * NSTG << 11)), (short)0, NSTG << 11, 0x00020000);
+  const int lo = lane * 16;
   v4i Bq[kUpD][4];
   auto issue = [&](int s, int q) {
-    Bq[q][0] = ldg16_nt(bg + s * 2048);
-    Bq[q][1] = ldg16_nt(bg + s * 2048 + 1024);
-    Bq[q][2] = ldg16_nt(bu + s * 2048);
-    Bq[q][3] = ldg16_nt(bu + s * 2048 + 1024);
+    Bq[q][0] = __builtin_amdgcn_raw_buffer_load_b128(grs, lo, s * 2048, 2);
+    Bq[q][1] = __builtin_amdgcn_raw_buffer_load_b128(grs, lo, s * 2048 + 1024, 2);
+    Bq[q][2] = __builtin_amdgcn_raw_buffer_load_b128(urs, lo, s * 2048, 2);
+    Bq[q][3] = __builtin_amdgcn_raw_buffer_load_b128(urs, lo, s * 2048 + 1024, 2);
   };
 #pragma unroll
   for (int s = 0; s < kUpD; ++s) issue(s, s);  // the first weight stages, before the token list
@@ -568,87 +581,86 @@ __global__ __launch_bounds__(256) void moe_up_kernel(MoeDev d) {
   if (cnt == 0) return;
   if constexpr (DT == Q36_MOE_FP8)
     for (int i = tid; i < (2 * I / 128) * NSTG; i += 256) ws_l[i] = S[i];
-  using Acc = typename std::conditional<DT == Q36_MOE_FP8, v4f, v4i>::type;
-  for (int g0 = 0; g0 < cnt; g0 += 64) {
-    const int nt = min(NT, (cnt - g0 + 15) / 16);
-    if (g0 > 0) {
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)d.xq, (short)0, d.M * H, 0x00020000);
+  const int n = ch * 16 + lr;
+  // One group of up to TG tokens with NTT 16-token tiles (rows past the group's tokens are zero):
+  // per 128-byte stage every fragment and scale read first, then the independent MFMAs, then the
+  // scaled adds (e4m3: block terms added in block order from zero), then SwiGLU -> h per slot.
+  auto group = [&](int g0, auto nttc) {
+    constexpr int NTT = decltype(nttc)::value;
+    using Acc = typename std::conditional<DT == Q36_MOE_FP8, v4f, v4i>::type;
+    Acc ag[NTT], au[NTT];
 #pragma unroll
-      for (int s = 0; s < kUpD; ++s) issue(s, s);
-    }
-    for (int i = tid; i < 64 * NSTG; i += 256) {
-      const int ti = g0 + i / NSTG;
-      if constexpr (DT == Q36_MOE_FP8)
-        xs_l[i] = ti < cnt ? d.xs[(size_t)slot_token(d, slots[ti]) * NSTG + i % NSTG] : 0.f;
-      else
-        xs_l[i] = (ti < cnt && i % NSTG == 0) ? d.xs[slot_token(d, slots[ti])] : 0.f;
-    }
-    Acc ag[NT], au[NT];
-#pragma unroll
-    for (int tt = 0; tt < NT; ++tt) {
+    for (int tt = 0; tt < NTT; ++tt) {
       ag[tt] = Acc{0, 0, 0, 0};
       au[tt] = Acc{0, 0, 0, 0};
     }
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      // this half's activation rows into LDS: thread -> (row tid/4, 256 bytes at 256 (tid%4))
+      // this half's activation rows into LDS by buffer DMA: wave w copies rows w, w + 4, ...,
+      // 1 KB each (lane l: bytes 16 l .. of the row); rows past the group read as zero
       __syncthreads();
-      {
-        const int rr = tid >> 2, seg = tid & 3;
+      for (int rr = wave; rr < 16 * NTT; rr += 4) {
         const int ti = g0 + rr;
-        const bool ok = ti < cnt && rr < 16 * nt;
-        const uint8_t* src = d.xq + (size_t)slot_token(d, slots[ok ? ti : 0]) * H + half * kUpKH + seg * 256;
-        v4i v[16];
-#pragma unroll
-        for (int c = 0; c < 16; ++c) v[c] = ok ? ldg16(src + 16 * c) : v4i{0, 0, 0, 0};
-#pragma unroll
-        for (int c = 0; c < 16; ++c) *reinterpret_cast<v4i*>(a_l + rr * kUpRow + seg * 256 + 16 * c) = v[c];
+        const int voff = ti < cnt ? slot_token(d, slots[ti]) * H + half * kUpKH + lane * 16 : d.M * H;
+        dma16(xrs, a_l + rr * kUpRow, voff);
       }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      asm volatile("" ::: "memory");
 #pragma unroll
       for (int sh = 0; sh < NSTG / 2; ++sh) {
         const int s = half * (NSTG / 2) + sh;
         const int q = s % kUpD;
+        v4i a[NTT][2];
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-          if (tt < nt) {
-            const uint8_t* ap = a_l + (tt * 16 + lr) * kUpRow + sh * 128 + lgp * 32;
-            const v4i a0 = *reinterpret_cast<const v4i*>(ap);
-            const v4i a1 = *reinterpret_cast<const v4i*>(ap + 16);
-            if constexpr (DT == Q36_MOE_FP8) {
-              const v8i a8 = cat8(a0, a1);
-              const v4f rg = mfma_fp8(a8, cat8(Bq[q][0], Bq[q][1]));
-              const v4f ru = mfma_fp8(a8, cat8(Bq[q][2], Bq[q][3]));
-              const float wg = ws_l[(ng / 128) * NSTG + s], wu = ws_l[((I + ng) / 128) * NSTG + s];
+        for (int tt = 0; tt < NTT; ++tt) {
+          const uint8_t* ap = a_l + (tt * 16 + lr) * kUpRow + sh * 128 + lgp * 32;
+          a[tt][0] = *reinterpret_cast<const v4i*>(ap);
+          a[tt][1] = *reinterpret_cast<const v4i*>(ap + 16);
+        }
+        if constexpr (DT == Q36_MOE_FP8) {
+          const float wg = ws_l[(ng / 128) * NSTG + s], wu = ws_l[((I + ng) / 128) * NSTG + s];
+          const v8i bgq = cat8(Bq[q][0], Bq[q][1]), buq = cat8(Bq[q][2], Bq[q][3]);
 #pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                const float xsr = xs_l[(tt * 16 + 4 * lgp + r) * NSTG + s];
-                float g = ag[tt][r] + (rg[r] * xsr) * wg;
-                float u = au[tt][r] + (ru[r] * xsr) * wu;
-                // pin the running sums here: left alone, the compiler sinks the whole chain below
-                // the loop and keeps every stage's MFMA result live
-                asm volatile("" : "+v"(g), "+v"(u));
-                ag[tt][r] = g;
-                au[tt][r] = u;
-              }
-            } else {
-              ag[tt] = mfma_i8(a0, Bq[q][0], ag[tt]);
-              ag[tt] = mfma_i8(a1, Bq[q][1], ag[tt]);
-              au[tt] = mfma_i8(a0, Bq[q][2], au[tt]);
-              au[tt] = mfma_i8(a1, Bq[q][3], au[tt]);
+          for (int tt = 0; tt < NTT; ++tt) {
+            const v8i a8 = cat8(a[tt][0], a[tt][1]);
+            const v4f rg = mfma_fp8(a8, bgq);
+            const v4f ru = mfma_fp8(a8, buq);
+            const float4 xsv = *reinterpret_cast<const float4*>(xs_t + s * TG + tt * 16 + 4 * lgp);
+            const float xr[4] = {xsv.x, xsv.y, xsv.z, xsv.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              ag[tt][r] = ag[tt][r] + (rg[r] * xr[r]) * wg;
+              au[tt][r] = au[tt][r] + (ru[r] * xr[r]) * wu;
             }
+          }
+          // the running sums are formed here (left alone, the compiler sinks the chain below the
+          // stage loop and keeps every stage's MFMA results live)
+#pragma unroll
+          for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(ag[tt][r]), "+v"(au[tt][r]));
+        } else {
+#pragma unroll
+          for (int tt = 0; tt < NTT; ++tt) {
+            ag[tt] = mfma_i8(a[tt][0], Bq[q][0], ag[tt]);
+            ag[tt] = mfma_i8(a[tt][1], Bq[q][1], ag[tt]);
+            au[tt] = mfma_i8(a[tt][0], Bq[q][2], au[tt]);
+            au[tt] = mfma_i8(a[tt][1], Bq[q][3], au[tt]);
           }
         }
         if (s + kUpD < NSTG) issue(s + kUpD, q);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    const int n = ch * 16 + lr;
 #pragma unroll
-    for (int tt = 0; tt < NT; ++tt)
+    for (int tt = 0; tt < NTT; ++tt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int ti = g0 + tt * 16 + 4 * lgp + r;
-        if (tt < nt && ti < cnt) {
+        if (ti < cnt) {
           const int s = slots[ti];
           float g, u;
           if constexpr (DT == Q36_MOE_FP8) {
@@ -659,7 +671,7 @@ __global__ __launch_bounds__(256) void moe_up_kernel(MoeDev d) {
               d.dbg_acc13[(size_t)s * 2 * I + n] = ag[tt][r];
               d.dbg_acc13[(size_t)s * 2 * I + I + n] = au[tt][r];
             }
-            const float xsc = xs_l[(tt * 16 + 4 * lgp + r) * NSTG];
+            const float xsc = xs_t[tt * 16 + 4 * lgp + r];
             g = ((float)ag[tt][r] * xsc) * S[n];
             u = ((float)au[tt][r] * xsc) * S[I + n];
           }
@@ -670,6 +682,27 @@ __global__ __launch_bounds__(256) void moe_up_kernel(MoeDev d) {
           if (d.dbg_h) d.dbg_h[(size_t)s * I + n] = (uint16_t)hb;
         }
       }
+  };
+  for (int g0 = 0; g0 < cnt; g0 += TG) {
+    const int nt = min(TG / 16, (cnt - g0 + 15) / 16);
+    if (g0 > 0) {
+#pragma unroll
+      for (int s = 0; s < kUpD; ++s) issue(s, s);
+      __syncthreads();  // the previous group's epilogue has read xs_t
+    }
+    for (int i = tid; i < TG * NSTG; i += 256) {
+      const int ti = g0 + i % TG, s = i / TG;
+      if constexpr (DT == Q36_MOE_FP8)
+        xs_t[i] = ti < cnt ? d.xs[(size_t)slot_token(d, slots[ti]) * NSTG + s] : 0.f;
+      else
+        xs_t[i] = (ti < cnt && s == 0) ? d.xs[slot_token(d, slots[ti])] : 0.f;
+    }
+    // two tile counts: one tile (most experts at decode sizes) or four (rows past the tokens are
+    // zero); a third instance would cost registers in all of them
+    if (nt == 1)
+      group(g0, std::integral_constant<int, 1>{});
+    else
+      group(g0, std::integral_constant<int, 4>{});
   }
 }
 constexpr size_t kUpLds = 64 * kUpRow + sizeof(float) * (64 * (kMoeH / 128) + (2 * kMoeI / 128) * (kMoeH / 128)) +
