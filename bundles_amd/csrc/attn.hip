@@ -79,8 +79,8 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* x, const
 }
 
 // ------------------------------------------------------------------------------------------
-// skinny e4m3 GEMM:  Y[t, n] = bf16(sum over the 128-blocks kb, in order, of (blocksum_kb(t, n) *
-// xs[t, kb]) * ws[n / 128, kb]).
+// skinny e4m3 GEMM:  Y[t, n] = bf16(acc), acc = fma(blocksum_kb(t, n), xs[t, kb] * ws[n / 128, kb], acc)
+// over the 128-blocks kb in increasing order from zero.
 // Both operands are stored in MFMA fragment order: for a 16-row tile and a 128-block, 2 KB holding
 // half h (16 bytes) of lane l's operand at h * 1024 + 16 l, so that a wave reads a fragment with two
 // 1 KB contiguous loads (row-major rows are K bytes apart: a lane-per-row load is 64 separate
@@ -161,10 +161,10 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmDev g) {
     for (int r = 0; r < RT; ++r)
 #pragma unroll
       for (int tt = 0; tt < TPW; ++tt) {
-        acc[r][tt][0] = acc[r][tt][0] + (rr[r][tt][0] * st.sc[tt].x) * st.ws;
-        acc[r][tt][1] = acc[r][tt][1] + (rr[r][tt][1] * st.sc[tt].y) * st.ws;
-        acc[r][tt][2] = acc[r][tt][2] + (rr[r][tt][2] * st.sc[tt].z) * st.ws;
-        acc[r][tt][3] = acc[r][tt][3] + (rr[r][tt][3] * st.sc[tt].w) * st.ws;
+        acc[r][tt][0] = __builtin_fmaf(rr[r][tt][0], st.sc[tt].x * st.ws, acc[r][tt][0]);
+        acc[r][tt][1] = __builtin_fmaf(rr[r][tt][1], st.sc[tt].y * st.ws, acc[r][tt][1]);
+        acc[r][tt][2] = __builtin_fmaf(rr[r][tt][2], st.sc[tt].z * st.ws, acc[r][tt][2]);
+        acc[r][tt][3] = __builtin_fmaf(rr[r][tt][3], st.sc[tt].w * st.ws, acc[r][tt][3]);
       }
     // the sums are formed here (left alone, the compiler sinks them below the K loop and keeps
     // every MFMA result live)

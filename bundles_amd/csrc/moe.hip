@@ -525,8 +525,8 @@ constexpr int kMoeH = 2048, kMoeI = 512;
 // its row (row = lane % 16, bytes 32 (lane / 16) of the 128-byte stage) of both operands -- one e4m3 16x16x128 MFMA, or two int8 16x16x64 MFMAs on the two 16-byte
 // halves (their K pairing is the same for src0 and src1, so the int32 sums are exact).  The
 // 16x16 result gives lane l weight row l%16 and token rows 4(l/16)+r; SwiGLU happens in the
-// lane.  For e4m3 the block terms (block sum * xs * ws) are added in increasing block order from
-// zero, the order of the block dequant sum.
+// lane.  For e4m3 the block sums are accumulated as acc = fma(block sum, xs * ws, acc) in
+// increasing block order from zero.
 constexpr int kUpD = 4;                    // weight stages in flight per wave
 constexpr int kUpKH = kMoeH / 2;           // K bytes per LDS activation half
 constexpr int kUpRow = kUpKH + 16;         // padded LDS row (spreads the 16 rows over the banks)
@@ -586,7 +586,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int n = ch * 16 + lr;
   // One group of up to TG tokens with NTT 16-token tiles (rows past the group's tokens are zero):
   // per 128-byte stage every fragment and scale read first, then the independent MFMAs, then the
-  // scaled adds (e4m3: block terms added in block order from zero), then SwiGLU -> h per slot.
+  // scaled accumulates (e4m3: in block order from zero), then SwiGLU -> h per slot.
   auto group = [&](int g0, auto nttc) {
     constexpr int NTT = decltype(nttc)::value;
     using Acc = typename std::conditional<DT == Q36_MOE_FP8, v4f, v4i>::type;
@@ -632,8 +632,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const float xr[4] = {xsv.x, xsv.y, xsv.z, xsv.w};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              ag[tt][r] = ag[tt][r] + (rg[r] * xr[r]) * wg;
-              au[tt][r] = au[tt][r] + (ru[r] * xr[r]) * wu;
+              ag[tt][r] = __builtin_fmaf(rg[r], xr[r] * wg, ag[tt][r]);
+              au[tt][r] = __builtin_fmaf(ru[r], xr[r] * wu, au[tt][r]);
             }
           }
           // the running sums are formed here (left alone, the compiler sinks the chain below the
@@ -711,19 +711,29 @@ constexpr size_t kUpLds = 64 * kUpRow + sizeof(float) * (64 * (kMoeH / 128) + (2
 // ------------------------------------------------------------------------------------------
 // 4. down GEMM x routing weight
 // ------------------------------------------------------------------------------------------
-// Workgroup = (unit, group of 4 x 32 output rows); each wave owns 32 rows (two 16-row MFMA
-// column tiles) over the whole K = I (4 stages of 128 bytes), loaded before the token scan.  Per
-// 16-token tile the workgroup quantizes the tile's h rows once into LDS (e4m3 per 128-group,
-// int8 per row) and every wave reads its MFMA operand from there.
-constexpr int kDnRows = 32;
+// Workgroup = (unit, group of 4 x 64 output rows); each wave owns 64 rows (four 16-row MFMA
+// tiles) over the whole K = I (4 stages of 128 bytes): 32 KB of weights per wave, loaded into
+// registers before the token list, so the grid (8 workgroups per active unit, two per CU) streams
+// the down weights in a single round.  Tokens go in groups of up to 64 (one or four 16-token
+// tiles): the workgroup loads every h row of the group, and the routing weight of every slot, in
+// one go, quantizes the rows into LDS (e4m3 per 128-group, int8 per row), and every wave reads its
+// MFMA operands from there.  The weights are the MFMA's first operand, so lane l ends with token
+// l%16 and four consecutive output columns 4(l/16) .. +3: one 8-byte store per tile.  The weight
+// tiles go in pairs, so one pair's accumulators and one stage's operands stay in registers.
+constexpr int kDnRows = 64;
+constexpr int kDnCT = kDnRows / 16;
 constexpr int kDnGroups = kMoeH / (4 * kDnRows);
+constexpr int kDnTG = 64;
+constexpr int kDnRow = kMoeI + 16;  // padded LDS row: 16 rows' 16-byte reads hit distinct banks
 template <int DT>
-__global__ __launch_bounds__(256) void moe_down_kernel(MoeDev d) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void moe_down_kernel(MoeDev d) {
   constexpr int H = kMoeH, I = kMoeI, NSTG = I / 128;
   __shared__ int slots[kMaxM];
   __shared__ int wtot[4];
-  __shared__ __align__(16) uint8_t hq[16][I];
-  __shared__ float hs[16][NSTG];
+  __shared__ __align__(16) uint8_t hq[kDnTG * kDnRow];
+  __shared__ float hs[kDnTG][NSTG];      // activation scales per row (e4m3: per 128-group)
+  __shared__ float wl[kDnTG];            // routing weight per row of the group
+  __shared__ __align__(16) float sn[4 * kDnRows];  // int8 weight scale per output row of the workgroup
   const int unit = blockIdx.x / kDnGroups, grp = blockIdx.x % kDnGroups;
   const bool shared = unit == 0;
   if (!shared && unit - 1 >= d.ctl[2]) return;
@@ -732,119 +742,168 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeDev d) {
   const uint8_t* W = shared ? d.sw2 : d.w2 + (size_t)e * H * I;
   const float* S =
       shared ? d.ss2 : d.s2 + (DT == Q36_MOE_FP8 ? (size_t)e * (H / 128) * NSTG : (size_t)e * H);
-  const int n0 = (grp * 4 + wave) * kDnRows;
-  v4i B[2][NSTG][2];
+  const int n0 = __builtin_amdgcn_readfirstlane((grp * 4 + wave) * kDnRows);  // wave-uniform
+  // weights in fragment order, loaded through one buffer resource per wave with the tile and
+  // stage offsets in the scalar offset (one address register for all 32 loads)
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W + ((size_t)(n0 >> 4) * NSTG << 11)), (short)0, kDnCT * NSTG << 11, 0x00020000);
+  v4i B[kDnCT][NSTG][2];
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
+  for (int ct = 0; ct < kDnCT; ++ct)
 #pragma unroll
     for (int s = 0; s < NSTG; ++s) {
-      const uint8_t* src = W + ((size_t)((n0 >> 4) + ct) * NSTG << 11) + (s << 11) + lane * 16;  // fragment order
-      B[ct][s][0] = ldg16_nt(src);
-      B[ct][s][1] = ldg16_nt(src + 1024);
+      B[ct][s][0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, (ct * NSTG + s) << 11, 2);
+      B[ct][s][1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, ((ct * NSTG + s) << 11) + 1024, 2);
     }
   int e_chk;
   const int cnt = unit_slots(d, unit, slots, wtot, &e_chk);
   if (cnt == 0) return;
-  float wsc[2][NSTG];
+  // weight scales: e4m3 per 128x128 block (the wave's 64 rows sit in one block row), int8 per row
+  float wsc[NSTG];
   if constexpr (DT == Q36_MOE_FP8) {
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int s = 0; s < NSTG; ++s) wsc[ct][s] = S[(size_t)((n0 + ct * 16) / 128) * NSTG + s];
+    for (int s = 0; s < NSTG; ++s) wsc[s] = S[(size_t)(n0 / 128) * NSTG + s];
+  } else {
+    sn[tid] = S[grp * 4 * kDnRows + tid];
   }
-  for (int t0 = 0; t0 < cnt; t0 += 16) {
+  auto group = [&](int g0, auto nttc) {
+    constexpr int NTT = decltype(nttc)::value;
     {
-      // quantize the tile: thread -> (row tid/16, values 32 (tid%16) .. +31); a 128-group is
-      // four neighbouring threads, a row sixteen
+      // load: thread -> rows tid/16 + 16 j (j < NTT), values 32 (tid%16) .. +31 of each; a
+      // 128-group is four neighbouring threads, a row sixteen
       const int tr = tid >> 4, q16 = tid & 15;
-      const bool ok = t0 + tr < cnt;
-      const uint8_t* src = reinterpret_cast<const uint8_t*>(d.h + (size_t)slots[ok ? t0 + tr : 0] * I) + q16 * 64;
-      v4i raw[4];
+      v4i raw[NTT][4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) raw[v] = ldg16(src + 16 * v);
-      float hv[32];
+      for (int j = 0; j < NTT; ++j) {
+        const int ti = g0 + tr + 16 * j;
+        const bool ok = ti < cnt;
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(d.h + (size_t)slots[ok ? ti : g0] * I) + q16 * 64;
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          hv[8 * v + 2 * q] = ok ? bf_lo((uint32_t)raw[v][q]) : 0.f;
-          hv[8 * v + 2 * q + 1] = ok ? bf_hi((uint32_t)raw[v][q]) : 0.f;
-        }
-      float m = 0.f;
-#pragma unroll
-      for (int v = 0; v < 32; ++v) m = fmaxf(m, fabsf(hv[v]));
-      uint32_t wd[8];
-      if constexpr (DT == Q36_MOE_FP8) {
-        m = fmaxf(m, __shfl_xor(m, 1));
-        m = fmaxf(m, __shfl_xor(m, 2));
-        const float inv = m > 0.f ? 448.f / m : 0.f;
-#pragma unroll
-        for (int v = 0; v < 8; ++v)
-          wd[v] = f2e4m3x2_hw(hv[4 * v] * inv, hv[4 * v + 1] * inv) |
-                  (f2e4m3x2_hw(hv[4 * v + 2] * inv, hv[4 * v + 3] * inv) << 16);
-        if ((q16 & 3) == 0) hs[tr][q16 >> 2] = m / 448.f;
-      } else {
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-        const float sc = m / 127.f, safe = m > 0.f ? sc : 1.f;
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          wd[v] = 0u;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) wd[v] |= ((uint32_t)round_i8(hv[4 * v + q] / safe) & 0xffu) << (8 * q);
-        }
-        if (q16 == 0) hs[tr][0] = sc;
+        for (int v = 0; v < 4; ++v) raw[j][v] = ok ? ldg16(src + 16 * v) : v4i{0, 0, 0, 0};
       }
-      uint4* dst = reinterpret_cast<uint4*>(&hq[tr][q16 * 32]);
-      dst[0] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
-      dst[1] = make_uint4(wd[4], wd[5], wd[6], wd[7]);
+      float wv = 0.f;
+      if (tid < 16 * NTT && g0 + tid < cnt) wv = shared ? 1.f : d.wts[slots[g0 + tid]];
+#pragma unroll
+      for (int j = 0; j < NTT; ++j) {
+        const int row = tr + 16 * j;
+        auto hval = [&](int i) {  // value i (0..31) of the thread's 32 in row j
+          const uint32_t w = (uint32_t)raw[j][i >> 3][(i >> 1) & 3];
+          return (i & 1) ? bf_hi(w) : bf_lo(w);
+        };
+        float m = 0.f;
+#pragma unroll
+        for (int v = 0; v < 32; ++v) m = fmaxf(m, fabsf(hval(v)));
+        uint32_t wd[8];
+        if constexpr (DT == Q36_MOE_FP8) {
+          m = fmaxf(m, __shfl_xor(m, 1));
+          m = fmaxf(m, __shfl_xor(m, 2));
+          const float inv = m > 0.f ? 448.f / m : 0.f;
+#pragma unroll
+          for (int v = 0; v < 8; ++v)
+            wd[v] = f2e4m3x2_hw(hval(4 * v) * inv, hval(4 * v + 1) * inv) |
+                    (f2e4m3x2_hw(hval(4 * v + 2) * inv, hval(4 * v + 3) * inv) << 16);
+          if ((q16 & 3) == 0) hs[row][q16 >> 2] = m / 448.f;
+        } else {
+#pragma unroll
+          for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+          const float sc = m / 127.f, safe = m > 0.f ? sc : 1.f;
+#pragma unroll
+          for (int v = 0; v < 8; ++v) {
+            wd[v] = 0u;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) wd[v] |= ((uint32_t)round_i8(hval(4 * v + q) / safe) & 0xffu) << (8 * q);
+          }
+          if (q16 == 0) hs[row][0] = sc;
+        }
+        uint4* dst = reinterpret_cast<uint4*>(&hq[row * kDnRow + q16 * 32]);
+        dst[0] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        dst[1] = make_uint4(wd[4], wd[5], wd[6], wd[7]);
+      }
+      if (tid < 16 * NTT) wl[tid] = wv;
     }
     __syncthreads();
-    v4i A[NSTG][2];
 #pragma unroll
-    for (int s = 0; s < NSTG; ++s) {
-      A[s][0] = *reinterpret_cast<const v4i*>(&hq[lr][s * 128 + lgp * 32]);
-      A[s][1] = *reinterpret_cast<const v4i*>(&hq[lr][s * 128 + lgp * 32 + 16]);
-    }
+    for (int cp = 0; cp < kDnCT; cp += 2) {
+      using Acc = typename std::conditional<DT == Q36_MOE_FP8, v4f, v4i>::type;
+      Acc acc[2][NTT];
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const int n = n0 + ct * 16 + lr;
-      float yv[4];
-      if constexpr (DT == Q36_MOE_FP8) {
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int s = 0; s < NSTG; ++s) {
-          const v4f rr = mfma_fp8(cat8(A[s][0], A[s][1]), cat8(B[ct][s][0], B[ct][s][1]));
+        for (int tt = 0; tt < NTT; ++tt) acc[c][tt] = Acc{0, 0, 0, 0};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[r] = acc[r] + (rr[r] * hs[4 * lgp + r][s]) * wsc[ct][s];
+      for (int s = 0; s < NSTG; ++s) {
+        v4i a[NTT][2];
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt) {
+          const uint8_t* ap = &hq[(tt * 16 + lr) * kDnRow + s * 128 + lgp * 32];
+          a[tt][0] = *reinterpret_cast<const v4i*>(ap);
+          a[tt][1] = *reinterpret_cast<const v4i*>(ap + 16);
         }
+        if constexpr (DT == Q36_MOE_FP8) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) yv[r] = acc[r];
-      } else {
-        v4i acc = {0, 0, 0, 0};
+          for (int tt = 0; tt < NTT; ++tt) {
+            const float xw = hs[tt * 16 + lr][s] * wsc[s];  // this lane's token
+            const v8i a8 = cat8(a[tt][0], a[tt][1]);
 #pragma unroll
-        for (int s = 0; s < NSTG; ++s) {
-          acc = mfma_i8(A[s][0], B[ct][s][0], acc);
-          acc = mfma_i8(A[s][1], B[ct][s][1], acc);
+            for (int c = 0; c < 2; ++c) {
+              const v4f rr = mfma_fp8(cat8(B[cp + c][s][0], B[cp + c][s][1]), a8);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[c][tt][r] = __builtin_fmaf(rr[r], xw, acc[c][tt][r]);
+            }
+          }
+          // the running sums are formed per stage (left alone, the compiler sinks the chain and
+          // keeps every stage's MFMA results live)
+#pragma unroll
+          for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(acc[c][tt][r]));
+        } else {
+#pragma unroll
+          for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+              acc[c][tt] = mfma_i8(B[cp + c][s][0], a[tt][0], acc[c][tt]);
+              acc[c][tt] = mfma_i8(B[cp + c][s][1], a[tt][1], acc[c][tt]);
+            }
         }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // lane: token tt*16 + l%16, output columns n .. n+3
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int ti2 = t0 + 4 * lgp + r;
-          if (ti2 < cnt && d.dbg_acc2) d.dbg_acc2[(size_t)slots[ti2] * H + n] = acc[r];
-          yv[r] = ((float)acc[r] * hs[4 * lgp + r][0]) * S[n];
+      for (int tt = 0; tt < NTT; ++tt) {
+        const int row = tt * 16 + lr, ti = g0 + row;
+        if (ti < cnt) {
+          const int sl = slots[ti];
+          const float wt = wl[row];
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const int nl = wave * kDnRows + (cp + c) * 16 + 4 * lgp;  // column within the workgroup
+            const int n = grp * 4 * kDnRows + nl;
+            float yv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if constexpr (DT == Q36_MOE_FP8) {
+                yv[r] = acc[c][tt][r];
+              } else {
+                if (d.dbg_acc2) d.dbg_acc2[(size_t)sl * H + n + r] = acc[c][tt][r];
+                yv[r] = ((float)acc[c][tt][r] * hs[row][0]) * sn[nl + r];
+              }
+            }
+            *reinterpret_cast<uint2*>(&d.y[(size_t)sl * H + n]) =
+                make_uint2(pack_bf2(yv[0] * wt, yv[1] * wt), pack_bf2(yv[2] * wt, yv[3] * wt));
+          }
         }
       }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int ti2 = t0 + 4 * lgp + r;
-        if (ti2 < cnt) {
-          const int s = slots[ti2];
-          const float wt = shared ? 1.f : d.wts[s];
-          d.y[(size_t)s * H + n] = (uint16_t)f2bf(yv[r] * wt);
-        }
-      }
     }
-    __syncthreads();
+  };
+  for (int g0 = 0; g0 < cnt; g0 += kDnTG) {
+    if (g0 > 0) __syncthreads();  // the previous group's operand reads are done
+    if (cnt - g0 <= 16)
+      group(g0, std::integral_constant<int, 1>{});
+    else
+      group(g0, std::integral_constant<int, 4>{});
   }
 }
 

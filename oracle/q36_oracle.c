@@ -258,8 +258,9 @@ int q36o_route(const uint16_t* x, const uint16_t* wr, const float* bias, const i
  * mode 0: exact int32 sum (L/qk_moe_prefill_i8.cu:3646-3654 up_w8a8; H/w8a8.py:39-75).
  * mode 1: e4m3 128-blocks; each block sum of e4m3 x e4m3 products is formed exactly (double
  * holds it: products span 2^-18 .. 2^17.6, a 128-term sum needs < 44 bits), rounded once to
- * fp32, then acc += (bsum * xs[kb]) * ws[kb] in increasing kb (the DeepSeek-style block dequant
- * the configuration asks for; no reference counterpart). */
+ * fp32, then acc = fma(bsum, xs[kb] * ws[kb], acc) in increasing kb from zero (the block dequant
+ * of DeepSeek-style fp8 GEMMs, accumulator += partial * (scale_a * scale_b); the configuration asks
+ * for it and the reference has no counterpart). */
 static const float* g_e4m3_lut(void) {
   static float lut[256];
   static int init = 0;
@@ -281,7 +282,7 @@ static float fp8_row_dot(const uint8_t* xq, const float* xs, const uint8_t* wq, 
   for (int kb = 0; kb < K / 128; ++kb) {
     double bs = 0.0;
     for (int i = 0; i < 128; ++i) bs += (double)lut[xq[kb * 128 + i]] * (double)lut[wq[kb * 128 + i]];
-    acc = acc + ((float)bs * xs[kb]) * ws[kb];
+    acc = fmaf((float)bs, xs[kb] * ws[kb], acc);
   }
   return acc;
 }
@@ -580,8 +581,9 @@ int q36o_gdn_verify(const q36o_gdn_args* a) {
 /* attention projections                                                                */
 /* ------------------------------------------------------------------------------------ */
 
-/* y[t, n] = sum over 128-blocks of the e4m3 block dot (exact, rounded once) * xs * ws, the same
- * block rule as the fp8 experts; the result is rounded to bf16 (the projection's output dtype). */
+/* y[t, n] = the e4m3 block dots (exact, rounded once) accumulated as fma(dot, xs * ws, acc) over
+ * the 128-blocks in order, the same block rule as the fp8 experts; the result is rounded to bf16
+ * (the projection's output dtype). */
 static void fp8_linear(const uint8_t* xq, const float* xs, int T, const uint8_t* w, const float* s, int N,
                        int K, float* y) {
 #pragma omp parallel for collapse(2) schedule(static)
