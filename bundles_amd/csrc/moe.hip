@@ -713,7 +713,7 @@ constexpr size_t kUpLds = 64 * kUpRow + sizeof(float) * (64 * (kMoeH / 128) + (2
 // ------------------------------------------------------------------------------------------
 // Workgroup = (unit, group of 4 x 64 output rows); each wave owns 64 rows (four 16-row MFMA
 // tiles) over the whole K = I (4 stages of 128 bytes): 32 KB of weights per wave, loaded into
-// registers before the token list, so the grid (8 workgroups per active unit, two per CU) streams
+// registers right after the first group's h rows, so the grid (8 workgroups per active unit, two per CU) streams
 // the down weights in a single round.  Tokens go in groups of up to 64 (one or four 16-token
 // tiles): the workgroup loads every h row of the group, and the routing weight of every slot, in
 // one go, quantizes the rows into LDS (e4m3 per 128-group, int8 per row), and every wave reads its
@@ -748,41 +748,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W + ((size_t)(n0 >> 4) * NSTG << 11)), (short)0, kDnCT * NSTG << 11, 0x00020000);
   v4i B[kDnCT][NSTG][2];
+  auto issue_weights = [&]() {
 #pragma unroll
-  for (int ct = 0; ct < kDnCT; ++ct)
+    for (int ct = 0; ct < kDnCT; ++ct)
 #pragma unroll
-    for (int s = 0; s < NSTG; ++s) {
-      B[ct][s][0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, (ct * NSTG + s) << 11, 2);
-      B[ct][s][1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, ((ct * NSTG + s) << 11) + 1024, 2);
-    }
+      for (int s = 0; s < NSTG; ++s) {
+        B[ct][s][0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, (ct * NSTG + s) << 11, 2);
+        B[ct][s][1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, ((ct * NSTG + s) << 11) + 1024, 2);
+      }
+  };
+  // the token list comes first: the first group's h rows are loaded before the weights, so their
+  // quantization overlaps the weight stream (vector loads complete in issue order)
   int e_chk;
   const int cnt = unit_slots(d, unit, slots, wtot, &e_chk);
   if (cnt == 0) return;
   // weight scales: e4m3 per 128x128 block (the wave's 64 rows sit in one block row), int8 per row
-  float wsc[NSTG];
+  float wsc[NSTG], snv = 0.f;
   if constexpr (DT == Q36_MOE_FP8) {
 #pragma unroll
     for (int s = 0; s < NSTG; ++s) wsc[s] = S[(size_t)(n0 / 128) * NSTG + s];
   } else {
-    sn[tid] = S[grp * 4 * kDnRows + tid];
+    snv = S[grp * 4 * kDnRows + tid];
   }
-  auto group = [&](int g0, auto nttc) {
+  const int hbytes = (d.M * d.k + d.M) * I * 2, tbytes = d.M * d.k * 4;
+  const __amdgpu_buffer_rsrc_t hrs = __builtin_amdgcn_make_buffer_rsrc((void*)d.h, (short)0, hbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc((void*)d.wts, (short)0, tbytes, 0x00020000);
+  auto group = [&](int g0, auto nttc, auto firstc) {
     constexpr int NTT = decltype(nttc)::value;
+    constexpr bool FIRST = decltype(firstc)::value;
     {
       // load: thread -> rows tid/16 + 16 j (j < NTT), values 32 (tid%16) .. +31 of each; a
       // 128-group is four neighbouring threads, a row sixteen
+      // (buffer loads: rows past the tokens read as zero without a branch, which would make the
+      // compiler wait for each load at the join)
       const int tr = tid >> 4, q16 = tid & 15;
       v4i raw[NTT][4];
 #pragma unroll
       for (int j = 0; j < NTT; ++j) {
         const int ti = g0 + tr + 16 * j;
-        const bool ok = ti < cnt;
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(d.h + (size_t)slots[ok ? ti : g0] * I) + q16 * 64;
+        const int voff = ti < cnt ? slots[ti] * (I * 2) + q16 * 64 : hbytes;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) raw[j][v] = ok ? ldg16(src + 16 * v) : v4i{0, 0, 0, 0};
+        for (int v = 0; v < 4; ++v) raw[j][v] = __builtin_amdgcn_raw_buffer_load_b128(hrs, voff + 16 * v, 0, 0);
       }
-      float wv = 0.f;
-      if (tid < 16 * NTT && g0 + tid < cnt) wv = shared ? 1.f : d.wts[slots[g0 + tid]];
+      const bool wok = tid < 16 * NTT && g0 + tid < cnt;
+      float wv = wok ? 1.f : 0.f;
+      if (!shared)
+        wv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(trs, wok ? slots[g0 + tid] * 4 : tbytes, 0, 0));
+      if constexpr (FIRST) {
+        issue_weights();
+        if constexpr (DT != Q36_MOE_FP8) sn[tid] = snv;
+      }
 #pragma unroll
       for (int j = 0; j < NTT; ++j) {
         const int row = tr + 16 * j;
@@ -898,12 +913,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   };
-  for (int g0 = 0; g0 < cnt; g0 += kDnTG) {
-    if (g0 > 0) __syncthreads();  // the previous group's operand reads are done
-    if (cnt - g0 <= 16)
-      group(g0, std::integral_constant<int, 1>{});
-    else
-      group(g0, std::integral_constant<int, 4>{});
+  if (cnt <= 16) {
+    group(0, std::integral_constant<int, 1>{}, std::true_type{});
+  } else {
+    group(0, std::integral_constant<int, 4>{}, std::true_type{});
+    for (int g0 = kDnTG; g0 < cnt; g0 += kDnTG) {
+      __syncthreads();  // the previous group's operand reads are done
+      group(g0, std::integral_constant<int, 4>{}, std::false_type{});
+    }
   }
 }
 
