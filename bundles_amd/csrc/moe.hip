@@ -520,16 +520,18 @@ constexpr int kMoeH = 2048, kMoeI = 512;
 // workgroup returns at once when e has no tokens).  Each wave owns one chunk: 16 gate rows and
 // the matching 16 up rows over the whole K = H, streamed from HBM in 16 stages of 128 bytes per
 // row with kUpD stages in flight; no reduction across waves.  The activation rows of up to 64
-// tokens (4 tiles of 16) are shared by the four waves through LDS, one K half at a time.
+// tokens (4 tiles of 16) are shared by the four waves through LDS (one tile: the whole K; four
+// tiles: 512-byte K chunks through two buffers); the token list, rows and scales are requested
+// before the weights.
 // Weights are stored in MFMA fragment order (q36_pack_frag8).  Per stage a lane holds 32 bytes of
 // its row (row = lane % 16, bytes 32 (lane / 16) of the 128-byte stage) of both operands -- one e4m3 16x16x128 MFMA, or two int8 16x16x64 MFMAs on the two 16-byte
 // halves (their K pairing is the same for src0 and src1, so the int32 sums are exact).  The
 // 16x16 result gives lane l weight row l%16 and token rows 4(l/16)+r; SwiGLU happens in the
 // lane.  For e4m3 the block sums are accumulated as acc = fma(block sum, xs * ws, acc) in
 // increasing block order from zero.
-constexpr int kUpD = 4;                    // weight stages in flight per wave
-constexpr int kUpKH = kMoeH / 2;           // K bytes per LDS activation half
-constexpr int kUpRow = kUpKH + 16;         // padded LDS row (spreads the 16 rows over the banks)
+constexpr int kUpD = 2;                    // weight stages in flight per wave
+constexpr int kUpBuf0 = 16 * (kMoeH + 16);  // 16 padded whole-K rows, or one 64 x 512-byte chunk
+constexpr int kUpBuf1 = 64 * 512;           // the other chunk buffer
 constexpr int kUpGroups = kMoeI / 16 / 4;  // workgroups per unit (4 chunks each)
 // Buffer load of 16 bytes per lane straight into LDS (lane l writes lds + 16 l); offsets past the
 // buffer's size read as zero.
@@ -540,12 +542,15 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, void* lds, int 
 template <int DT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void moe_up_kernel(MoeDev d) {
   constexpr int H = kMoeH, I = kMoeI, NSTG = H / 128, TG = 64;
-  extern __shared__ __align__(16) char up_lds[];
-  uint8_t* a_l = reinterpret_cast<uint8_t*>(up_lds);                     // [TG][kUpRow]
-  float* xs_t = reinterpret_cast<float*>(up_lds + TG * kUpRow);           // [NSTG][TG] (token fastest)
-  float* ws_l = xs_t + TG * NSTG;                                         // [2I/128][NSTG]
-  int* slots = reinterpret_cast<int*>(ws_l + (2 * I / 128) * NSTG);       // [kMaxM]
-  int* wtot = slots + kMaxM;                                              // [4]
+  // activation rows: buffer 0 holds a one-tile group's 16 padded whole-K rows or the even K
+  // chunks of a four-tile group, buffer 1 the odd chunks.  Separate objects, so the compiler sees
+  // that a copy into one buffer does not touch reads of the other.
+  __shared__ __align__(16) uint8_t a_b0[kUpBuf0];
+  __shared__ __align__(16) uint8_t a_b1[kUpBuf1];
+  __shared__ __align__(16) float xs_t[TG * NSTG];            // [NSTG][TG] (token fastest)
+  __shared__ float ws_l[(2 * I / 128) * NSTG];               // [2I/128][NSTG]
+  __shared__ int slots[kMaxM];
+  __shared__ int wtot[4];
   const int unit = blockIdx.x / kUpGroups, grp = blockIdx.x % kUpGroups;
   const bool shared = unit == 0;
   if (!shared && unit - 1 >= d.ctl[2]) return;
@@ -574,22 +579,82 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     Bq[q][2] = __builtin_amdgcn_raw_buffer_load_b128(urs, lo, s * 2048, 2);
     Bq[q][3] = __builtin_amdgcn_raw_buffer_load_b128(urs, lo, s * 2048 + 1024, 2);
   };
-#pragma unroll
-  for (int s = 0; s < kUpD; ++s) issue(s, s);  // the first weight stages, before the token list
+  // the token list comes first: each group's activation rows and scales are requested before its
+  // first weight stages, so they arrive while the weights stream (vector loads complete in issue
+  // order)
   int e_chk;
   const int cnt = unit_slots(d, unit, slots, wtot, &e_chk);
   if (cnt == 0) return;
-  if constexpr (DT == Q36_MOE_FP8)
-    for (int i = tid; i < (2 * I / 128) * NSTG; i += 256) ws_l[i] = S[i];
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)d.xq, (short)0, d.M * H, 0x00020000);
+  constexpr int NXS = DT == Q36_MOE_FP8 ? NSTG : 1;  // activation scales per token
+  const int xsbytes = d.M * NXS * 4;
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc((void*)d.xs, (short)0, xsbytes, 0x00020000);
   const int n = ch * 16 + lr;
   // One group of up to TG tokens with NTT 16-token tiles (rows past the group's tokens are zero):
   // per 128-byte stage every fragment and scale read first, then the independent MFMAs, then the
-  // scaled accumulates (e4m3: in block order from zero), then SwiGLU -> h per slot.
+  // scaled accumulates (e4m3: in block order from zero), then SwiGLU -> h per slot.  A one-tile
+  // group holds its rows' whole K in LDS; a four-tile group one K half at a time.
   auto group = [&](int g0, auto nttc) {
     constexpr int NTT = decltype(nttc)::value;
+    // activation rows in LDS: a one-tile group holds its 16 rows' whole K (padded rows, one
+    // buffer); a four-tile group streams K in 4 chunks of 512 bytes through two buffers, so the
+    // next chunk's copy overlaps the current chunk's stages and the weight stream never drains.
+    // Ring rows are unpadded: 16-byte piece p of row r sits at position p ^ (r % 16), which puts
+    // the 16 rows of one MFMA read on distinct banks.
+    constexpr int NC = NTT == 1 ? 1 : 4, KC = H / NC, SPC = NSTG / NC;
+    constexpr int ROWB = NC == 1 ? KC + 16 : KC, BUFB = 16 * NTT * ROWB;
+    static_assert(BUFB <= kUpBuf0 && (NC == 1 || BUFB <= kUpBuf1), "activation rows exceed their buffers");
+    static_assert(NC == 1 || kUpD <= SPC, "a chunk must issue a full window of weight stages");
     using Acc = typename std::conditional<DT == Q36_MOE_FP8, v4f, v4i>::type;
+    // chunk c of the group's rows into its buffer by buffer DMA (rows past the group read as zero)
+    auto rows_dma = [&](int c) {
+      if constexpr (NC == 1) {
+        // wave w copies rows w, w + 4, ..., 1 KB per call (lane l: bytes 16 l ..)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int rr = wave + 4 * k, ti = g0 + rr;
+          const int voff = ti < cnt ? slot_token(d, slots[ti]) * H + lane * 16 : d.M * H;
+#pragma unroll
+          for (int h = 0; h < KC / 1024; ++h) dma16(xrs, a_b0 + rr * ROWB + h * 1024, voff + h * 1024);
+        }
+      } else {
+        // one call fills two rows (lanes 0-31 row 2m, lanes 32-63 row 2m + 1); wave w takes the
+        // row pairs w, w + 4, ...; a lane fetches the piece that belongs at its position
+        uint8_t* buf = (c & 1) ? a_b1 : a_b0;
+#pragma unroll
+        for (int k = 0; k < 8 * NTT / 4; ++k) {
+          const int m = wave + 4 * k, rr = 2 * m + (lane >> 5), ti = g0 + rr, p = lane & 31;
+          const int voff = ti < cnt ? slot_token(d, slots[ti]) * H + c * KC + 16 * (p ^ (rr & 15)) : d.M * H;
+          dma16(xrs, buf + 2 * m * KC, voff);
+        }
+      }
+    };
+    // scales of the group (x: [NXS][TG], token fastest; e4m3 weights: [2I/128][NSTG]) into
+    // registers now, into LDS after the weight stages are requested
+    float xsr[TG * NSTG / 256], wsr = 0.f;
+#pragma unroll
+    for (int q = 0; q < TG * NSTG / 256; ++q) {
+      const int i = tid + 256 * q, ti = g0 + i % TG, sx = i / TG;
+      const int off = ti < cnt && sx < NXS ? (slot_token(d, slots[ti]) * NXS + sx) * 4 : xsbytes;
+      xsr[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, off, 0, 0));
+    }
+    if constexpr (DT == Q36_MOE_FP8) {
+      constexpr int NW = (2 * I / 128) * NSTG;
+      static_assert(NW <= 256, "one weight scale per thread");
+      const __amdgpu_buffer_rsrc_t wss = __builtin_amdgcn_make_buffer_rsrc((void*)S, (short)0, NW * 4, 0x00020000);
+      wsr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wss, g0 == 0 && tid < NW ? tid * 4 : NW * 4, 0, 0));
+    }
+    rows_dma(0);
+#pragma unroll
+    for (int s = 0; s < kUpD; ++s) issue(s, s);
+#pragma unroll
+    for (int q = 0; q < TG * NSTG / 256; ++q) xs_t[tid + 256 * q] = xsr[q];
+    if constexpr (DT == Q36_MOE_FP8)
+      if (g0 == 0 && tid < (2 * I / 128) * NSTG) ws_l[tid] = wsr;
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kUpD) : "memory");  // the rows, not the weights
+    __syncthreads();
+    asm volatile("" ::: "memory");
     Acc ag[NTT], au[NTT];
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt) {
@@ -597,28 +662,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       au[tt] = Acc{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      // this half's activation rows into LDS by buffer DMA: wave w copies rows w, w + 4, ...,
-      // 1 KB each (lane l: bytes 16 l .. of the row); rows past the group read as zero
-      __syncthreads();
-      for (int rr = wave; rr < 16 * NTT; rr += 4) {
-        const int ti = g0 + rr;
-        const int voff = ti < cnt ? slot_token(d, slots[ti]) * H + half * kUpKH + lane * 16 : d.M * H;
-        dma16(xrs, a_l + rr * kUpRow, voff);
+    for (int c = 0; c < NC; ++c) {
+      if (c > 0) {
+        // chunk c landed (its copy is older than the chunk's 4 * SPC weight loads) and every wave
+        // is done with chunk c - 1, whose buffer the next copy reuses
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * SPC) : "memory");
+        __syncthreads();
+        asm volatile("" ::: "memory");
       }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      asm volatile("" ::: "memory");
+      if (c + 1 < NC) rows_dma(c + 1);
+      const uint8_t* buf = (c & 1) ? a_b1 : a_b0;
 #pragma unroll
-      for (int sh = 0; sh < NSTG / 2; ++sh) {
-        const int s = half * (NSTG / 2) + sh;
+      for (int sl = 0; sl < SPC; ++sl) {
+        const int s = c * SPC + sl;
         const int q = s % kUpD;
         v4i a[NTT][2];
 #pragma unroll
         for (int tt = 0; tt < NTT; ++tt) {
-          const uint8_t* ap = a_l + (tt * 16 + lr) * kUpRow + sh * 128 + lgp * 32;
-          a[tt][0] = *reinterpret_cast<const v4i*>(ap);
-          a[tt][1] = *reinterpret_cast<const v4i*>(ap + 16);
+          const int row = tt * 16 + lr;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int piece = sl * 8 + lgp * 2 + h;  // 16-byte piece within the row's chunk
+            a[tt][h] = *reinterpret_cast<const v4i*>(buf + row * ROWB + 16 * (NC == 1 ? piece : piece ^ lr));
+          }
         }
         if constexpr (DT == Q36_MOE_FP8) {
           const float wg = ws_l[(ng / 128) * NSTG + s], wu = ws_l[((I + ng) / 128) * NSTG + s];
@@ -684,29 +750,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
   };
   for (int g0 = 0; g0 < cnt; g0 += TG) {
-    const int nt = min(TG / 16, (cnt - g0 + 15) / 16);
-    if (g0 > 0) {
-#pragma unroll
-      for (int s = 0; s < kUpD; ++s) issue(s, s);
-      __syncthreads();  // the previous group's epilogue has read xs_t
-    }
-    for (int i = tid; i < TG * NSTG; i += 256) {
-      const int ti = g0 + i % TG, s = i / TG;
-      if constexpr (DT == Q36_MOE_FP8)
-        xs_t[i] = ti < cnt ? d.xs[(size_t)slot_token(d, slots[ti]) * NSTG + s] : 0.f;
-      else
-        xs_t[i] = (ti < cnt && s == 0) ? d.xs[slot_token(d, slots[ti])] : 0.f;
-    }
+    if (g0 > 0) __syncthreads();  // the previous group's epilogue has read xs_t
     // two tile counts: one tile (most experts at decode sizes) or four (rows past the tokens are
     // zero); a third instance would cost registers in all of them
-    if (nt == 1)
+    if (cnt - g0 <= 16)
       group(g0, std::integral_constant<int, 1>{});
     else
       group(g0, std::integral_constant<int, 4>{});
   }
 }
-constexpr size_t kUpLds = 64 * kUpRow + sizeof(float) * (64 * (kMoeH / 128) + (2 * kMoeI / 128) * (kMoeH / 128)) +
-                          sizeof(int) * (kMaxM + 4);
 
 // ------------------------------------------------------------------------------------------
 // 4. down GEMM x routing weight
@@ -1157,9 +1209,7 @@ int launch_lists(const MoeDev& d, hipStream_t st) {
 
 template <int DT>
 int launch_up_t(const MoeDev& d, hipStream_t st) {
-  int rc = ensure_lds(reinterpret_cast<const void*>(&moe_up_kernel<DT>), kUpLds, "q36_moe_up");
-  if (rc) return rc;
-  moe_up_kernel<DT><<<(d.E + 1) * kUpGroups, 256, kUpLds, st>>>(d);
+  moe_up_kernel<DT><<<(d.E + 1) * kUpGroups, 256, 0, st>>>(d);
   return check_launch("q36_moe_up");
 }
 template <int DT>
