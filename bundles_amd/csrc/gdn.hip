@@ -8,11 +8,14 @@
 //   (:786-791); value head hv reads key head hv / 2 (:9-11,520).  The reference keeps a replay
 //   ring for rollback; this node writes every position's state instead.
 //
-// One workgroup of 512 threads per (sequence, value head).  Thread (v = tid / 4, c4 = tid % 4)
-// holds row v of the 128x128 fp32 state in registers, columns {16 j + 4 c4 + i : j < 8, i < 4}:
-// a row dot is 32 local fma plus a two-step quad reduction, a snapshot store writes 64
-// contiguous bytes per row per instruction.  The prologue computes the unit's conv outputs
-// (q and k of key head hv/2, v of head hv), the norms and the gates into LDS.
+// One workgroup of 512 threads per (sequence, value head).  Thread (r = tid / 8, c8 = tid % 8)
+// holds rows r and r + 64 of the 128x128 fp32 state in registers, columns
+// {32 jj + 4 c8 + i : jj < 4, i < 4} of each: a row dot is 16 local fma plus a three-step
+// reduction over the row's 8 threads, and a snapshot store writes whole 128-byte lines (8 rows x
+// 128 contiguous bytes per instruction).  The prologue requests the conv inputs, the output
+// gate z and the gate inputs, then the state rows (half before the conv, half after); it computes
+// the unit's conv outputs (q and k of key head hv/2, v of head hv), the norms and the gates into
+// LDS while the state arrives.
 #include "q36_device.h"
 #include "q36_host.h"
 
@@ -46,18 +49,26 @@ __device__ __forceinline__ float bfs(const uint16_t* p) { return bf2f(*p); }
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8, 8))) void gdn_verify_kernel(GdnDev d) {
   __shared__ float qs[kTMax][GK], ks[kTMax][GK], vs[kTMax][GV];
   __shared__ float os[kTMax][GV];
+  __shared__ float zs[kTMax][GV], nws[GV];  // the output gate's z and the norm weight, prefetched
   __shared__ float gate_g[kTMax], gate_b[kTMax];
   const int unit = blockIdx.x;
   const int bq = unit / GHV, hv = unit % GHV, hk = hv / 2;
   const int T = d.T;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int row = tid >> 2, c4 = tid & 3;
+  const int r0 = tid >> 3, c8 = tid & 7;
+  // state register j (< 8): row r0 + 64 (j / 4), columns 32 (j % 4) + 4 c8 .. +3
+  auto soff = [&](int j) { return (r0 + 64 * (j >> 2)) * GK + 32 * (j & 3) + 4 * c8; };
 
-  // conv + SiLU for the unit's 384 channels: q (hk), k (hk), v (hv)
-  if (tid < 3 * 128) {
-    const int part = tid >> 7, i = tid & 127;
-    const int ch = part == 0 ? hk * GK + i : part == 1 ? GHK * GK + hk * GK + i : 2 * GHK * GK + hv * GV + i;
-    float w[kTMax + 3];
+  // Requests first, in this order: the conv inputs (threads < 384), the output gate z and the norm
+  // weight (threads >= 384), the gate inputs, then the 64 KB of state rows.  Loads complete in
+  // issue order, so the conv and the prefetch wait only for their own data while the state is in
+  // flight.
+  const int part = tid >> 7, i = tid & 127;  // conv channel (part < 3) or value channel (part 3)
+  const int ch = part == 0 ? hk * GK + i : part == 1 ? GHK * GK + hk * GK + i : 2 * GHK * GK + hv * GV + i;
+  float w[kTMax + 3], cw[4];
+  v4i zr = {0, 0, 0, 0};
+  float nwv = 0.f;
+  if (part < 3) {
     const uint16_t* cs = d.conv_state + ((size_t)bq * GQKV + ch) * 3;
     w[0] = bfs(cs);
     w[1] = bfs(cs + 1);
@@ -65,9 +76,29 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 #pragma unroll
     for (int t = 0; t < kTMax; ++t)
       w[3 + t] = t < T ? bfs(d.mixed + ((size_t)bq * T + t) * GQKV + ch) : 0.f;
-    float cw[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) cw[q] = bfs(d.conv_w + (size_t)ch * 4 + q);
+  } else {
+    // z of the unit's positions: thread i < 16 T loads 8 values of position i / 16
+    if (i < 16 * T)
+      zr = *reinterpret_cast<const v4i*>(d.z + ((size_t)bq * T + (i >> 4)) * GZ + hv * GV + (i & 15) * 8);
+    nwv = bfs(d.norm_w + i);
+  }
+  float av = 0.f, bv = 0.f;
+  if (tid < T) {
+    const size_t r = (size_t)bq * T + tid;
+    av = bfs(d.a + r * GHV + hv);
+    bv = bfs(d.b + r * GHV + hv);
+  }
+  const float* s0 = d.S0 + ((size_t)bq * GHV + hv) * GV * GK;
+  v4f st[8];
+  // half of the state before the conv and half after it (all of it at once would not fit the
+  // 64 registers of eight waves per SIMD beside the conv's inputs)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) st[j] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(s0 + soff(j)));
+
+  if (part < 3) {
+    // conv + SiLU for the unit's 384 channels: q (hk), k (hk), v (hv)
 #pragma unroll
     for (int t = 0; t < kTMax; ++t) {
       if (t < T) {
@@ -87,15 +118,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 #pragma unroll
       for (int q = 0; q < 3; ++q) co[q] = (uint16_t)f2bf(w[T + q]);
     }
-  }
-  // the state row into registers; it lands while the gates and the norms are computed
-  const float* s0 = d.S0 + (((size_t)bq * GHV + hv) * GV + row) * GK + 4 * c4;
-  v4f st[8];
+  } else {
+    if (i < 16 * T) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) st[j] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(s0 + 16 * j));
+      for (int q = 0; q < 4; ++q) {
+        zs[i >> 4][(i & 15) * 8 + 2 * q] = bf_lo((uint32_t)zr[q]);
+        zs[i >> 4][(i & 15) * 8 + 2 * q + 1] = bf_hi((uint32_t)zr[q]);
+      }
+    }
+    nws[i] = nwv;
+  }
+#pragma unroll
+  for (int j = 4; j < 8; ++j) st[j] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(s0 + soff(j)));
   if (tid < T) {
-    const size_t r = (size_t)bq * T + tid;
-    const float av = bfs(d.a + r * GHV + hv), bv = bfs(d.b + r * GHV + hv);
     const float xg = av + d.dt_bias[hv];
     const float sp = xg <= 20.f ? logf(1.f + expf_q(xg)) : xg;
     gate_g[tid] = expf_q(-expf_q(d.A_log[hv]) * sp);  // e^{g}
@@ -115,36 +150,51 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   }
   __syncthreads();
 
-  const size_t snap_stride = (size_t)GHV * GV * GK;  // one position of one sequence
-  float* snap = d.snaps + ((((size_t)bq * T) * GHV + hv) * GV + row) * GK + 4 * c4;
+  // snapshot stores through a buffer resource: the lane's offset in one register, the position's
+  // block and the register's row/column step (the same for every lane) in the scalar offset, so no
+  // store needs an address register of its own: the recurrence fits the 64 registers of eight
+  // waves per SIMD
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(  // the sequence's T x 2 MB
+      d.snaps + (size_t)__builtin_amdgcn_readfirstlane(bq * T) * GHV * GV * GK, (short)0,
+      __builtin_amdgcn_readfirstlane(T * GHV * GV * GK * 4), 0x00020000);
+  const int slane = soff(0) * 4;
   for (int t = 0; t < T; ++t) {
     const float eg = gate_g[t], beta = gate_b[t];
-    float kv = 0.f;
+    float kv[2] = {0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const v4f kk = *reinterpret_cast<const v4f*>(&ks[t][16 * j + 4 * c4]);
+      const v4f kk = *reinterpret_cast<const v4f*>(&ks[t][32 * (j & 3) + 4 * c8]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kv = __builtin_fmaf(st[j][i], kk[i], kv);
+      for (int i = 0; i < 4; ++i) kv[j >> 2] = __builtin_fmaf(st[j][i], kk[i], kv[j >> 2]);
     }
-    kv = kv + __shfl_xor(kv, 1);
-    kv = kv + __shfl_xor(kv, 2);
-    const float u = beta * (vs[t][row] - eg * kv);
-    float ov = 0.f;
+    float u[2], ov[2] = {0.f, 0.f};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      kv[h] = kv[h] + __shfl_xor(kv[h], 1);
+      kv[h] = kv[h] + __shfl_xor(kv[h], 2);
+      kv[h] = kv[h] + __shfl_xor(kv[h], 4);
+      u[h] = beta * (vs[t][r0 + 64 * h] - eg * kv[h]);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const v4f kk = *reinterpret_cast<const v4f*>(&ks[t][16 * j + 4 * c4]);
-      const v4f qq = *reinterpret_cast<const v4f*>(&qs[t][16 * j + 4 * c4]);
+      const v4f kk = *reinterpret_cast<const v4f*>(&ks[t][32 * (j & 3) + 4 * c8]);
+      const v4f qq = *reinterpret_cast<const v4f*>(&qs[t][32 * (j & 3) + 4 * c8]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        st[j][i] = __builtin_fmaf(eg, st[j][i], u * kk[i]);
-        ov = __builtin_fmaf(st[j][i], qq[i], ov);
+        st[j][i] = __builtin_fmaf(eg, st[j][i], u[j >> 2] * kk[i]);
+        ov[j >> 2] = __builtin_fmaf(st[j][i], qq[i], ov[j >> 2]);
       }
       // plain stores: measured 89 us per 32 x 5 step against 128 us with non-temporal ones
-      *reinterpret_cast<v4f*>(snap + (size_t)t * snap_stride + 16 * j) = st[j];
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, st[j]), srs, slane,
+                                             (t * GHV + hv) * (GV * GK * 4) + ((j >> 2) * 64 * GK + (j & 3) * 32) * 4, 0);
     }
-    ov = ov + __shfl_xor(ov, 1);
-    ov = ov + __shfl_xor(ov, 2);
-    if (c4 == 0) os[t][row] = rbf(ov);  // the core output is bf16
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      ov[h] = ov[h] + __shfl_xor(ov[h], 1);
+      ov[h] = ov[h] + __shfl_xor(ov[h], 2);
+      ov[h] = ov[h] + __shfl_xor(ov[h], 4);
+      if (c8 == 0) os[t][r0 + 64 * h] = rbf(ov[h]);  // the core output is bf16
+    }
   }
   __syncthreads();
   // gated RMSNorm per position: y = bf16(((o * rstd) * w) * (z * sigmoid(z)))
@@ -157,8 +207,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     for (int h = 0; h < 2; ++h) {
       const int v = lane + 64 * h;
       const float o = h ? o1 : o0;
-      const float zz = bfs(d.z + r * GZ + hv * GV + v);
-      const float y = ((o * rstd) * bfs(d.norm_w + v)) * (zz * sigmoid_q(zz));
+      const float zz = zs[t][v];
+      const float y = ((o * rstd) * nws[v]) * (zz * sigmoid_q(zz));
       d.out[r * GZ + hv * GV + v] = (uint16_t)f2bf(y);
     }
   }
