@@ -10,9 +10,9 @@
 // or W8A16); their numerics follow the MoE experts: per-token x 128-channel activation scales,
 // one e4m3 block sum per 128-channel block, terms added in block order.
 //
-// Kernels: act_quant (bf16 -> e4m3 + scales, optionally gated), fp8_gemm (skinny GEMM: each wave
-// streams the whole K for its own tokens with both operands straight from global memory), norm_rope
-// (one wave per token and head).
+// Kernels: act_quant (bf16 -> e4m3 + scales, optionally gated), proj_gemm (each wave streams two
+// 16-row weight tiles over K from HBM; the token group's activations come through an LDS chunk
+// ring shared by the workgroup), norm_rope (one wave per token and head).
 #include "q36_device.h"
 #include "q36_host.h"
 
@@ -20,9 +20,6 @@ namespace q36 {
 namespace {
 
 __device__ __forceinline__ v4i ldg16a(const uint8_t* p) { return *reinterpret_cast<const v4i*>(p); }
-__device__ __forceinline__ v4i ldg16a_nt(const uint8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
-}
 __device__ __forceinline__ v8i cat8a(v4i a, v4i b) {
   v8i r = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   return r;
@@ -34,15 +31,12 @@ __device__ __forceinline__ v4f mfma_e4m3(v8i a, v8i b) {
 
 // ------------------------------------------------------------------------------------------
 // activation quantization: one workgroup per token; thread tid owns 8-element chunks tid + 256 r.
-// The e4m3 values are written in MFMA fragment order (below), the GEMM's activation loads then
-// being 1 KB contiguous per wave instruction.
-// gate != nullptr: the value quantized is bf16(x * sigmoid(gate)) (the o_proj input).  Scales are
-// stored transposed with the token count rounded up to 4, s[group][Tp], so that a GEMM lane reads
-// its four tokens' scales with one 16-byte load.
+// Row-major e4m3 codes q[T][K] and per 128-group scales s[T][K/128].
+// gate != nullptr: the value quantized is bf16(x * sigmoid(gate)) (the o_proj input).
 // ------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* x, const uint16_t* gate, int K, uint8_t* q,
                                                         float* s) {
-  const int t = blockIdx.x, tid = threadIdx.x, Tp = (gridDim.x + 3) & ~3;
+  const int t = blockIdx.x, tid = threadIdx.x;
   for (int c = tid; 8 * c < K; c += 256) {
     const v4i xv = ldg16a(reinterpret_cast<const uint8_t*>(x + (size_t)t * K + 8 * c));
     float f[8];
@@ -68,131 +62,160 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* x, const
     uint32_t wd[2] = {0u, 0u};
 #pragma unroll
     for (int i = 0; i < 8; i += 2) wd[i >> 2] |= f2e4m3x2_hw(f[i] * inv, f[i + 1] * inv) << (8 * (i & 3));
-    // fragment layout: 16-token tile, 128-block kb, half h, lane l = 16 g + t % 16, byte j holds
-    // element k = 128 kb + 32 g + 16 h + j of token t (the lane's MFMA operand is its two 16-byte
-    // halves, 1 KB apart)
-    const int k = 8 * c, kb = k >> 7, g = (k >> 5) & 3, h = (k >> 4) & 1, j = k & 15;
-    const size_t off = (((size_t)(t >> 4) * (K >> 7) + kb) << 11) + (h << 10) + ((g * 16 + (t & 15)) << 4) + j;
-    *reinterpret_cast<uint2*>(q + off) = make_uint2(wd[0], wd[1]);
-    if ((c & 15) == 0) s[(size_t)(c / 16) * Tp + t] = m / 448.f;
+    *reinterpret_cast<uint2*>(q + (size_t)t * K + 8 * c) = make_uint2(wd[0], wd[1]);
+    if ((c & 15) == 0) s[(size_t)t * (K >> 7) + c / 16] = m / 448.f;
   }
 }
 
 // ------------------------------------------------------------------------------------------
-// skinny e4m3 GEMM:  Y[t, n] = bf16(acc), acc = fma(blocksum_kb(t, n), xs[t, kb] * ws[n / 128, kb], acc)
-// over the 128-blocks kb in increasing order from zero.
-// Both operands are stored in MFMA fragment order: for a 16-row tile and a 128-block, 2 KB holding
-// half h (16 bytes) of lane l's operand at h * 1024 + 16 l, so that a wave reads a fragment with two
-// 1 KB contiguous loads (row-major rows are K bytes apart: a lane-per-row load is 64 separate
-// requests).
-// Workgroup = RT 16-row weight tiles x 4 waves of TPW 16-token tiles each.  Every wave streams the
-// whole K for its own tokens, loading both MFMA operands straight from global memory four blocks
-// ahead (the K loop is fully unrolled, so the register stages rotate by name); the weight
-// fragments the four waves share come from L1 after the first.  No LDS.  MFMA src0 = tokens
-// (lane row l%16), src1 = weight rows; lane l of the 16x16 result holds weight row l%16 and token
-// rows 4 (l/16) + r.
+// e4m3 projection GEMM:  Y[t, n] = bf16(acc), acc = fma(blocksum_kb(t, n), xs[t, kb] * ws[n / 128, kb],
+// acc) over the 128-blocks kb in increasing order from zero.
+// Weights in MFMA fragment order (q36_pack_frag8): for a 16-row tile and a 128-block, 2 KB holding
+// half h (16 bytes) of lane l's operand at h * 1024 + 16 l; a wave reads a fragment with two 1 KB
+// contiguous loads.
+// Workgroup = 128 weight rows (4 waves x two 16-row tiles) x one group of 16 NTT tokens.  Each wave
+// streams its two tiles over K from HBM in 128-byte stages, kPD stages in flight, through buffer
+// loads with the stage offset in the scalar offset.  The group's activation rows go through LDS
+// in 512-byte K chunks, double-buffered (a chunk's copy overlaps the previous chunk's stages, so the
+// weight stream never drains), shared by the four waves; a chunk row's 16-byte piece p sits at
+// position p ^ (row % 16), which puts the 16 rows of one MFMA read on distinct banks.  The weights
+// are the MFMA's first operand: lane l ends with token l % 16 of the tile and rows 4 (l / 16) .. +3,
+// one 8-byte store.  The token groups of a row block are 72 or 16 workgroups apart in the grid, so
+// they run on one XCD and share its L2 for the weights.
 // ------------------------------------------------------------------------------------------
 struct GemmDev {
-  const uint8_t* A;   // e4m3 [T16 / 16 tiles][K / 128 blocks][2 halves][64 lanes][16 B]
-  const float* AsT;   // [K/128, Tp], Tp = T rounded up to 4
+  const uint8_t* A;   // e4m3 [T, K] row-major
+  const float* As;    // [T, K/128]
   int T, K;
   const uint8_t* W;   // e4m3 in fragment order [N / 16][K / 128][2][64][16 B]
   const float* Ws;    // [N/128, K/128]
   int N;
   uint16_t* Y;        // bf16 [T, N]
 };
+constexpr int kPKC = 512;  // K bytes per LDS chunk
+__device__ __forceinline__ void pdma16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds, 16, voff, 0, 0, 0);
+}
 
-template <int RT, int TPW, int NKB>
-__global__ __launch_bounds__(256) void fp8_gemm_kernel(GemmDev g) {
-  constexpr int D = 4;  // blocks in flight
+template <int NTT, int NKB, int kPD>  // token tiles, K blocks, weight stages in flight per wave
+__global__ __launch_bounds__(256) void proj_gemm_kernel(GemmDev g) {
+  constexpr int TG = 16 * NTT, SPC = kPKC / 128, NC = NKB / SPC;
+  static_assert(NKB % SPC == 0 && kPD <= SPC, "K must be whole chunks, a chunk a full window of stages");
+  // separate objects, so the compiler sees that a copy into one buffer does not touch reads of the other
+  __shared__ __align__(16) uint8_t a_b0[TG * kPKC];
+  __shared__ __align__(16) uint8_t a_b1[TG * kPKC];
+  __shared__ __align__(16) float xs_l[NKB * TG];  // [NKB][TG], token fastest
+  __shared__ float ws_l[4][NKB];                  // each wave's weight block scales
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
-  const int n0 = blockIdx.x * 16 * RT;
-  const int tw = (blockIdx.y * 4 + wave) * TPW * 16;  // first token of this wave
-  if (tw >= g.T) return;                                // no tokens: nothing to do (no barriers)
-  const int Tp = (g.T + 3) & ~3;
-  const uint8_t* wp[RT];
+  const int t0 = blockIdx.y * TG;
+  const int n0 = __builtin_amdgcn_readfirstlane(blockIdx.x * 128 + wave * 32);  // the wave's two tiles
+  const int K = NKB * 128;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g.W + ((size_t)(n0 >> 4) * NKB << 11)), (short)0, 2 * NKB << 11, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)g.A, (short)0, g.T * K, 0x00020000);
+  const int xsbytes = g.T * NKB * 4;
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc((void*)g.As, (short)0, xsbytes, 0x00020000);
+  // the wave's weight scales (one 128-row block) go to LDS with the activation scales: a vector load
+  // per stage would be the newest load at its wait and drain the weight stream
+  const float wsv = lane < NKB ? g.Ws[(size_t)(n0 / 128) * NKB + lane] : 0.f;
+  v4i Bq[kPD][4];
+  auto issue = [&](int s, int q) {
+    Bq[q][0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, s * 2048, 2);
+    Bq[q][1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, s * 2048 + 1024, 2);
+    Bq[q][2] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, (NKB + s) * 2048, 2);
+    Bq[q][3] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, (NKB + s) * 2048 + 1024, 2);
+  };
+  // chunk c of the group's rows: one call fills two rows (lanes 0-31 row 2m, 32-63 row 2m + 1); a
+  // lane fetches the piece that belongs at its position; rows past T read as zero
+  auto rows_dma = [&](int c) {
+    uint8_t* buf = (c & 1) ? a_b1 : a_b0;
 #pragma unroll
-  for (int r = 0; r < RT; ++r) wp[r] = g.W + ((size_t)((n0 >> 4) + r) * NKB << 11) + lane * 16;
-  const uint8_t* ap[TPW];
-  int sct[TPW];  // first of the lane's four output tokens per tile, clamped into the scale row
+    for (int k = 0; k < TG / 8; ++k) {
+      const int m = wave + 4 * k, rr = 2 * m + (lane >> 5), p = lane & 31;
+      const int voff = t0 + rr < g.T ? (t0 + rr) * K + c * kPKC + 16 * (p ^ (rr & 15)) : g.T * K;
+      pdma16(xrs, buf + 2 * m * kPKC, voff);
+    }
+  };
+  // the group's activation scales into registers, then LDS once the first weights are requested
+  float xsr[NKB * TG / 256];
 #pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) {
-    const int tile = min((tw >> 4) + tt, (g.T - 1) >> 4);  // tiles past T: the last one (discarded)
-    ap[tt] = g.A + ((size_t)tile * NKB << 11) + lane * 16;
-    sct[tt] = min(tw + tt * 16 + 4 * lgp, (g.T - 1) & ~3);
+  for (int q = 0; q < NKB * TG / 256; ++q) {
+    const int i = tid + 256 * q, tt = i % TG, kb = i / TG;
+    const int off = t0 + tt < g.T ? ((t0 + tt) * NKB + kb) * 4 : xsbytes;
+    xsr[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, off, 0, 0));
   }
-  const float* wsr = g.Ws + (size_t)(n0 / 128) * NKB;
-  struct Stage {
-    v4i w[RT][2];
-    v4i a[TPW][2];
-    float4 sc[TPW];
-    float ws;
-  };
-  auto load = [&](Stage& st, int kb) {
+  rows_dma(0);
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      st.w[r][0] = ldg16a(wp[r] + kb * 2048);
-      st.w[r][1] = ldg16a(wp[r] + kb * 2048 + 1024);
+  for (int s = 0; s < kPD; ++s) issue(s, s);
+#pragma unroll
+  for (int q = 0; q < NKB * TG / 256; ++q) xs_l[tid + 256 * q] = xsr[q];
+  if (lane < NKB) ws_l[wave][lane] = wsv;
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kPD) : "memory");  // the rows, not the weights
+  __syncthreads();
+  asm volatile("" ::: "memory");
+  v4f acc[2][NTT];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int tt = 0; tt < NTT; ++tt) acc[c][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c > 0) {
+      // chunk c landed (its copy is older than the chunk's 4 * SPC weight loads) and every wave is
+      // done with chunk c - 1, whose buffer the next copy reuses
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * SPC) : "memory");
+      __syncthreads();
+      asm volatile("" ::: "memory");
     }
+    if (c + 1 < NC) rows_dma(c + 1);
+    const uint8_t* buf = (c & 1) ? a_b1 : a_b0;
 #pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-      st.a[tt][0] = ldg16a(ap[tt] + kb * 2048);
-      st.a[tt][1] = ldg16a(ap[tt] + kb * 2048 + 1024);
-      // tokens past T read padding or the next row: their results are never stored
-      st.sc[tt] = *reinterpret_cast<const float4*>(g.AsT + (size_t)kb * Tp + sct[tt]);
-    }
-    st.ws = wsr[kb];
-  };
-  float acc[RT][TPW][4];
+    for (int sl = 0; sl < SPC; ++sl) {
+      const int s = c * SPC + sl, q = s % kPD;
+      const float ws = ws_l[wave][s];
+      v8i a[NTT];
 #pragma unroll
-  for (int r = 0; r < RT; ++r)
-#pragma unroll
-    for (int tt = 0; tt < TPW; ++tt)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[r][tt][q] = 0.f;
-  auto compute = [&](const Stage& st) {
-    v4f rr[RT][TPW];
-#pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-      for (int tt = 0; tt < TPW; ++tt)
-        rr[r][tt] = mfma_e4m3(cat8a(st.a[tt][0], st.a[tt][1]), cat8a(st.w[r][0], st.w[r][1]));
-#pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-      for (int tt = 0; tt < TPW; ++tt) {
-        acc[r][tt][0] = __builtin_fmaf(rr[r][tt][0], st.sc[tt].x * st.ws, acc[r][tt][0]);
-        acc[r][tt][1] = __builtin_fmaf(rr[r][tt][1], st.sc[tt].y * st.ws, acc[r][tt][1]);
-        acc[r][tt][2] = __builtin_fmaf(rr[r][tt][2], st.sc[tt].z * st.ws, acc[r][tt][2]);
-        acc[r][tt][3] = __builtin_fmaf(rr[r][tt][3], st.sc[tt].w * st.ws, acc[r][tt][3]);
+      for (int tt = 0; tt < NTT; ++tt) {
+        const int row = tt * 16 + lr;
+        const v4i a0 = *reinterpret_cast<const v4i*>(buf + row * kPKC + 16 * ((sl * 8 + lgp * 2) ^ lr));
+        const v4i a1 = *reinterpret_cast<const v4i*>(buf + row * kPKC + 16 * ((sl * 8 + lgp * 2 + 1) ^ lr));
+        a[tt] = cat8a(a0, a1);
       }
-    // the sums are formed here (left alone, the compiler sinks them below the K loop and keeps
-    // every MFMA result live)
+      const v8i w0 = cat8a(Bq[q][0], Bq[q][1]), w1 = cat8a(Bq[q][2], Bq[q][3]);
 #pragma unroll
-    for (int r = 0; r < RT; ++r)
+      for (int tt = 0; tt < NTT; ++tt) {
+        const float xw = xs_l[s * TG + tt * 16 + lr] * ws;  // this lane's token
+        const v4f r0 = mfma_e4m3(w0, a[tt]);
+        const v4f r1 = mfma_e4m3(w1, a[tt]);
 #pragma unroll
-      for (int tt = 0; tt < TPW; ++tt)
+        for (int r = 0; r < 4; ++r) {
+          acc[0][tt][r] = __builtin_fmaf(r0[r], xw, acc[0][tt][r]);
+          acc[1][tt][r] = __builtin_fmaf(r1[r], xw, acc[1][tt][r]);
+        }
+      }
+      // the running sums are formed here (left alone, the compiler sinks the chain below the
+      // stage loop and keeps every stage's MFMA results live)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) asm volatile("" : "+v"(acc[r][tt][q]));
-  };
-  Stage st[D];
+      for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-  for (int i = 0; i < D; ++i) load(st[i], i);
+        for (int tt = 0; tt < NTT; ++tt)
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    compute(st[kb % D]);
-    if (kb + D < NKB) load(st[kb % D], kb + D);
-  }
-#pragma unroll
-  for (int r = 0; r < RT; ++r)
-#pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-      const int n = n0 + r * 16 + lr;
-      const int t = tw + tt * 16 + 4 * lgp;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (t + q < g.T) g.Y[(size_t)(t + q) * g.N + n] = (uint16_t)f2bf(acc[r][tt][q]);
+          for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(acc[c2][tt][r]));
+      if (s + kPD < NKB) issue(s + kPD, q);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  }
+  // lane: token t0 + 16 tt + l % 16, rows n0 + 16 c + 4 (l / 16) .. +3
+#pragma unroll
+  for (int tt = 0; tt < NTT; ++tt) {
+    const int t = t0 + tt * 16 + lr;
+    if (t < g.T) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        *reinterpret_cast<uint2*>(g.Y + (size_t)t * g.N + n0 + c * 16 + 4 * lgp) =
+            make_uint2(pack_bf2(acc[c][tt][0], acc[c][tt][1]), pack_bf2(acc[c][tt][2], acc[c][tt][3]));
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -287,8 +310,8 @@ AttnWs attn_ws(int T) {
     o = align_up(o + b, 256);
     return r;
   };
-  w.xq = take((size_t)((T + 15) & ~15) * 2048);
-  w.xs = take(sizeof(float) * (size_t)16 * ((T + 3) & ~3));
+  w.xq = take((size_t)T * 2048);
+  w.xs = take(sizeof(float) * (size_t)16 * T);
   w.qkv = take(sizeof(uint16_t) * (size_t)T * 9216);
   w.total = o;
   return w;
@@ -304,17 +327,17 @@ OprojWs oproj_ws(int T) {
     o = align_up(o + b, 256);
     return r;
   };
-  w.aq = take((size_t)((T + 15) & ~15) * 4096);
-  w.as = take(sizeof(float) * (size_t)32 * ((T + 3) & ~3));
+  w.aq = take((size_t)T * 4096);
+  w.as = take(sizeof(float) * (size_t)32 * T);
   w.total = o;
   return w;
 }
 
-// RT 16-row tiles per workgroup; TPW token tiles per wave (a workgroup covers 64 TPW tokens)
-template <int RT, int TPW, int NKB>
+// grid: (N / 128 row blocks, token groups of 16 NTT)
+template <int NTT, int NKB, int PD>
 void launch_gemm(const GemmDev& g, hipStream_t st) {
-  const dim3 grid(g.N / (16 * RT), (g.T + 64 * TPW - 1) / (64 * TPW));
-  fp8_gemm_kernel<RT, TPW, NKB><<<grid, 256, 0, st>>>(g);
+  const dim3 grid(g.N / 128, (g.T + 16 * NTT - 1) / (16 * NTT));
+  proj_gemm_kernel<NTT, NKB, PD><<<grid, 256, 0, st>>>(g);
 }
 
 // 8-bit codes (e4m3 or int8) [N, K] row-major -> fragment order; thread = one 16-byte chunk of the output
@@ -358,10 +381,12 @@ extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
   uint16_t* qkv = reinterpret_cast<uint16_t*>(ws + L.qkv);
   act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr, 2048, xq, xs);
   const GemmDev g{xq, xs, a->T, 2048, static_cast<const uint8_t*>(a->wqkv), a->sqkv, 9216, qkv};
-  if (a->T > 64)
-    launch_gemm<2, 2, 16>(g, st);
+  // measured at 128 tokens: two-tile groups with 2 stages in flight beat four-tile groups (the
+  // weight reads from L2 double, the grid doubles to 288 workgroups) and one-tile groups
+  if (a->T > 16)
+    launch_gemm<2, 16, 2>(g, st);
   else
-    launch_gemm<1, 1, 16>(g, st);
+    launch_gemm<1, 16, 4>(g, st);
   RopeDev r{a->T, a->max_pos, qkv, static_cast<const uint16_t*>(a->q_norm_w),
             static_cast<const uint16_t*>(a->k_norm_w), a->eps, a->cos_sin, a->positions,
             static_cast<uint16_t*>(a->q), static_cast<uint16_t*>(a->gate), static_cast<uint16_t*>(a->k),
@@ -388,7 +413,8 @@ extern "C" int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream) {
   act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->attn), static_cast<const uint16_t*>(a->gate),
                                          4096, aq, as);
   const GemmDev g{aq, as, a->T, 4096, static_cast<const uint8_t*>(a->wo), a->so, 2048, static_cast<uint16_t*>(a->out)};
-  launch_gemm<1, 1, 32>(g, st);
+  // o_proj has 16 row blocks: one-tile groups (128 workgroups at 128 tokens), 4 stages in flight
+  launch_gemm<1, 32, 4>(g, st);
   return check_launch("q36_attn_oproj");
 }
 
