@@ -10,12 +10,12 @@
 // Kernels:
 //   lmh_prep   one wave per row: norm (sum of squares in the fixed 64-lane order), int8 quant,
 //              and the row's argmax key reset to 0.
-//   lmh_gemm   256 x 256 output tile per workgroup (4 waves, 128 x 128 each, int32 accumulators
-//              in AGPRs), K in 64-byte steps through a 4-stage LDS ring filled by buffer loads
-//              straight into LDS, three steps ahead (no register staging).  Epilogue: bf16
-//              logits, per-row max of the 64-bit key (order-preserving bf16 bits << 32 | ~index)
-//              over the tile, one 64-bit atomic max per row and tile: the result does not depend
-//              on the order the workgroups finish in.
+//   lmh_gemm   256 x 256 output tile per workgroup (4 waves, 128 x 128 each, 32x32x32 int8 MFMAs
+//              with the weights as operand A, int32 accumulators in AGPRs), K in 64-byte steps
+//              through a 4-stage LDS ring filled by buffer loads straight into LDS, three steps
+//              ahead (no register staging).  Epilogue: bf16 logits, per-row max of the 64-bit key
+//              (order-preserving bf16 bits << 32 | ~index) over the tile, one 64-bit atomic max per
+//              row and tile: the result does not depend on the order the workgroups finish in.
 //   lmh_ids    key -> token id.
 // Block -> tile mapping: block b runs on XCD b % 8; the eight row tiles of one vocab tile are
 // consecutive blocks of the same XCD, so the weight tile is fetched from HBM once and served to
@@ -120,6 +120,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ __align__(1024) int8_t a_s0[kBM * kBK], a_s1[kBM * kBK], a_s2[kBM * kBK], a_s3[kBM * kBK];
   __shared__ __align__(1024) int8_t b_s0[kBN * kBK], b_s1[kBN * kBK], b_s2[kBN * kBK], b_s3[kBN * kBK];
   __shared__ uint32_t rkey[2][kBM];
+  __shared__ __align__(16) float ws_l[kBN];  // the tile's weight scales
   auto a_st = [&](auto st) -> int8_t* {
     if constexpr (decltype(st)::value == 0) return a_s0;
     else if constexpr (decltype(st)::value == 1) return a_s1;
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int b = blockIdx.x, xcd = b & 7, j = b >> 3;
   const int rt = j % nrt, vt = (j / nrt) * 8 + xcd;
   if (vt >= nvt) return;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves of 128 x 128
   const int r0 = rt * kBM, v0 = vt * kBN;
   // global -> LDS by buffer loads with the LDS bit (no registers; rows past R or V read as zero).
@@ -149,6 +150,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       (void*)(d.xq + (size_t)r0 * kLH), (short)0, min(d.R - r0, kBM) * kLH, 0x00020000);
   const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(d.wq + (size_t)v0 * kLH), (short)0, min(d.V - v0, kBN) * kLH, 0x00020000);
+  if (tid < kBN / 4)
+    *reinterpret_cast<float4*>(&ws_l[4 * tid]) =
+        v0 + 4 * tid < d.V ? *reinterpret_cast<const float4*>(d.ws + v0 + 4 * tid) : make_float4(0.f, 0.f, 0.f, 0.f);
   const int voff = (lane >> 2) * kLH + (((lane & 3) ^ ((lane >> 3) & 3)) << 4);
   const int wq4 = __builtin_amdgcn_readfirstlane(wave) * 4;
   auto issue_to = [&](int ks, int8_t* as, int8_t* bs) {
@@ -162,8 +166,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   auto issue = [&](int ks, auto st) { issue_to(ks, a_st(st), b_st(st)); };
   constexpr int NK = kLH / kBK;
   static_assert(NK % 4 == 0 && NK >= 8, "K steps");
-  const int fa = bswz(wm * 128 + lr, lgp), fb = bswz(wn * 128 + lr, lgp);  // + 16 kBK per fragment
-  v4i acc[8][8];
+  // 32x32x32 int8 MFMA (twice the rate of 16x16x64 on gfx950): the weight rows are operand A, the
+  // token rows operand B.  Lane l reads tile row 32 t + l % 32, K bytes 16 (l / 32) of each 32-byte
+  // half step (LDS chunk 2 h + l / 32); the result gives lane l token l % 32 and vocab rows
+  // 8 (j / 4) + 4 (l / 32) + j % 4 of register j.
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int fx0 = bswz(wm * 128 + l32, lh), fx1 = bswz(wm * 128 + l32, 2 + lh);  // + 32 kBK per tile
+  const int fw0 = bswz(wn * 128 + l32, lh), fw1 = bswz(wn * 128 + l32, 2 + lh);
+  v16i acc[4][4];  // [vocab tile][token tile]
   // One K step.  The wait leaves the 16 loads of steps ks + 1 and ks + 2 in flight, so this wave's
   // loads of step ks are in LDS and its LDS reads of step ks - 1 are done; after the barrier both
   // hold for all four waves.  Step ks + 3 then refills the stage step ks - 1 used (past the end the
@@ -177,20 +187,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     issue(min(ks + 3, NK - 1), nxt);
     const int8_t* as = a_st(cur);
     const int8_t* bs = b_st(cur);
-    v4i af[8], bfr[8];
+    v4i xf[2][4], wf[2][4];
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi) af[mi] = *reinterpret_cast<const v4i*>(as + fa + mi * 16 * kBK);
-#pragma unroll
-    for (int ni = 0; ni < 8; ++ni) bfr[ni] = *reinterpret_cast<const v4i*>(bs + fb + ni * 16 * kBK);
+    for (int t = 0; t < 4; ++t) {
+      xf[0][t] = *reinterpret_cast<const v4i*>(as + fx0 + t * 32 * kBK);
+      xf[1][t] = *reinterpret_cast<const v4i*>(as + fx1 + t * 32 * kBK);
+      wf[0][t] = *reinterpret_cast<const v4i*>(bs + fw0 + t * 32 * kBK);
+      wf[1][t] = *reinterpret_cast<const v4i*>(bs + fw1 + t * 32 * kBK);
+    }
     // all 16 fragment reads go out before the first MFMA (left alone, the scheduler reuses one
     // fragment register and waits out a full LDS latency per row of MFMAs)
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int ni = 0; ni < 8; ++ni)
-        acc[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-            af[mi], bfr[ni], decltype(first)::value ? v4i{0, 0, 0, 0} : acc[mi][ni], 0, 0, 0);
+      for (int vi = 0; vi < 4; ++vi)
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+          acc[vi][ti] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+              wf[h][vi], xf[h][ti], (decltype(first)::value && h == 0) ? v16i{} : acc[vi][ti], 0, 0, 0);
   };
   issue(0, ic<0>{});
   issue(1, ic<1>{});
@@ -206,50 +221,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     body(ks + 3, ic<3>{}, ic<2>{}, std::false_type{});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  // Epilogue: lane holds columns cb + ni*16 + lr and rows r0 + wm*128 + mi*16 + 4 lgp + q.  Each
-  // logit is rounded to bf16 once (hardware round-to-nearest-even); the lane keeps the first
-  // largest of its eight columns per row by a float compare (-0 == +0 as in the bf16 argmax); the
-  // 16 lanes of a row then combine a 32-bit key (order-preserving bf16 bits << 16 | 0xffff - column
-  // in the tile) by DPP max, the two column waves through LDS, and the tile through one 64-bit
-  // atomic max per row.  Column groups past V (V % 16 == 0) are wave-uniform and skipped.
-  const int cb = v0 + wn * 128;
-  const int nv = min(8, (d.V - cb) / 16);
-  float wsv[8];
+  // Epilogue: lane l holds tokens r0 + wm*128 + 32 ti + l % 32 and, per token, vocab columns
+  // cb + 32 vi + 8 (j / 4) + 4 (l / 32) + j % 4.  Each logit is rounded to bf16 once (hardware
+  // round-to-nearest-even) and folded into a 32-bit key (order-preserving bf16 bits << 16 |
+  // 0xffff - column in the tile; -0 and +0 share a key, as in the bf16 argmax): the lane's max key
+  // over its 64 columns, one exchange with lane l ^ 32, the two column waves through LDS, and the
+  // tile through one 64-bit atomic max per row.  Columns past V are skipped.
+  auto epilogue = [&](auto store, auto partial) {
 #pragma unroll
-  for (int ni = 0; ni < 8; ++ni) wsv[ni] = ni < nv ? d.ws[cb + ni * 16 + lr] : 0.f;
-  auto epilogue = [&](auto store) {
+    for (int ti = 0; ti < 4; ++ti) {
+      const int rl = wm * 128 + ti * 32 + l32;
+      const int row = r0 + rl;
+      const float xsr = row < d.R ? d.xs[row] : 0.f;
+      uint32_t best = 0u;
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi) {
+      for (int vi = 0; vi < 4; ++vi)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int rl = wm * 128 + mi * 16 + 4 * lgp + q;
-        const int row = r0 + rl;
-        const float xsr = row < d.R ? d.xs[row] : 0.f;
-        float best = -__builtin_inff();
-        int bi = 0;
+        for (int jg = 0; jg < 4; ++jg) {
+          const int cl = wn * 128 + vi * 32 + 8 * jg + 4 * lh;  // first of the 4 columns, in the tile
+          const float4 w4 = *reinterpret_cast<const float4*>(&ws_l[cl]);
+          const float wq[4] = {w4.x, w4.y, w4.z, w4.w};
+          float lg[4];
 #pragma unroll
-        for (int ni = 0; ni < 8; ++ni) {
-          const float lg = round_bf16(((float)acc[mi][ni][q] * xsr) * wsv[ni]);
-          if (ni < nv) {
-            if (lg > best) {
-              best = lg;
-              bi = ni;
-            }
-            if constexpr (decltype(store)::value)
-              if (row < d.R) d.logits[(size_t)row * d.V + cb + ni * 16 + lr] = (uint16_t)(__float_as_uint(lg) >> 16);
+          for (int q = 0; q < 4; ++q) {
+            lg[q] = round_bf16(((float)acc[vi][ti][4 * jg + q] * xsr) * wq[q]);
+            uint32_t b16 = __float_as_uint(lg[q] + 0.f) >> 16;
+            b16 = (b16 & 0x8000u) ? (~b16 & 0xffffu) : (b16 | 0x8000u);
+            const uint32_t key = (b16 << 16) | (0xffffu - (uint32_t)(cl + q));
+            if (!decltype(partial)::value || v0 + cl + q < d.V) best = max(best, key);
           }
+          if constexpr (decltype(store)::value)
+            if (row < d.R && v0 + cl < d.V)  // V % 16 == 0: the 4 columns are all in or all out
+              *reinterpret_cast<uint2*>(d.logits + (size_t)row * d.V + v0 + cl) =
+                  make_uint2((__float_as_uint(lg[0]) >> 16) | (__float_as_uint(lg[1]) & 0xffff0000u),
+                             (__float_as_uint(lg[2]) >> 16) | (__float_as_uint(lg[3]) & 0xffff0000u));
         }
-        uint32_t b16 = __float_as_uint(best + 0.f) >> 16;
-        b16 = (b16 & 0x8000u) ? (~b16 & 0xffffu) : (b16 | 0x8000u);
-        const uint32_t key = row16_max_u32((b16 << 16) | (0xffffu - (uint32_t)(wn * 128 + bi * 16 + lr)));
-        if (lr == 0) rkey[wn][rl] = key;
-      }
+      best = max(best, (uint32_t)__shfl_xor((int)best, 32));
+      if (lh == 0) rkey[wn][rl] = best;
     }
   };
-  if (d.logits)
-    epilogue(std::true_type{});
-  else
-    epilogue(std::false_type{});
+  // the column checks only in the last vocab tile
+  if (v0 + kBN <= d.V) {
+    if (d.logits)
+      epilogue(std::true_type{}, std::false_type{});
+    else
+      epilogue(std::false_type{}, std::false_type{});
+  } else {
+    if (d.logits)
+      epilogue(std::true_type{}, std::true_type{});
+    else
+      epilogue(std::false_type{}, std::true_type{});
+  }
   __syncthreads();
   if (r0 + tid < d.R) {
     const uint32_t k = max(rkey[0][tid], rkey[1][tid]);
@@ -294,9 +316,9 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
   Q36_REQUIRE(a->R >= 1 && a->R <= (1 << 20), "q36_lmhead_argmax: R=%d out of range", a->R);
   Q36_REQUIRE(a->V >= 16 && a->V % 16 == 0, "q36_lmhead_argmax: V=%d must be a positive multiple of 16", a->V);
   Q36_REQUIRE(a->h && a->wq && a->ws && a->ids && a->workspace, "q36_lmhead_argmax: a required pointer is null");
-  Q36_REQUIRE(aligned16(a->h) && aligned16(a->wq) && aligned16(a->norm_w) &&
+  Q36_REQUIRE(aligned16(a->h) && aligned16(a->wq) && aligned16(a->ws) && aligned16(a->norm_w) &&
                   (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0,
-              "q36_lmhead_argmax: h, wq, norm_w must be 16-byte and workspace 256-byte aligned");
+              "q36_lmhead_argmax: h, wq, ws, norm_w must be 16-byte and workspace 256-byte aligned");
   const LmhWs L = lmh_ws(a->R);
   Q36_REQUIRE(a->workspace_bytes >= L.total, "q36_lmhead_argmax: workspace of %zu bytes < %zu required",
               a->workspace_bytes, L.total);
