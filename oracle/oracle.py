@@ -60,6 +60,12 @@ class OprojArgs(C.Structure):
     _fields_ = [("T", I32), ("attn", P), ("gate", P), ("wo", P), ("so", P), ("out", P), ("n_threads", I32)]
 
 
+class DecodeArgs(C.Structure):
+    _fields_ = [("B", I32), ("NT", I32), ("HQ", I32), ("HKV", I32), ("D", I32), ("q", P), ("kcache", P),
+                ("vcache", P), ("page_table", P), ("pt_stride", I32), ("seqlens", P), ("scale", C.c_float),
+                ("out", P), ("n_threads", I32)]
+
+
 class LmheadArgs(C.Structure):
     _fields_ = [("R", I32), ("H", I32), ("V", I32), ("h", P), ("norm_w", P), ("eps", C.c_float), ("wq", P),
                 ("ws", P), ("ids", P), ("logits", P), ("n_threads", I32)]
@@ -76,6 +82,8 @@ def _declare(L):
     L.q36o_e4m3_to_f32.argtypes = [C.c_uint8]
     L.q36o_expf.restype = C.c_float
     L.q36o_expf.argtypes = [C.c_float]
+    L.q36o_f16_round.restype = C.c_float
+    L.q36o_f16_round.argtypes = [C.c_float]
     L.q36o_dot_canon.restype = C.c_float
     L.q36o_dot_canon.argtypes = [P, P, I32]
     L.q36o_quant_rows_i8.argtypes = [P, I32, I32, P, P]
@@ -84,7 +92,7 @@ def _declare(L):
     L.q36o_route.restype = I32
     L.q36o_route.argtypes = [P, P, P, P, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P]
     for fn, st in (("q36o_moe", MoeArgs), ("q36o_gdn_verify", GdnArgs), ("q36o_attn_proj", AttnArgs),
-                   ("q36o_attn_oproj", OprojArgs), ("q36o_lmhead", LmheadArgs)):
+                   ("q36o_attn_oproj", OprojArgs), ("q36o_lmhead", LmheadArgs), ("q36o_attn_decode", DecodeArgs)):
         f = getattr(L, fn)
         f.restype = I32
         f.argtypes = [C.POINTER(st)]
@@ -278,3 +286,28 @@ def lmhead(h, norm_w, eps, wq, ws, want_logits=False, n_threads=0):
     if lib().q36o_lmhead(C.byref(a)):
         raise ValueError("q36o_lmhead failed")
     return ids, logits
+
+
+# ---------------------------------------------------------------- decode attention
+def attn_decode(q, kcache, vcache, page_table, seqlens, NT, scale, n_threads=0):
+    """q bf16 bits [B*NT, HQ, D]; caches e4m3 codes [slots, HKV, D]; page_table int32 [B, L];
+    seqlens int32 [B] -> bf16 bits [B*NT, HQ, D]."""
+    q = np.ascontiguousarray(q, np.uint16)
+    kcache = np.ascontiguousarray(kcache, np.uint8)
+    vcache = np.ascontiguousarray(vcache, np.uint8)
+    page_table = np.ascontiguousarray(page_table, np.int32)
+    seqlens = np.ascontiguousarray(seqlens, np.int32)
+    T, HQ, D = q.shape
+    B = seqlens.shape[0]
+    HKV = kcache.shape[1]
+    out = np.empty_like(q)
+    a = DecodeArgs(B, NT, HQ, HKV, D, _p(q), _p(kcache), _p(vcache), _p(page_table), page_table.shape[1],
+                   _p(seqlens), scale, _p(out), n_threads)
+    if lib().q36o_attn_decode(C.byref(a)):
+        raise ValueError("q36o_attn_decode failed")
+    return out
+
+
+def f16_round(x):
+    L = lib()
+    return np.array([L.q36o_f16_round(float(v)) for v in np.ravel(x)], np.float32).reshape(np.shape(x))

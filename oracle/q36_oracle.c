@@ -673,6 +673,77 @@ int q36o_attn_oproj(const q36o_oproj_args* a) {
 }
 
 /* ------------------------------------------------------------------------------------ */
+/* decode / verify attention                                                            */
+/* ------------------------------------------------------------------------------------ */
+
+/* IEEE binary16 round-to-nearest-even of a float, returned as the float it represents (normal
+ * and subnormal range; |x| above the f16 maximum saturates, which softmax weights in [0, 1] never
+ * reach). */
+float q36o_f16_round(float x) {
+  uint32_t u = f2u(x), sign = u & 0x80000000u;
+  float ax = fabsf(x);
+  if (!(ax == ax)) return x;
+  if (ax >= 65504.f) return u2f(sign | f2u(65504.f));
+  if (ax < 6.103515625e-05f) {  /* below 2^-14: a multiple of the subnormal step 2^-24 */
+    double q = (double)ax * 16777216.0, f = floor(q), r = q - f;
+    if (r > 0.5 || (r == 0.5 && fmod(f, 2.0) != 0.0)) f += 1.0;
+    return u2f(sign | f2u((float)(f / 16777216.0)));
+  }
+  uint32_t a = f2u(ax), lsb = (a >> 13) & 1u, rest = a & 0x1fffu;
+  a &= ~0x1fffu;
+  if (rest > 0x1000u || (rest == 0x1000u && lsb)) a += 0x2000u;
+  return u2f(sign | a);
+}
+
+/* Attention of each query token over its request's keys, the restatement of the verify kernel's
+ * arithmetic (L/qk_attn_verify.cu:156-208 q -> e4m3, :233-337 scores and softmax, :480-560 P V with
+ * f16 weights, :560-600 the normalised output): query token t of request r sees key positions
+ * 0 .. seqlens[r] - NT + t (the causal rule among the NT new tokens); q head i reads kv head
+ * i / (HQ / HKV).  s_k = (sum_d e4m3(q)_d k_d) * scale exactly, p_k = exp(s_k - max s), the P V
+ * product uses p_k rounded to f16 and the normaliser the unrounded p_k: out = bf16(sum p16 v / sum p).
+ * The sums are exact (double); the kernel's split / online order is a rounding difference. */
+int q36o_attn_decode(const q36o_decode_args* a) {
+  const int B = a->B, NT = a->NT, HQ = a->HQ, HKV = a->HKV, D = a->D, G = HQ / HKV;
+  if (HQ % HKV || NT < 1) return -1;
+  if (a->n_threads > 0) omp_set_num_threads(a->n_threads);
+#pragma omp parallel for collapse(3) schedule(dynamic)
+  for (int r = 0; r < B; ++r)
+    for (int t = 0; t < NT; ++t)
+      for (int i = 0; i < HQ; ++i) {
+        const int h = i / G, nk = a->seqlens[r] - NT + t + 1;
+        const uint16_t* qr = a->q + (((size_t)r * NT + t) * HQ + i) * D;
+        uint16_t* o = a->out + (((size_t)r * NT + t) * HQ + i) * D;
+        if (nk <= 0) {
+          for (int d = 0; d < D; ++d) o[d] = 0;
+          continue;
+        }
+        float* q8 = (float*)malloc(sizeof(float) * D);
+        double* sc = (double*)malloc(sizeof(double) * nk);
+        double* acc = (double*)calloc(D, sizeof(double));
+        for (int d = 0; d < D; ++d) q8[d] = q36o_e4m3_to_f32(q36o_f32_to_e4m3(q36o_bf16_to_f32(qr[d])));
+        double mx = -INFINITY;
+        for (int k = 0; k < nk; ++k) {
+          const uint8_t* kr = a->kcache + ((size_t)a->page_table[(size_t)r * a->pt_stride + k] * HKV + h) * D;
+          double dot = 0.0;
+          for (int d = 0; d < D; ++d) dot += (double)q8[d] * (double)q36o_e4m3_to_f32(kr[d]);
+          sc[k] = (double)(float)dot * (double)a->scale;
+          if (sc[k] > mx) mx = sc[k];
+        }
+        double l = 0.0;
+        for (int k = 0; k < nk; ++k) {
+          const double p = exp(sc[k] - mx);
+          const double p16 = (double)q36o_f16_round((float)p);
+          l += p;
+          const uint8_t* vr = a->vcache + ((size_t)a->page_table[(size_t)r * a->pt_stride + k] * HKV + h) * D;
+          for (int d = 0; d < D; ++d) acc[d] += p16 * (double)q36o_e4m3_to_f32(vr[d]);
+        }
+        for (int d = 0; d < D; ++d) o[d] = q36o_f32_to_bf16((float)(acc[d] / l));
+        free(q8); free(sc); free(acc);
+      }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------------------ */
 /* int8 lm_head + argmax                                                                */
 /* ------------------------------------------------------------------------------------ */
 

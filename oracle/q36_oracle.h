@@ -140,6 +140,22 @@ typedef struct {
 } q36o_lmhead_args;
 int q36o_lmhead(const q36o_lmhead_args* a);
 
+/* ---- decode / verify attention over an e4m3 KV cache ---- */
+typedef struct {
+  int B, NT, HQ, HKV, D;            /* requests, query tokens per request, q heads, kv heads, head dim */
+  const uint16_t* q;                /* bf16 [B*NT, HQ, D]: normed and roped queries */
+  const uint8_t* kcache;            /* e4m3 [slots, HKV, D] */
+  const uint8_t* vcache;            /* e4m3 [slots, HKV, D] */
+  const int32_t* page_table;        /* [B, pt_stride]: the cache slot of key position i */
+  int pt_stride;
+  const int32_t* seqlens;           /* [B]: key positions per request, the NT new ones included */
+  float scale;                      /* softmax scale */
+  uint16_t* out;                    /* bf16 [B*NT, HQ, D] */
+  int n_threads;
+} q36o_decode_args;
+int q36o_attn_decode(const q36o_decode_args* a);
+float q36o_f16_round(float x);
+
 #ifdef __cplusplus
 }
 #endif
