@@ -55,6 +55,13 @@ class LmheadArgs(C.Structure):
                 ("ws", P), ("ids", P), ("logits", P), ("workspace", P), ("workspace_bytes", SZ)]
 
 
+class DecodeArgs(C.Structure):
+    _fields_ = [("B", I32), ("NT", I32), ("HQ", I32), ("HKV", I32), ("D", I32), ("splits", I32), ("q", P),
+                ("k_cache", P), ("v_cache", P), ("num_slots", C.c_int64), ("page_table", P), ("pt_stride", I32),
+                ("seqlens", P), ("out_loc", P), ("k_new", P), ("v_new", P), ("scale", C.c_float), ("out", P),
+                ("workspace", P), ("workspace_bytes", SZ)]
+
+
 _lib = None
 
 # (name, restype, argtypes) of every exported symbol; tests check that each one resolves.
@@ -73,6 +80,8 @@ SYMBOLS = [
     ("q36_oproj_workspace_bytes", SZ, [I32]),
     ("q36_attn_proj", I32, [C.POINTER(AttnArgs), P]),
     ("q36_attn_oproj", I32, [C.POINTER(OprojArgs), P]),
+    ("q36_attn_decode_workspace_bytes", SZ, [I32, I32]),
+    ("q36_attn_decode", I32, [C.POINTER(DecodeArgs), P]),
     ("q36_lmhead_workspace_bytes", SZ, [I32]),
     ("q36_lmhead_argmax", I32, [C.POINTER(LmheadArgs), P]),
     ("q36_quant_rows_i8", I32, [P, C.c_int64, I32, P, P, P]),

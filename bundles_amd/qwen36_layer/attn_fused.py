@@ -1,9 +1,11 @@
-"""Fused gated full-attention projections on libq36 (q36_attn_proj, q36_attn_oproj).
+"""Fused gated full attention on libq36 (q36_attn_proj, q36_attn_decode, q36_attn_oproj).
 
 Mirrors the reference's attention glue (R = qwen36_nodes_kb34, L = R/qwen36_layer): the fused
 qkv projection + q/k norm + partial RoPE + e4m3 KV write (L/attn_fused.py:232-273,
-L/qk_attn_verify.cu:765-797 attn_prefill_front) and the gated o_proj input
-(L/qk_attn_verify.cu:730-737).  Weights are e4m3 with 128x128 block scales (prepare_weights).
+L/qk_attn_verify.cu:765-797 attn_prefill_front), the decode / verify attention over the e4m3
+KV cache with its split count (L/attn_fused.py:110-124 attn_verify_fused, L/qk_attn_verify.cu:354-760)
+and the gated o_proj input (L/qk_attn_verify.cu:730-737).  Weights are e4m3 with 128x128 block
+scales (prepare_weights).
 """
 from __future__ import annotations
 
@@ -13,7 +15,7 @@ from dataclasses import dataclass
 import torch
 
 from .. import _lib
-from .._lib import AttnArgs, OprojArgs, check, ptr
+from .._lib import AttnArgs, DecodeArgs, OprojArgs, check, ptr
 from .moe import quantize_blocks_e4m3
 
 N_Q_HEADS, N_KV_HEADS, HEAD_DIM, HIDDEN = 16, 2, 256, 2048
@@ -85,4 +87,45 @@ def attn_oproj(attn, gate, w: AttnWeights, ws: Workspace, out=None, stream=None)
     out = torch.empty((T, HIDDEN), dtype=torch.bfloat16, device=attn.device) if out is None else out
     a = OprojArgs(T, ptr(attn), ptr(gate), ptr(w.wo_p), ptr(w.so), ptr(out), ptr(ws.oproj), ws.oproj.numel())
     check(_lib.lib().q36_attn_oproj(C.byref(a), _lib.stream_handle(stream)), "q36_attn_oproj")
+    return out
+
+
+class DecodeWorkspace:
+    """Split partials of q36_attn_decode for up to B_max requests at a fixed split count
+    (0 = the library's default min(64, CUs / (B * 2)), resolved per call: the buffer is sized for
+    the largest count any B <= B_max can take)."""
+
+    def __init__(self, B_max: int, device, splits: int = 0):
+        L = _lib.lib()
+        self.B_max, self.splits = B_max, splits
+        need = max(L.q36_attn_decode_workspace_bytes(b, splits) for b in range(1, B_max + 1))
+        self.buf = torch.empty(need, dtype=torch.uint8, device=device)
+
+
+def attn_decode(q, k_cache, v_cache, page_table, seqlens, NT: int, scale: float, ws: DecodeWorkspace,
+                out_loc=None, k_new=None, v_new=None, out=None, stream=None):
+    """Attention of B requests' NT new tokens over the e4m3 KV cache (one-token pages).
+
+    q bf16 [B*NT, 16, 256]; k_cache / v_cache e4m3 codes (uint8) [slots, 2, 256]; page_table int32
+    [B, >= max seqlens]; seqlens int32 [B] (new tokens included).  With out_loc (int64 [B*NT]) the
+    new tokens' k_new / v_new rows are written into the cache first.  Returns bf16 [B*NT, 16, 256]
+    = softmax(scale * e4m3(q) k^T) V per query head, causal among the new tokens, not gated.
+    """
+    T = q.shape[0]
+    if T % NT:
+        raise ValueError(f"attn_decode: {T} query rows are not a multiple of NT={NT}")
+    B = T // NT
+    if B > ws.B_max:
+        raise ValueError(f"attn_decode: {B} requests exceed the workspace's {ws.B_max}")
+    for name, t, dt in (("q", q, torch.bfloat16), ("k_cache", k_cache, torch.uint8), ("v_cache", v_cache, torch.uint8),
+                        ("page_table", page_table, torch.int32), ("seqlens", seqlens, torch.int32)):
+        if t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"attn_decode: {name} must be a contiguous {dt} tensor")
+    if out_loc is not None and (out_loc.dtype != torch.int64 or k_new is None or v_new is None):
+        raise ValueError("attn_decode: out_loc must be int64 and comes with k_new and v_new")
+    out = torch.empty_like(q) if out is None else out
+    a = DecodeArgs(B, NT, q.shape[1], k_cache.shape[1], q.shape[2], ws.splits, ptr(q), ptr(k_cache), ptr(v_cache),
+                   k_cache.shape[0], ptr(page_table), page_table.shape[1], ptr(seqlens), ptr(out_loc), ptr(k_new),
+                   ptr(v_new), scale, ptr(out), ptr(ws.buf), ws.buf.numel())
+    check(_lib.lib().q36_attn_decode(C.byref(a), _lib.stream_handle(stream)), "q36_attn_decode")
     return out

@@ -206,6 +206,37 @@ size_t q36_oproj_workspace_bytes(int32_t T);
 int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream);
 int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream);
 
+/* ---- Decode / verify attention over the e4m3 KV cache: replaces attn_verify_kernel
+ * (L/qk_attn_verify.cu:354-760) with its split count (L/attn_fused.py:110-124) ----
+ * q bf16 [B*NT, HQ, D] (normed, roped, as q36_attn_proj writes it); k_cache, v_cache e4m3
+ * [num_slots, HKV, D]; page_table int32 [B, pt_stride]: the cache slot of key position i (one-token
+ * pages); seqlens int32 [B]: key positions of each request, its NT new tokens included (query token t
+ * sees positions 0 .. seqlens - NT + t).  out_loc (optional) int64 [B*NT]: the slots the new tokens'
+ * K/V rows (k_new, v_new e4m3 [B*NT, HKV, D], q36_attn_proj's k8 / v8) are written to first.
+ * Scores s = (e4m3(q) . k) * scale, softmax weights rounded to f16 for P V, V widened to f16.
+ * out bf16 [B*NT, HQ, D] = bf16(o / l), not gated (the o_proj applies the sigmoid gate).
+ * splits: 0 = min(64, CUs / (B * HKV)).  Constraints: HQ = 16, HKV = 2, D = 256, 1 <= NT <= 4,
+ * num_slots * HKV * D < 2^31; q, caches 16-byte aligned. */
+typedef struct q36_decode_args {
+  int32_t B, NT, HQ, HKV, D, splits;
+  const void* q;
+  void* k_cache;
+  void* v_cache;
+  int64_t num_slots;
+  const int32_t* page_table;
+  int32_t pt_stride;
+  const int32_t* seqlens;
+  const int64_t* out_loc;
+  const void* k_new;
+  const void* v_new;
+  float scale;
+  void* out;
+  void* workspace;
+  size_t workspace_bytes;
+} q36_decode_args;
+size_t q36_attn_decode_workspace_bytes(int32_t B, int32_t splits);
+int q36_attn_decode(const q36_decode_args* a, q36_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------
  * Int8 lm_head fused with greedy argmax (H/w8a8.py:116-120 w8a8_linear + the stock argmax,
  * H/node.py:136-151).  h bf16 [R, H] (H = 2048) -> optional final Gemma RMSNorm (norm_w bf16 [H],

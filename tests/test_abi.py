@@ -41,7 +41,8 @@ def test_every_declared_symbol_is_exported(L):
 def test_struct_layouts_match_header(tmp_path):
     from bundles_amd import _lib
     structs = {"q36_moe_args": _lib.MoeArgs, "q36_moe_ws_layout": _lib.MoeWsLayout, "q36_gdn_args": _lib.GdnArgs,
-               "q36_attn_args": _lib.AttnArgs, "q36_oproj_args": _lib.OprojArgs, "q36_lmhead_args": _lib.LmheadArgs}
+               "q36_attn_args": _lib.AttnArgs, "q36_oproj_args": _lib.OprojArgs, "q36_lmhead_args": _lib.LmheadArgs,
+               "q36_decode_args": _lib.DecodeArgs}
     hdr = open(HEADER).read()
     structs = {k: v for k, v in structs.items() if f"typedef struct {k}" in hdr}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
@@ -80,6 +81,15 @@ def test_invalid_arguments_are_rejected(L):
     g.B, g.T = 2, 9
     assert L.q36_gdn_verify(C.byref(g), None) == _lib.Q36_EINVAL
     assert b"T=9" in L.q36_last_error()
+    d = _lib.DecodeArgs()
+    d.B, d.NT, d.HQ, d.HKV, d.D = 4, 4, 32, 4, 128
+    assert L.q36_attn_decode(C.byref(d), None) == _lib.Q36_EINVAL
+    assert b"HQ=32" in L.q36_last_error()
+    d.HQ, d.HKV, d.D, d.NT = 16, 2, 256, 5
+    assert L.q36_attn_decode(C.byref(d), None) == _lib.Q36_EINVAL
+    assert b"NT=5" in L.q36_last_error()
+    d.NT = 4
+    assert L.q36_attn_decode(C.byref(d), None) == _lib.Q36_EINVAL  # null pointers
 
 
 def test_workspace_layout_is_consistent(L):
