@@ -11,15 +11,18 @@
 //
 // Kernels:
 //   kv_scatter      the new tokens' e4m3 K and V rows into the cache slots out_loc[t].
-//   decode_split    workgroup = (split, KV head, request), 4 waves; the 32 query rows (4 tokens x 8
-//                   heads) of the group against 64-key tiles of the split's key range.  Scores:
-//                   wave w takes keys 16 w .. of the tile, e4m3 16x16x128 MFMA of the query
-//                   fragments (registers, whole kernel) and the keys (straight from the cache by
-//                   page table).  Softmax: tile row max through LDS, online rescale, weights
-//                   rounded to f16 into LDS.  P V: wave w owns dims 64 w ..; f16 16x16x32 MFMA, V
-//                   staged in LDS by buffer DMA (16-byte pieces XOR-swizzled by key) and read
-//                   key-major with the LDS transpose read, widened e4m3 -> f16 (exact).  The next
-//                   tile's keys and values are requested while this one computes.
+//   decode_split    workgroup = (split, KV head, request), 4 independent waves; each wave streams
+//                   its own contiguous run of 32-key steps for the group's 8 query heads x NT tokens
+//                   (16 or 32 query rows) with its own running max / weight sum / output, and the
+//                   four are merged once at the end.  Scores S^T = K Q^T: e4m3 16x16x128 MFMA with
+//                   the keys as operand A straight from the cache (registers) and the e4m3 query
+//                   fragments as operand B, so a lane holds one query row: the row max needs two
+//                   cross-lane steps and the output rescale is one factor per lane.  O^T += V^T P^T:
+//                   f16 16x16x32 MFMA, V^T read from LDS with the transpose read (V rows staged by
+//                   buffer DMA in the key order the lane's weights are in), P^T the lane's own
+//                   weights rounded to f16.  Keys, values and page-table entries stream through a
+//                   4-stage per-wave pipeline with no workgroup barrier; the output is rescaled only
+//                   when a row max grows by more than 2^8 (weights up to 2^8 are exact in f16).
 //   decode_combine  per (request, KV head): the splits' partials weighted by exp2(m_s - M) / L.
 #include <math.h>
 
@@ -31,11 +34,19 @@
 namespace q36 {
 namespace {
 
-constexpr int kQH = 16, kKVH = 2, kDD = 256, kGQ = kQH / kKVH, kDNT = 4, kDRows = kGQ * kDNT, kKT = 64;
-constexpr int kPRow = kKT * 2 + 16;  // P row in LDS: 64 f16 weights + 16 bytes (16 rows on distinct banks)
+constexpr int kQH = 16, kKVH = 2, kDD = 256, kGQ = kQH / kKVH, kDNT = 4, kDRows = kGQ * kDNT;
+constexpr int kST = 32;              // keys per wave step
+constexpr int kNS = 3;               // key / value stages per wave (steps in flight + 1)
+constexpr int kPTD = 2 * kNS;        // page-table lookahead in steps
+constexpr int kPTR = 8;              // page-table ring entries per wave (one step each)
+constexpr int kVS = 4 * kST * kDD;   // one stage of the four waves' value rows (32 KB)
+constexpr float kLazy = 8.f;         // rescale when a row max grows past the reference by 2^8
+static_assert(kPTR >= kPTD && (kPTR & (kPTR - 1)) == 0, "page-table ring");
+static_assert(kVS == 2 * 16 * kDD * 4, "a stage holds two waves' fp32 output of one row tile at the merge");
+static_assert(kNS == 3, "the stage arrays and the prologue are written out for three stages");
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef float v2f __attribute__((ext_vector_type(2)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 struct DecodeDev {
   int B, NT, splits, pt_stride;
@@ -58,13 +69,23 @@ __device__ __forceinline__ v8i cat8d(v4i a, v4i b) {
   v8i r = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   return r;
 }
-// 8 e4m3 codes (two words) -> 8 f16 (every e4m3 value is an f16 value: exact)
+// 8 e4m3 codes (two words) -> 8 f16 (every e4m3 value is an f16 value: exact at scale 1)
 __device__ __forceinline__ v8h widen8(int w0, int w1) {
-  const v2f a = __builtin_amdgcn_cvt_pk_f32_fp8(w0, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(w0, true);
-  const v2f c = __builtin_amdgcn_cvt_pk_f32_fp8(w1, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(w1, true);
-  v8h r = {(_Float16)a.x, (_Float16)a.y, (_Float16)b.x, (_Float16)b.y,
-           (_Float16)c.x, (_Float16)c.y, (_Float16)d.x, (_Float16)d.y};
-  return r;
+  const v2h a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.f, false);
+  const v2h b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.f, true);
+  const v2h c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.f, false);
+  const v2h e = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.f, true);
+  return v8h{a.x, a.y, b.x, b.y, c.x, c.y, e.x, e.y};
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) uint8_t*)p);
+}
+// LDS read by asm: the compiler counts the buffer DMA into the same array as a pending write and
+// would wait for every load in flight; the caller waits (lgkmcnt) before using the value.
+__device__ __forceinline__ int lds_ld32_asm(const void* p) {
+  int v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+  return v;
 }
 
 __global__ __launch_bounds__(256) void kv_scatter_kernel(const uint8_t* k8, const uint8_t* v8, const int64_t* loc, int T,
@@ -79,23 +100,31 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(const uint8_t* k8, cons
   *reinterpret_cast<v4i*>((isv ? vc : kc) + dst) = *reinterpret_cast<const v4i*>((isv ? v8 : k8) + src);
 }
 
-__global__ __launch_bounds__(256) void decode_split_kernel(DecodeDev d) {
-  __shared__ __align__(16) uint8_t vbuf0[kKT * kDD];
-  __shared__ __align__(16) uint8_t vbuf1[kKT * kDD];
-  __shared__ __align__(16) uint8_t ps[kDRows * kPRow];
-  __shared__ float red_m[4][kDRows], red_l[4][kDRows];
+template <int RT>
+__global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
+  __shared__ __align__(16) uint8_t vs0[kVS];
+  __shared__ __align__(16) uint8_t vs1[kVS];
+  __shared__ __align__(16) uint8_t vs2[kVS];
+  __shared__ __align__(16) int32_t ptl[4][kPTR][64];
+  __shared__ float mw[4][kDRows], lwv[4][kDRows];
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z, S = d.splits;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
   const int NT = d.NT, nk = d.seqlens[b], npre = nk - NT;
-  const int tiles = (nk + kKT - 1) / kKT, per = tiles / S, rem = tiles % S;
-  const int t0 = s * per + min(s, rem), t1 = t0 + per + (s < rem ? 1 : 0);
+  // steps of the request, the split's share (contiguous), the wave's share of that
+  const int steps = nk > 0 ? (nk + kST - 1) / kST : 0, per = steps / S, rem = steps % S;
+  const int st0 = s * per + min(s, rem), nst = per + (s < rem ? 1 : 0);
+  const int ws0 = st0 + (wave * nst) / 4, ws1 = st0 + ((wave + 1) * nst) / 4;
+  const int kbeg = ws0 * kST, kend = min(ws1 * kST, nk);  // the wave's keys [kbeg, kend)
+  const int npad = (ws1 - ws0 + kNS - 1) / kNS * kNS;     // steps run (a multiple of the stages)
   const int grp = (b * kKVH + h) * S + s;
-  // query fragments (score MFMA operand A): row 16 rt + l16 = token (row / 8), head h*8 + row % 8;
-  // dims 128 kb + 32 lg .. +31 rounded to e4m3 (rows of tokens past NT are zero)
-  v8i qa[2][2];
+  // query fragments (score operand B): column 16 rt + l16 = query row (token row / 8, head
+  // h * 8 + row % 8), dims 128 kb + 32 lg .. +31 rounded to e4m3; rows of tokens past NT are zero
+  v8i qb[RT][2];
+  int lim[RT];  // the row's last visible key (-1: none): causal among the new tokens, wave range
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
     const int row = 16 * rt + l16, t = row >> 3;
+    lim[rt] = t < NT ? min(kend - 1, npre + t) : -1;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       int w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -110,7 +139,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeDev d) {
                                  (f2e4m3x2_hw(bf_lo((uint32_t)raw[2 * j + 1]), bf_hi((uint32_t)raw[2 * j + 1])) << 16));
         }
       }
-      qa[rt][kb] = v8i{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]};
+      qb[rt][kb] = v8i{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]};
     }
   }
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)d.kc, (short)0, (int)d.kv_bytes, 0x00020000);
@@ -118,156 +147,210 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeDev d) {
   // the request's page-table row through a bounded buffer (an entry past the row reads as slot 0)
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(d.pt + (size_t)b * d.pt_stride), (short)0, 4 * d.pt_stride, 0x00020000);
-  auto ptr_at = [&](int key) { return __builtin_amdgcn_raw_buffer_load_b32(prs, 4 * key, 0, 0); };
-  // per-lane state for rows 16 rt + 4 lg + r (index 4 rt + r): running max, this wave's weight sum
-  float m[8], lw[8];
+  int32_t* ring = &ptl[wave][0][0];
+  // Page-table entries of step j into ring entry j % 8 (lanes 32..63 repeat lanes 0..31).  Keys past
+  // the wave's range take the slot of its last key: their loads are repeats that stay in L2, their
+  // scores are masked and their values are real cache rows (finite), so 0 * V stays 0.
+  auto pt_dma = [&](int j) {
+    const int key = max(min(kbeg + kST * j + (lane & 31), kend - 1), 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(prs, ring + (j & (kPTR - 1)) * 64, 4, 4 * key, 0, 0, 0);
+  };
+  // Step j into stage Q: the 32 keys' rows as score operand A (kf[Q][kt]: key 16 kt + l16, dims
+  // 128 half + 32 lg ..), and the 32 value rows into the wave's LDS rows: DMA call m writes rows
+  // 4 m .. 4 m + 3 with key 16 (m & 1) + 4 (m >> 1) + (row % 4), so rows 8 g .. 8 g + 7 hold keys
+  // 4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3 (the order of lane group g's weights); 16-byte
+  // piece p of row r sits at position p ^ (r % 16).
+  v4i kf[kNS][2][4];
+  auto stage = [&](auto qc) -> uint8_t* {
+    constexpr int Q = decltype(qc)::value;
+    return (Q == 0 ? vs0 : Q == 1 ? vs1 : vs2) + wave * (kST * kDD);
+  };
+  auto fetch = [&](int j, auto qc) {
+    constexpr int Q = decltype(qc)::value;
+    const int32_t* e = ring + (j & (kPTR - 1)) * 64;
+    int ks0 = lds_ld32_asm(e + l16), ks1 = lds_ld32_asm(e + 16 + l16);
+    int vsl0 = lds_ld32_asm(e + lg), vsl1 = lds_ld32_asm(e + 16 + lg), vsl2 = lds_ld32_asm(e + 4 + lg),
+        vsl3 = lds_ld32_asm(e + 20 + lg), vsl4 = lds_ld32_asm(e + 8 + lg), vsl5 = lds_ld32_asm(e + 24 + lg),
+        vsl6 = lds_ld32_asm(e + 12 + lg), vsl7 = lds_ld32_asm(e + 28 + lg);
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(ks0), "+v"(ks1), "+v"(vsl0), "+v"(vsl1), "+v"(vsl2), "+v"(vsl3), "+v"(vsl4), "+v"(vsl5),
+                   "+v"(vsl6), "+v"(vsl7)::"memory");
+    const int kb0 = (ks0 * kKVH + h) * kDD + 32 * lg, kb1 = (ks1 * kKVH + h) * kDD + 32 * lg;
+    kf[Q][0][0] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0, 0, 0);
+    kf[Q][0][1] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0 + 16, 0, 0);
+    kf[Q][0][2] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0 + 128, 0, 0);
+    kf[Q][0][3] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0 + 144, 0, 0);
+    kf[Q][1][0] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1, 0, 0);
+    kf[Q][1][1] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1 + 16, 0, 0);
+    kf[Q][1][2] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1 + 128, 0, 0);
+    kf[Q][1][3] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1 + 144, 0, 0);
+    uint8_t* vb = stage(qc);
+    const int vsl[8] = {vsl0, vsl1, vsl2, vsl3, vsl4, vsl5, vsl6, vsl7};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    m[i] = -INFINITY;
-    lw[i] = 0.f;
+    for (int m = 0; m < 8; ++m) {
+      const int row = 4 * m + lg;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vb + 4 * m * kDD, 16,
+                                               (vsl[m] * kKVH + h) * kDD + 16 * (l16 ^ (row & 15)), 0, 0, 0);
+    }
+  };
+  // per-lane state: running max (base 2) of query row 16 rt + l16, the lane's share of its weight
+  // sum, and O^T (lane: row 16 rt + l16, dims 16 dt + 4 lg + r)
+  float m[RT], l[RT];
+  v4f o[RT][16];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    m[rt] = -INFINITY;
+    l[rt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) o[rt][dt] = v4f{0.f, 0.f, 0.f, 0.f};
   }
-  v4f o[2][4];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[rt][dt] = v4f{0.f, 0.f, 0.f, 0.f};
-  // Requests of tile it into buffer set Q (registers kf[Q], LDS vbuf_Q): the wave's 16 keys (score
-  // operand B: key 16 w + l16, dims 128 kb + 32 lg ..) and its 16 value rows (4 calls of 4 keys;
-  // lane l: key 4 c + l / 16, position l16 holds piece l16 ^ key % 16).  The page-table entry of a
-  // tile is loaded one tile earlier, so a fetch never waits on it.
-  v4i kf[2][4];
-  auto key_of = [&](int it) { return min(it * kKT + 16 * wave + l16, nk - 1); };
-  auto fetch = [&](int it, int slot, auto qc) {
+  auto compute = [&](int j, auto qc) {
     constexpr int Q = decltype(qc)::value;
-    (void)it;
-    const int kbase = (slot * kKVH + h) * kDD + 32 * lg;
-    kf[Q][0] = __builtin_amdgcn_raw_buffer_load_b128(krs, kbase, 0, 0);
-    kf[Q][1] = __builtin_amdgcn_raw_buffer_load_b128(krs, kbase + 16, 0, 0);
-    kf[Q][2] = __builtin_amdgcn_raw_buffer_load_b128(krs, kbase + 128, 0, 0);
-    kf[Q][3] = __builtin_amdgcn_raw_buffer_load_b128(krs, kbase + 144, 0, 0);
-    uint8_t* vb = Q ? vbuf1 : vbuf0;
+    v4f sc[RT][2];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int kl = 16 * wave + 4 * c + lg;       // key within the tile
-      const int vslot = __shfl(slot, 4 * c + lg);  // lane 4 c + lg holds that key's slot
-      const int voff = (vslot * kKVH + h) * kDD + 16 * (l16 ^ (kl & 15));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vb + (16 * wave + 4 * c) * kDD, 16, voff, 0, 0, 0);
-    }
-  };
-  int slot_next = ptr_at(key_of(min(t0 + 1, max(t1 - 1, t0))));
-  if (t0 < t1) fetch(t0, ptr_at(key_of(t0)), std::integral_constant<int, 0>{});
-  auto step = [&](int it, auto qc) {
-    constexpr int Q = decltype(qc)::value;
-    const bool more = it + 1 < t1;
-    // scores of the wave's 16 keys for the 32 rows
-    v4f sr[2];
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      sr[rt] = mfma_e4m3(qa[rt][0], cat8d(kf[Q][0], kf[Q][1]), v4f{0.f, 0.f, 0.f, 0.f});
-      sr[rt] = mfma_e4m3(qa[rt][1], cat8d(kf[Q][2], kf[Q][3]), sr[rt]);
-    }
-    const int key = it * kKT + 16 * wave + l16;
-    float sv[8];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * rt + 4 * lg + r, t = row >> 3;
-        const bool ok = t < NT && key <= npre + t;  // key < nk follows
-        sv[4 * rt + r] = ok ? sr[rt][r] * d.scale_log2 : -INFINITY;
+      for (int kt = 0; kt < 2; ++kt) {
+        sc[rt][kt] = mfma_e4m3(cat8d(kf[Q][kt][0], kf[Q][kt][1]), qb[rt][0], v4f{0.f, 0.f, 0.f, 0.f});
+        sc[rt][kt] = mfma_e4m3(cat8d(kf[Q][kt][2], kf[Q][kt][3]), qb[rt][1], sc[rt][kt]);
       }
-    // tile row max: the wave's 16 keys (lanes l16), then the four waves through LDS
-    float mx[8];
+    const int key0 = kbeg + kST * j + 4 * lg;  // lane's keys: key0 + 16 kt + r
+    float sv[RT][8], tmax[RT];
+    bool need = false;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = sv[i];
+    for (int rt = 0; rt < RT; ++rt) {
+      float mx = -INFINITY;
 #pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) v = fmaxf(v, __shfl_xor(v, o2));
-      mx[i] = v;
+      for (int i = 0; i < 8; ++i) {
+        const int key = key0 + 16 * (i >> 2) + (i & 3);
+        sv[rt][i] = key <= lim[rt] ? sc[rt][i >> 2][i & 3] * d.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sv[rt][i]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      tmax[rt] = fmaxf(mx, __shfl_xor(mx, 32));
+      need |= tmax[rt] > m[rt] + kLazy;
     }
-    __syncthreads();  // the previous tile's reads of red_m, ps and the other value buffer are done
-    if (more) fetch(it + 1, slot_next, std::integral_constant<int, Q ^ 1>{});
-    // always one page-table load (clamped), so the count of loads after this tile's values is fixed
-    slot_next = ptr_at(key_of(min(it + 2, t1 - 1)));
-    if (l16 == 0) {
+    if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) red_m[wave][16 * (i >> 2) + 4 * lg + (i & 3)] = mx[i];
-    }
-    __syncthreads();
-    float alpha[8];
+      for (int rt = 0; rt < RT; ++rt) {
+        const float mn = fmaxf(m[rt], tmax[rt]);
+        const float al = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[rt] - mn);
+        m[rt] = mn;
+        l[rt] *= al;
+        // four dim tiles at a time: the accumulators live in AGPRs and go through VGPRs to scale
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = 16 * (i >> 2) + 4 * lg + (i & 3);
-      const float tm = fmaxf(fmaxf(red_m[0][row], red_m[1][row]), fmaxf(red_m[2][row], red_m[3][row]));
-      const float mn = fmaxf(m[i], tm);
-      alpha[i] = mn == -INFINITY ? 1.f : exp2f(m[i] - mn);
-      m[i] = mn;
-      const float p = sv[i] == -INFINITY ? 0.f : exp2f(sv[i] - mn);
-      *reinterpret_cast<_Float16*>(ps + row * kPRow + 2 * (16 * wave + l16)) = (_Float16)p;
-      float ssum = p;
+        for (int dg = 0; dg < 16; dg += 4) {
 #pragma unroll
-      for (int o2 = 1; o2 < 16; o2 <<= 1) ssum += __shfl_xor(ssum, o2);
-      lw[i] = lw[i] * alpha[i] + ssum;
-    }
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[rt][dt][r] *= alpha[4 * rt + r];
-    // this tile's values have landed: newer are the next tile's 4 key and 4 value loads (if any)
-    // and one page-table load
-    if (more)
-      asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-    __syncthreads();
-    asm volatile("" ::: "memory");
-    const uint8_t* vb = Q ? vbuf1 : vbuf0;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      v8h pa[2];
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-        pa[rt] = *reinterpret_cast<const v8h*>(ps + (16 * rt + l16) * kPRow + 64 * kk + 16 * lg);
-      const int kr = 32 * kk + 8 * lg + (l16 >> 1);  // the value row (key) this lane addresses
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const int pos = (4 * wave + dt) ^ (kr & 15);
-        const v2i raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-            (__attribute__((address_space(3))) v2i*)(vb + kr * kDD + 16 * pos + 8 * (l16 & 1)));
-        const v8h vv = widen8(raw.x, raw.y);
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], vv, o[rt][dt], 0, 0, 0);
+          for (int i = 0; i < 4; ++i) {
+            o[rt][dg + i] *= al;
+            asm volatile("" : "+a"(o[rt][dg + i]));  // back into AGPRs (no VGPR copy across the join)
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
+    v8h pb[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p = sv[rt][i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[rt][i] - m[rt]);
+        ps += p;
+        pb[rt][i] = (_Float16)p;
+      }
+      l[rt] += ps;
+    }
+    // this stage's values have landed: newer are one page-table DMA and (kNS - 1) steps' requests
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(1 + (kNS - 1) * 17) : "memory");
+    const uint8_t* vb = stage(qc);
+    const int vrow = 8 * lg + (l16 >> 1);
+#pragma unroll
+    for (int dg = 0; dg < 16; dg += 4) {
+      // four dim tiles at a time (the scheduler would otherwise hoist all 16 reads and conversions)
+      v2i raw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        raw[i] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) v2i*)(vb + vrow * kDD + 16 * ((dg + i) ^ (vrow & 15)) + 8 * (l16 & 1)));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v8h vv = widen8(raw[i].x, raw[i].y);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          o[rt][dg + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pb[rt], o[rt][dg + i], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
-  for (int it = t0; it < t1; it += 2) {
-    step(it, std::integral_constant<int, 0>{});
-    if (it + 1 < t1) step(it + 1, std::integral_constant<int, 1>{});
+  // prologue: entries of steps 0 .. kPTD - kNS, then the first kNS - 1 steps' requests, each
+  // followed by the page-table DMA kPTD steps ahead (the order every step keeps)
+  for (int j = 0; j <= kPTD - kNS; ++j) pt_dma(j);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  fetch(0, std::integral_constant<int, 0>{});
+  pt_dma(kPTD - kNS + 1);
+  fetch(1, std::integral_constant<int, 1>{});
+  pt_dma(kPTD - kNS + 2);
+  auto step = [&](int j, auto qc) {
+    constexpr int Q = decltype(qc)::value;
+    fetch(j + kNS - 1, std::integral_constant<int, (Q + kNS - 1) % kNS>{});
+    pt_dma(j + kPTD);
+    compute(j, qc);
+  };
+  for (int j = 0; j < npad; j += kNS) {
+    step(j, std::integral_constant<int, 0>{});
+    step(j + 1, std::integral_constant<int, 1>{});
+    step(j + 2, std::integral_constant<int, 2>{});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  // partials: unnormalised o, the running max and the weight sum (summed over the four waves)
+  // merge the four waves: M = max of the waves' maxima; per row tile, each wave's output scaled by
+  // exp2(m - M) into its own 16 KB (fp32 [16 rows][256], 16-byte piece c of row r at c ^ r), then
+  // summed in wave order into this split's partial
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    float lt = l[rt] + __shfl_xor(l[rt], 16);
+    lt = lt + __shfl_xor(lt, 32);
+    if (lg == 0) {
+      mw[wave][16 * rt + l16] = m[rt];
+      lwv[wave][16 * rt + l16] = lt;
+    }
+  }
+  __syncthreads();
+  float* ob = reinterpret_cast<float*>((wave < 2 ? vs0 : vs1) + (wave & 1) * (kVS / 2));
+  const float* o0 = reinterpret_cast<const float*>(vs0);
+  const float* o1 = reinterpret_cast<const float*>(vs0 + kVS / 2);
+  const float* o2 = reinterpret_cast<const float*>(vs1);
+  const float* o3 = reinterpret_cast<const float*>(vs1 + kVS / 2);
   float* wo = d.ws_o + (size_t)grp * kDRows * kDD;
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int rt = 0; rt < RT; ++rt) {
+    if (rt > 0) __syncthreads();  // the previous tile's sums have read the buffers
+    const int row = 16 * rt + l16;
+    const float M = fmaxf(fmaxf(mw[0][row], mw[1][row]), fmaxf(mw[2][row], mw[3][row]));
+    const float f = m[rt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[rt] - M);
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) wo[(16 * rt + 4 * lg + r) * kDD + 64 * wave + 16 * dt + l16] = o[rt][dt][r];
-  __syncthreads();
-  if (l16 == 0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) red_l[wave][16 * (i >> 2) + 4 * lg + (i & 3)] = lw[i];
+    for (int dt = 0; dt < 16; ++dt)
+      *reinterpret_cast<v4f*>(ob + l16 * kDD + 4 * ((4 * dt + lg) ^ l16)) = o[rt][dt] * f;
+    __syncthreads();
+    const int rows = min(16, NT * kGQ - 16 * rt);
+    for (int e = tid; e < rows * (kDD / 4); e += 256) {
+      const int r = e / (kDD / 4), c = e % (kDD / 4), at = r * kDD + 4 * (c ^ r);
+      const v4f a = (*reinterpret_cast<const v4f*>(o0 + at) + *reinterpret_cast<const v4f*>(o1 + at)) +
+                    (*reinterpret_cast<const v4f*>(o2 + at) + *reinterpret_cast<const v4f*>(o3 + at));
+      *reinterpret_cast<v4f*>(wo + (16 * rt + r) * kDD + 4 * c) = a;
+    }
   }
-  if (wave == 0 && l16 == 0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) red_m[0][16 * (i >> 2) + 4 * lg + (i & 3)] = m[i];
-  }
-  __syncthreads();
   if (tid < kDRows) {
-    d.ws_ml[(size_t)grp * 2 * kDRows + tid] = red_m[0][tid];
-    d.ws_ml[(size_t)grp * 2 * kDRows + kDRows + tid] = (red_l[0][tid] + red_l[1][tid]) + (red_l[2][tid] + red_l[3][tid]);
+    const int row = tid;
+    float M = -INFINITY, L = 0.f;
+    if (row < 16 * RT) {
+      M = fmaxf(fmaxf(mw[0][row], mw[1][row]), fmaxf(mw[2][row], mw[3][row]));
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        if (mw[w][row] != -INFINITY) L += __builtin_amdgcn_exp2f(mw[w][row] - M) * lwv[w][row];
+    }
+    d.ws_ml[(size_t)grp * 2 * kDRows + row] = M;
+    d.ws_ml[(size_t)grp * 2 * kDRows + kDRows + row] = L;
   }
 }
 
@@ -361,7 +444,10 @@ extern "C" int q36_attn_decode(const q36_decode_args* a, q36_stream_t stream) {
               a->scale * 1.44269504088896340736f, reinterpret_cast<float*>(ws),
               reinterpret_cast<float*>(ws + align_up(sizeof(float) * (size_t)a->B * kKVH * S * kDRows * kDD, 256)),
               static_cast<uint16_t*>(a->out)};
-  decode_split_kernel<<<dim3(S, kKVH, a->B), 256, 0, st>>>(d);
+  if (a->NT <= 2)
+    decode_split_kernel<1><<<dim3(S, kKVH, a->B), 256, 0, st>>>(d);
+  else
+    decode_split_kernel<2><<<dim3(S, kKVH, a->B), 256, 0, st>>>(d);
   decode_combine_kernel<<<dim3(kKVH, a->B), 256, 0, st>>>(d);
   return check_launch("q36_attn_decode");
 }
