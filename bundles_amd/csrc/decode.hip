@@ -23,7 +23,8 @@
 //                   weights rounded to f16.  Keys, values and page-table entries stream through a
 //                   4-stage per-wave pipeline with no workgroup barrier; the output is rescaled only
 //                   when a row max grows by more than 2^8 (weights up to 2^8 are exact in f16).
-//   decode_combine  per (request, KV head): the splits' partials weighted by exp2(m_s - M) / L.
+//   decode_combine  the splits' partials weighted by exp2(m_s - M) / L (with one split the split
+//                   kernel writes the output itself).
 #include <math.h>
 
 #include <type_traits>
@@ -39,10 +40,12 @@ constexpr int kST = 32;              // keys per wave step
 constexpr int kNS = 3;               // key / value stages per wave (steps in flight + 1)
 constexpr int kPTD = 2 * kNS;        // page-table lookahead in steps
 constexpr int kPTR = 8;              // page-table ring entries per wave (one step each)
-constexpr int kVS = 4 * kST * kDD;   // one stage of the four waves' value rows (32 KB)
+constexpr int kVG = 4 * kDD + 64;    // a group of 4 value rows in LDS (64 bytes of padding)
+constexpr int kVW = 8 * kVG;         // one wave's 32 value rows
+constexpr int kVS = 4 * kVW;         // one stage of the four waves' value rows
 constexpr float kLazy = 8.f;         // rescale when a row max grows past the reference by 2^8
 static_assert(kPTR >= kPTD && (kPTR & (kPTR - 1)) == 0, "page-table ring");
-static_assert(kVS == 2 * 16 * kDD * 4, "a stage holds two waves' fp32 output of one row tile at the merge");
+static_assert(kVS >= 2 * 16 * kDD * 4, "a stage holds two waves' fp32 output of one row tile at the merge");
 static_assert(kNS == 3, "the stage arrays and the prologue are written out for three stages");
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
@@ -106,9 +109,10 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
   __shared__ __align__(16) uint8_t vs1[kVS];
   __shared__ __align__(16) uint8_t vs2[kVS];
   __shared__ __align__(16) int32_t ptl[4][kPTR][64];
-  __shared__ float mw[4][kDRows], lwv[4][kDRows];
+  __shared__ float mw[4][kDRows], lwv[4][kDRows], rowM[kDRows], rowL[kDRows];
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z, S = d.splits;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS bases stay scalar
   const int NT = d.NT, nk = d.seqlens[b], npre = nk - NT;
   // steps of the request, the split's share (contiguous), the wave's share of that
   const int steps = nk > 0 ? (nk + kST - 1) / kST : 0, per = steps / S, rem = steps % S;
@@ -116,6 +120,7 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
   const int ws0 = st0 + (wave * nst) / 4, ws1 = st0 + ((wave + 1) * nst) / 4;
   const int kbeg = ws0 * kST, kend = min(ws1 * kST, nk);  // the wave's keys [kbeg, kend)
   const int npad = (ws1 - ws0 + kNS - 1) / kNS * kNS;     // steps run (a multiple of the stages)
+  const int kfull = min(kend - 1, npre);  // keys up to here are visible to every query row
   const int grp = (b * kKVH + h) * S + s;
   // query fragments (score operand B): column 16 rt + l16 = query row (token row / 8, head
   // h * 8 + row % 8), dims 128 kb + 32 lg .. +31 rounded to e4m3; rows of tokens past NT are zero
@@ -158,12 +163,14 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
   // Step j into stage Q: the 32 keys' rows as score operand A (kf[Q][kt]: key 16 kt + l16, dims
   // 128 half + 32 lg ..), and the 32 value rows into the wave's LDS rows: DMA call m writes rows
   // 4 m .. 4 m + 3 with key 16 (m & 1) + 4 (m >> 1) + (row % 4), so rows 8 g .. 8 g + 7 hold keys
-  // 4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3 (the order of lane group g's weights); 16-byte
-  // piece p of row r sits at position p ^ (r % 16).
+  // 4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3 (the order of lane group g's weights).  Row group m
+  // (one DMA call, 1 KB) starts at m * (1 KB + 64 B) and 16-byte piece p of its row i sits at position
+  // p ^ i: the eight rows a lane group reads for one dim tile fall on eight distinct 16-byte bank
+  // slots, and only the low two bits of a piece's position depend on the lane.
   v4i kf[kNS][2][4];
   auto stage = [&](auto qc) -> uint8_t* {
     constexpr int Q = decltype(qc)::value;
-    return (Q == 0 ? vs0 : Q == 1 ? vs1 : vs2) + wave * (kST * kDD);
+    return (Q == 0 ? vs0 : Q == 1 ? vs1 : vs2) + wave * kVW;
   };
   auto fetch = [&](int j, auto qc) {
     constexpr int Q = decltype(qc)::value;
@@ -187,11 +194,9 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
     uint8_t* vb = stage(qc);
     const int vsl[8] = {vsl0, vsl1, vsl2, vsl3, vsl4, vsl5, vsl6, vsl7};
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const int row = 4 * m + lg;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vb + 4 * m * kDD, 16,
-                                               (vsl[m] * kKVH + h) * kDD + 16 * (l16 ^ (row & 15)), 0, 0, 0);
-    }
+    for (int m = 0; m < 8; ++m)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vb + m * kVG, 16, (vsl[m] * kKVH + h) * kDD + 16 * (l16 ^ lg), 0, 0,
+                                               0);
   };
   // per-lane state: running max (base 2) of query row 16 rt + l16, the lane's share of its weight
   // sum, and O^T (lane: row 16 rt + l16, dims 16 dt + 4 lg + r)
@@ -199,13 +204,25 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
   v4f o[RT][16];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    m[rt] = -INFINITY;
+    m[rt] = -1e30f;
     l[rt] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) o[rt][dt] = v4f{0.f, 0.f, 0.f, 0.f};
   }
+  // lane's value-read address: row 8 lg + l16 / 2 = group 2 lg + l16 / 8, row (l16 / 2) % 4 in it,
+  // half l16 % 2; dim tile dt adds 64 (dt / 4) + 16 ((dt % 4) ^ row)
+  const int vri = (l16 >> 1) & 3, vbase = (2 * lg + (l16 >> 3)) * kVG + vri * kDD + 8 * (l16 & 1);
   auto compute = [&](int j, auto qc) {
     constexpr int Q = decltype(qc)::value;
+    // this stage's values have landed (newer: one page-table DMA and kNS - 1 steps' requests); all
+    // sixteen transposed reads are issued now and complete under the scores and the softmax
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(1 + (kNS - 1) * 17) : "memory");
+    const uint8_t* vb = stage(qc) + vbase;
+    v2i vraw[16];
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt)
+      vraw[dt] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          (__attribute__((address_space(3))) v2i*)(vb + 64 * (dt >> 2) + 16 * ((dt & 3) ^ vri)));
     v4f sc[RT][2];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -214,27 +231,42 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
         sc[rt][kt] = mfma_e4m3(cat8d(kf[Q][kt][0], kf[Q][kt][1]), qb[rt][0], v4f{0.f, 0.f, 0.f, 0.f});
         sc[rt][kt] = mfma_e4m3(cat8d(kf[Q][kt][2], kf[Q][kt][3]), qb[rt][1], sc[rt][kt]);
       }
-    const int key0 = kbeg + kST * j + 4 * lg;  // lane's keys: key0 + 16 kt + r
-    float sv[RT][8], tmax[RT];
+    // Softmax weights.  Only a step with keys some query row must not see (the causal edge, the end
+    // of the wave's range) masks them to -inf; rows of tokens past NT have zero queries, stay finite
+    // and are never written.  The running max starts at a finite -1e30, so exp2 of a masked score
+    // is 0 with no special case.  Scores are raw MFMA sums, scaled inside the exponent's fma.
+    const float sl2 = d.scale_log2;
+    float sv[RT][8];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sv[rt][i] = sc[rt][i >> 2][i & 3];
+    if (kbeg + kST * j + kST - 1 > kfull) {  // uniform over the wave
+      const int key0 = kbeg + kST * j + 4 * lg;  // lane's keys: key0 + 16 kt + r
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (key0 + 16 * (i >> 2) + (i & 3) > lim[rt]) sv[rt][i] = -INFINITY;
+    }
+    float tmax[RT];
     bool need = false;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int key = key0 + 16 * (i >> 2) + (i & 3);
-        sv[rt][i] = key <= lim[rt] ? sc[rt][i >> 2][i & 3] * d.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, sv[rt][i]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      tmax[rt] = fmaxf(mx, __shfl_xor(mx, 32));
+      float mx = fmaxf(fmaxf(fmaxf(sv[rt][0], sv[rt][1]), fmaxf(sv[rt][2], sv[rt][3])),
+                       fmaxf(fmaxf(sv[rt][4], sv[rt][5]), fmaxf(sv[rt][6], sv[rt][7])));
+      // across the four lane groups (rows of 16 lanes) that hold the same query row
+      const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+      const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      tmax[rt] = fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1])) * sl2;
       need |= tmax[rt] > m[rt] + kLazy;
     }
     if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         const float mn = fmaxf(m[rt], tmax[rt]);
-        const float al = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[rt] - mn);
+        const float al = __builtin_amdgcn_exp2f(m[rt] - mn);
         m[rt] = mn;
         l[rt] *= al;
         // four dim tiles at a time: the accumulators live in AGPRs and go through VGPRs to scale
@@ -255,32 +287,17 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
       float ps = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float p = sv[rt][i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[rt][i] - m[rt]);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[rt][i], sl2, -m[rt]));
         ps += p;
         pb[rt][i] = (_Float16)p;
       }
       l[rt] += ps;
     }
-    // this stage's values have landed: newer are one page-table DMA and (kNS - 1) steps' requests
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(1 + (kNS - 1) * 17) : "memory");
-    const uint8_t* vb = stage(qc);
-    const int vrow = 8 * lg + (l16 >> 1);
 #pragma unroll
-    for (int dg = 0; dg < 16; dg += 4) {
-      // four dim tiles at a time (the scheduler would otherwise hoist all 16 reads and conversions)
-      v2i raw[4];
+    for (int dt = 0; dt < 16; ++dt) {
+      const v8h vv = widen8(vraw[dt].x, vraw[dt].y);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        raw[i] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-            (__attribute__((address_space(3))) v2i*)(vb + vrow * kDD + 16 * ((dg + i) ^ (vrow & 15)) + 8 * (l16 & 1)));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const v8h vv = widen8(raw[i].x, raw[i].y);
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-          o[rt][dg + i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pb[rt], o[rt][dg + i], 0, 0, 0);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+      for (int rt = 0; rt < RT; ++rt) o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pb[rt], o[rt][dt], 0, 0, 0);
     }
   };
   // prologue: entries of steps 0 .. kPTD - kNS, then the first kNS - 1 steps' requests, each
@@ -295,7 +312,9 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
     constexpr int Q = decltype(qc)::value;
     fetch(j + kNS - 1, std::integral_constant<int, (Q + kNS - 1) % kNS>{});
     pt_dma(j + kPTD);
+    __builtin_amdgcn_sched_barrier(0);  // requests first: the compute below waits for step j's data
     compute(j, qc);
+    __builtin_amdgcn_sched_barrier(0);  // and the next step's requests stay after it
   };
   for (int j = 0; j < npad; j += kNS) {
     step(j, std::integral_constant<int, 0>{});
@@ -303,9 +322,10 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
     step(j + 2, std::integral_constant<int, 2>{});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  // merge the four waves: M = max of the waves' maxima; per row tile, each wave's output scaled by
-  // exp2(m - M) into its own 16 KB (fp32 [16 rows][256], 16-byte piece c of row r at c ^ r), then
-  // summed in wave order into this split's partial
+  // merge the four waves: M = max of the waves' maxima, L = sum of exp2(m_w - M) l_w; per row
+  // tile, each wave's output scaled by exp2(m - M) into its own 16 KB (fp32 [16 rows][256], 16-byte
+  // piece c of row r at c ^ r), then summed in wave order into this split's partial (or, with one
+  // split, normalised by L into the bf16 output)
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     float lt = l[rt] + __shfl_xor(l[rt], 16);
@@ -313,6 +333,22 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
     if (lg == 0) {
       mw[wave][16 * rt + l16] = m[rt];
       lwv[wave][16 * rt + l16] = lt;
+    }
+  }
+  __syncthreads();
+  if (tid < kDRows) {
+    const int row = tid;
+    float M = -1e30f, L = 0.f;
+    if (row < 16 * RT) {
+      M = fmaxf(fmaxf(mw[0][row], mw[1][row]), fmaxf(mw[2][row], mw[3][row]));
+#pragma unroll
+      for (int w = 0; w < 4; ++w) L += __builtin_amdgcn_exp2f(mw[w][row] - M) * lwv[w][row];
+    }
+    rowM[row] = M;
+    rowL[row] = L;
+    if (S > 1) {
+      d.ws_ml[(size_t)grp * 2 * kDRows + row] = M;
+      d.ws_ml[(size_t)grp * 2 * kDRows + kDRows + row] = L;
     }
   }
   __syncthreads();
@@ -325,70 +361,49 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     if (rt > 0) __syncthreads();  // the previous tile's sums have read the buffers
-    const int row = 16 * rt + l16;
-    const float M = fmaxf(fmaxf(mw[0][row], mw[1][row]), fmaxf(mw[2][row], mw[3][row]));
-    const float f = m[rt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[rt] - M);
+    const float M = rowM[16 * rt + l16];
+    const float f = __builtin_amdgcn_exp2f(m[rt] - M);
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt)
       *reinterpret_cast<v4f*>(ob + l16 * kDD + 4 * ((4 * dt + lg) ^ l16)) = o[rt][dt] * f;
     __syncthreads();
     const int rows = min(16, NT * kGQ - 16 * rt);
     for (int e = tid; e < rows * (kDD / 4); e += 256) {
-      const int r = e / (kDD / 4), c = e % (kDD / 4), at = r * kDD + 4 * (c ^ r);
+      const int r = e / (kDD / 4), c = e % (kDD / 4), at = r * kDD + 4 * (c ^ r), row = 16 * rt + r;
       const v4f a = (*reinterpret_cast<const v4f*>(o0 + at) + *reinterpret_cast<const v4f*>(o1 + at)) +
                     (*reinterpret_cast<const v4f*>(o2 + at) + *reinterpret_cast<const v4f*>(o3 + at));
-      *reinterpret_cast<v4f*>(wo + (16 * rt + r) * kDD + 4 * c) = a;
+      if (S > 1) {
+        *reinterpret_cast<v4f*>(wo + row * kDD + 4 * c) = a;
+      } else {
+        const float L = rowL[row], il = L > 0.f ? 1.f / L : 0.f;
+        uint16_t* dst = d.out + (((size_t)b * NT + (row >> 3)) * kQH + h * kGQ + (row & 7)) * kDD + 4 * c;
+        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(a[0] * il, a[1] * il), pack_bf2(a[2] * il, a[3] * il));
+      }
     }
-  }
-  if (tid < kDRows) {
-    const int row = tid;
-    float M = -INFINITY, L = 0.f;
-    if (row < 16 * RT) {
-      M = fmaxf(fmaxf(mw[0][row], mw[1][row]), fmaxf(mw[2][row], mw[3][row]));
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-        if (mw[w][row] != -INFINITY) L += __builtin_amdgcn_exp2f(mw[w][row] - M) * lwv[w][row];
-    }
-    d.ws_ml[(size_t)grp * 2 * kDRows + row] = M;
-    d.ws_ml[(size_t)grp * 2 * kDRows + kDRows + row] = L;
   }
 }
 
-// per (request, KV head): out = bf16(sum_s exp2(m_s - M) o_s / sum_s exp2(m_s - M) l_s), splits in order
+// out = bf16(sum_s exp2(m_s - M) o_s / L), L = sum_s exp2(m_s - M) l_s, splits in order; one
+// thread per 4 dims of one query row (rows b, t, head over the batch)
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeDev d) {
-  __shared__ float wgt[64][kDRows];
-  __shared__ float inv_l[kDRows];
-  const int h = blockIdx.x, b = blockIdx.y, S = d.splits, tid = threadIdx.x;
-  const int g0 = (b * kKVH + h) * S;
-  if (tid < kDRows) {
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, d.ws_ml[(size_t)(g0 + s) * 2 * kDRows + tid]);
-    float L = 0.f;
-    for (int s = 0; s < S; ++s) {
-      const float ms = d.ws_ml[(size_t)(g0 + s) * 2 * kDRows + tid];
-      const float w = ms == -INFINITY ? 0.f : exp2f(ms - M);
-      wgt[s][tid] = w;
-      L += w * d.ws_ml[(size_t)(g0 + s) * 2 * kDRows + kDRows + tid];
-    }
-    inv_l[tid] = L > 0.f ? 1.f / L : 0.f;
+  const int e = blockIdx.x * 256 + threadIdx.x, NT = d.NT, S = d.splits;
+  if (e >= d.B * NT * kQH * (kDD / 4)) return;
+  const int c = e % (kDD / 4), qr = e / (kDD / 4);  // qr = (b * NT + t) * 16 + head
+  const int head = qr % kQH, bt = qr / kQH, t = bt % NT, b = bt / NT;
+  const int h = head / kGQ, gr = t * kGQ + head % kGQ, g0 = (b * kKVH + h) * S;
+  float M = -1e30f;  // the split kernel's maxima are finite (-1e30 for a split with no visible key)
+  for (int s = 0; s < S; ++s) M = fmaxf(M, d.ws_ml[(size_t)(g0 + s) * 2 * kDRows + gr]);
+  float L = 0.f;
+  v4f a = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < S; ++s) {
+    const float ms = d.ws_ml[(size_t)(g0 + s) * 2 * kDRows + gr];
+    const float w = exp2f(ms - M);
+    L += w * d.ws_ml[(size_t)(g0 + s) * 2 * kDRows + kDRows + gr];
+    a += w * *reinterpret_cast<const v4f*>(d.ws_o + ((size_t)(g0 + s) * kDRows + gr) * kDD + 4 * c);
   }
-  __syncthreads();
-  for (int e = tid; e < d.NT * kGQ * kDD / 4; e += 256) {
-    const int row = e / (kDD / 4), dim = 4 * (e % (kDD / 4));
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < S; ++s) {
-      const float w = wgt[s][row];
-      const float4 v = *reinterpret_cast<const float4*>(d.ws_o + ((size_t)(g0 + s) * kDRows + row) * kDD + dim);
-      a.x += w * v.x;
-      a.y += w * v.y;
-      a.z += w * v.z;
-      a.w += w * v.w;
-    }
-    const float il = inv_l[row];
-    const int t = row >> 3;
-    uint16_t* dst = d.out + (((size_t)b * d.NT + t) * kQH + h * kGQ + (row & 7)) * kDD + dim;
-    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(a.x * il, a.y * il), pack_bf2(a.z * il, a.w * il));
-  }
+  const float il = L > 0.f ? 1.f / L : 0.f;
+  *reinterpret_cast<uint2*>(d.out + (size_t)qr * kDD + 4 * c) =
+      make_uint2(pack_bf2(a[0] * il, a[1] * il), pack_bf2(a[2] * il, a[3] * il));
 }
 
 int decode_splits(int B, int splits) {
@@ -448,6 +463,6 @@ extern "C" int q36_attn_decode(const q36_decode_args* a, q36_stream_t stream) {
     decode_split_kernel<1><<<dim3(S, kKVH, a->B), 256, 0, st>>>(d);
   else
     decode_split_kernel<2><<<dim3(S, kKVH, a->B), 256, 0, st>>>(d);
-  decode_combine_kernel<<<dim3(kKVH, a->B), 256, 0, st>>>(d);
+  if (S > 1) decode_combine_kernel<<<(a->B * a->NT * kQH * (kDD / 4) + 255) / 256, 256, 0, st>>>(d);
   return check_launch("q36_attn_decode");
 }
