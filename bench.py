@@ -6,7 +6,7 @@ MoE layer over one batch of 64 tokens with every input resident in HBM.  value =
 layer.  Beside it: the roofline of the dominant kernel (the expert up-projection, HBM-bound), the
 other nodes' step times, and the CPU oracle timed on this host's cores on the same workload.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only moe,gdn,lmhead,attn] [--copy-calib]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only moe,gdn,lmhead,attn,decode] [--copy-calib]
 """
 from __future__ import annotations
 
@@ -192,6 +192,47 @@ def bench_attn(args, torch, dev):
                 bytes=tot, gbs=tot / ((ms_p + ms_o) * 1e-3) / 1e9)
 
 
+def bench_decode(args, torch, dev):
+    """Config 5's attention layer: decode / verify attention over an e4m3 KV cache of 4096 keys per
+    sequence (one-token pages at random cache slots).  Verify: 64 sequences x 4 draft tokens (256
+    query tokens); decode: 256 sequences x 1 token.  One call = the split and combine kernels."""
+    from bundles_amd.qwen36_layer import attn_fused
+
+    ctx = 4096
+    res = {}
+    for name, B, NT in (("verify", 64, 4), ("decode", 256, 1)):
+        g = torch.Generator(device=dev).manual_seed(0)
+        slots = B * ctx + 64
+        q = torch.randn((B * NT, 16, 256), device=dev, generator=g).to(torch.bfloat16)
+        kc = torch.randn((slots, 2, 256), device=dev, generator=g).to(torch.float8_e4m3fn).view(torch.uint8)
+        vc = torch.randn((slots, 2, 256), device=dev, generator=g).to(torch.float8_e4m3fn).view(torch.uint8)
+        pt = torch.randperm(slots, device=dev, generator=g)[:B * ctx].to(torch.int32).reshape(B, ctx).contiguous()
+        sl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+        ws = attn_fused.DecodeWorkspace(B, dev)
+        out = torch.empty_like(q)
+
+        def step():
+            attn_fused.attn_decode(q, kc, vc, pt, sl, NT, 1.0 / 16.0, ws, out=out)
+
+        for _ in range(max(1, args.warmup)):
+            step()
+        torch.cuda.synchronize()
+        ms = events_time(step, args.steps, torch)
+        # algorithmic bytes: every cached key's K and V row of both KV heads, the page-table
+        # entries, the queries and the outputs
+        algo = B * ctx * (2 * 2 * 256 + 4) + 2 * B * NT * 16 * 256 * 2
+        res[name] = dict(us_per_step=ms * 1e3, bytes=algo, gbs=algo / (ms * 1e-3) / 1e9, sequences=B,
+                         query_tokens=B * NT, context=ctx, splits=_decode_splits(B))
+        del q, kc, vc, pt, ws, out
+    return res
+
+
+def _decode_splits(B):
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    return max(1, min(64, cus // (B * 2)))
+
+
 MFMA_I8_PEAK_TOPS = 5000.0  # MI355X dense int8, published
 
 
@@ -252,7 +293,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="moe,gdn,lmhead,attn",
+    ap.add_argument("--only", default="moe,gdn,lmhead,attn,decode",
                     help="comma list of the nodes to run (the headline needs moe)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 256 MiB device copy (the reference kernel for HBM counters)")
@@ -270,7 +311,7 @@ def main():
     print(f"bench: MoE fp8 batch 64, steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
     moe_res = bench_moe(args, torch, dev)
     print(f"bench: MoE done ({moe_res['ms_graph'] * 1e3:.1f} us/layer)", file=sys.stderr, flush=True)
-    gdn_res = lmh_res = attn_res = None
+    gdn_res = lmh_res = attn_res = dec_res = None
     if "gdn" in only:
         print("bench: GDN verify 32 x 5", file=sys.stderr, flush=True)
         gdn_res = bench_gdn(args, torch, dev)
@@ -281,6 +322,9 @@ def main():
     if "attn" in only:
         print("bench: attention projections 128 tokens", file=sys.stderr, flush=True)
         attn_res = bench_attn(args, torch, dev)
+    if "decode" in only:
+        print("bench: decode / verify attention over a 4096-key e4m3 cache", file=sys.stderr, flush=True)
+        dec_res = bench_decode(args, torch, dev)
     if args.copy_calib:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -332,6 +376,14 @@ def main():
             "frac_hbm": round(attn_res["gbs"] / HBM_PEAK_GBS, 4),
             "workload": "128 tokens, e4m3 128x128-block qkv [9216,2048] + o_proj [2048,4096] (eager back-to-back "
                         "launches; *_graph: one captured graph per call, replayed)"}
+    if dec_res:
+        line["attn_decode"] = {
+            k: {"us_per_step": round(v["us_per_step"], 2), "bytes": v["bytes"], "achieved_gbs": round(v["gbs"], 1),
+                "frac_hbm": round(v["gbs"] / HBM_PEAK_GBS, 4), "sequences": v["sequences"],
+                "query_tokens": v["query_tokens"], "context": v["context"], "splits": v["splits"]}
+            for k, v in dec_res.items()}
+        line["attn_decode"]["workload"] = ("16 q heads / 2 KV heads x 256, e4m3 KV cache, one-token pages at random "
+                                           "slots; verify = 64 seqs x 4 draft tokens, decode = 256 seqs x 1")
     if gdn_res:
         line["gdn_verify"] = {
             "us_per_step": round(gdn_res["us_per_step"], 2), "bytes": gdn_res["bytes"],
