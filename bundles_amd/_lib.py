@@ -55,6 +55,19 @@ class LmheadArgs(C.Structure):
                 ("ws", P), ("ids", P), ("logits", P), ("workspace", P), ("workspace_bytes", SZ)]
 
 
+class LinearSeg(C.Structure):
+    _fields_ = [("col0", I32), ("ld", I32), ("out", P)]
+
+
+class Fp8LinearArgs(C.Structure):
+    _fields_ = [("T", I32), ("N", I32), ("K", I32), ("n_out", I32), ("x", P), ("w", P), ("ws", P), ("nseg", I32),
+                ("seg", LinearSeg * 4), ("workspace", P), ("workspace_bytes", SZ)]
+
+
+class AddNormArgs(C.Structure):
+    _fields_ = [("T", I32), ("H", I32), ("delta", P), ("residual", P), ("norm_w", P), ("eps", C.c_float), ("out", P)]
+
+
 class DecodeArgs(C.Structure):
     _fields_ = [("B", I32), ("NT", I32), ("HQ", I32), ("HKV", I32), ("D", I32), ("splits", I32), ("q", P),
                 ("k_cache", P), ("v_cache", P), ("num_slots", C.c_int64), ("page_table", P), ("pt_stride", I32),
@@ -80,6 +93,9 @@ SYMBOLS = [
     ("q36_oproj_workspace_bytes", SZ, [I32]),
     ("q36_attn_proj", I32, [C.POINTER(AttnArgs), P]),
     ("q36_attn_oproj", I32, [C.POINTER(OprojArgs), P]),
+    ("q36_fp8_linear_workspace_bytes", SZ, [I32, I32]),
+    ("q36_fp8_linear", I32, [C.POINTER(Fp8LinearArgs), P]),
+    ("q36_add_rmsnorm", I32, [C.POINTER(AddNormArgs), P]),
     ("q36_attn_decode_workspace_bytes", SZ, [I32, I32]),
     ("q36_attn_decode", I32, [C.POINTER(DecodeArgs), P]),
     ("q36_lmhead_workspace_bytes", SZ, [I32]),

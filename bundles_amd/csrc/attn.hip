@@ -90,8 +90,16 @@ struct GemmDev {
   const uint8_t* W;   // e4m3 in fragment order [N / 16][K / 128][2][64][16 B]
   const float* Ws;    // [N/128, K/128]
   int N;
-  uint16_t* Y;        // bf16 [T, N]
+  // bf16 outputs: columns [c0[i], c0[i + 1]) of the first nout go to ys[i] with row stride ld[i]
+  // (column c0[i] at ys[i][t * ld[i]]); the rest are padding rows of W and are not written
+  int nseg, nout;
+  int c0[4], ld[4];
+  uint16_t* ys[4];
 };
+GemmDev gemm_dev(const uint8_t* A, const float* As, int T, int K, const uint8_t* W, const float* Ws, int N,
+                 uint16_t* Y) {
+  return GemmDev{A, As, T, K, W, Ws, N, 1, N, {0, 0, 0, 0}, {N, 0, 0, 0}, {Y, nullptr, nullptr, nullptr}};
+}
 constexpr int kPKC = 512;  // K bytes per LDS chunk
 __device__ __forceinline__ void pdma16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds, 16, voff, 0, 0, 0);
@@ -205,15 +213,21 @@ __global__ __launch_bounds__(256) void proj_gemm_kernel(GemmDev g) {
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  // lane: token t0 + 16 tt + l % 16, rows n0 + 16 c + 4 (l / 16) .. +3
+  // lane: token t0 + 16 tt + l % 16, rows n0 + 16 c + 4 (l / 16) .. +3 (four columns never straddle
+  // a segment: the boundaries are multiples of 4)
 #pragma unroll
   for (int tt = 0; tt < NTT; ++tt) {
     const int t = t0 + tt * 16 + lr;
     if (t < g.T) {
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-        *reinterpret_cast<uint2*>(g.Y + (size_t)t * g.N + n0 + c * 16 + 4 * lgp) =
-            make_uint2(pack_bf2(acc[c][tt][0], acc[c][tt][1]), pack_bf2(acc[c][tt][2], acc[c][tt][3]));
+      for (int c = 0; c < 2; ++c) {
+        const int col = n0 + c * 16 + 4 * lgp;
+        if (col < g.nout) {
+          const int sg = (g.nseg > 1 && col >= g.c0[1]) + (g.nseg > 2 && col >= g.c0[2]) + (g.nseg > 3 && col >= g.c0[3]);
+          *reinterpret_cast<uint2*>(g.ys[sg] + (size_t)t * g.ld[sg] + (col - g.c0[sg])) =
+              make_uint2(pack_bf2(acc[c][tt][0], acc[c][tt][1]), pack_bf2(acc[c][tt][2], acc[c][tt][3]));
+        }
+      }
     }
   }
 }
@@ -333,6 +347,23 @@ OprojWs oproj_ws(int T) {
   return w;
 }
 
+struct LinWs {
+  size_t xq, xs, total;
+};
+LinWs lin_ws(int T, int K) {
+  LinWs w;
+  size_t o = 0;
+  auto take = [&](size_t b) {
+    size_t r = o;
+    o = align_up(o + b, 256);
+    return r;
+  };
+  w.xq = take((size_t)T * K);
+  w.xs = take(sizeof(float) * (size_t)(K / 128) * T);
+  w.total = o;
+  return w;
+}
+
 // grid: (N / 128 row blocks, token groups of 16 NTT)
 template <int NTT, int NKB, int PD>
 void launch_gemm(const GemmDev& g, hipStream_t st) {
@@ -380,7 +411,7 @@ extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
   float* xs = reinterpret_cast<float*>(ws + L.xs);
   uint16_t* qkv = reinterpret_cast<uint16_t*>(ws + L.qkv);
   act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr, 2048, xq, xs);
-  const GemmDev g{xq, xs, a->T, 2048, static_cast<const uint8_t*>(a->wqkv), a->sqkv, 9216, qkv};
+  const GemmDev g = gemm_dev(xq, xs, a->T, 2048, static_cast<const uint8_t*>(a->wqkv), a->sqkv, 9216, qkv);
   // measured at 128 tokens: two-tile groups with 2 stages in flight beat four-tile groups (the
   // weight reads from L2 double, the grid doubles to 288 workgroups) and one-tile groups
   if (a->T > 16)
@@ -412,10 +443,60 @@ extern "C" int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream) {
   float* as = reinterpret_cast<float*>(ws + L.as);
   act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->attn), static_cast<const uint16_t*>(a->gate),
                                          4096, aq, as);
-  const GemmDev g{aq, as, a->T, 4096, static_cast<const uint8_t*>(a->wo), a->so, 2048, static_cast<uint16_t*>(a->out)};
+  const GemmDev g =
+      gemm_dev(aq, as, a->T, 4096, static_cast<const uint8_t*>(a->wo), a->so, 2048, static_cast<uint16_t*>(a->out));
   // o_proj has 16 row blocks: one-tile groups (128 workgroups at 128 tokens), 4 stages in flight
   launch_gemm<1, 32, 4>(g, st);
   return check_launch("q36_attn_oproj");
+}
+
+extern "C" size_t q36_fp8_linear_workspace_bytes(int32_t T, int32_t K) { return lin_ws(T, K).total; }
+
+extern "C" int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream) {
+  Q36_REQUIRE(a != nullptr, "q36_fp8_linear: null args");
+  Q36_REQUIRE(a->T >= 1 && a->T <= 65535, "q36_fp8_linear: T=%d out of range", a->T);
+  Q36_REQUIRE(a->K == 2048 || a->K == 4096, "q36_fp8_linear: K=%d unsupported (2048 or 4096)", a->K);
+  Q36_REQUIRE(a->N >= 128 && a->N % 128 == 0 && a->N <= (1 << 20), "q36_fp8_linear: N=%d must be a multiple of 128",
+              a->N);
+  Q36_REQUIRE(a->n_out >= 4 && a->n_out <= a->N && a->n_out % 4 == 0, "q36_fp8_linear: n_out=%d (N=%d)", a->n_out,
+              a->N);
+  Q36_REQUIRE(a->x && a->w && a->ws && a->workspace, "q36_fp8_linear: a required pointer is null");
+  Q36_REQUIRE(aligned16(a->x) && aligned16(a->w) && (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0,
+              "q36_fp8_linear: x, w must be 16-byte and workspace 256-byte aligned");
+  Q36_REQUIRE(a->nseg >= 1 && a->nseg <= 4 && a->seg[0].col0 == 0, "q36_fp8_linear: nseg=%d, first segment at %d",
+              a->nseg, a->seg[0].col0);
+  for (int i = 0; i < a->nseg; ++i) {
+    const int end = i + 1 < a->nseg ? a->seg[i + 1].col0 : a->n_out;
+    Q36_REQUIRE(a->seg[i].out && (reinterpret_cast<uintptr_t>(a->seg[i].out) & 7u) == 0,
+                "q36_fp8_linear: segment %d output null or not 8-byte aligned", i);
+    Q36_REQUIRE(a->seg[i].col0 % 4 == 0 && end > a->seg[i].col0 && a->seg[i].ld >= end - a->seg[i].col0 &&
+                    a->seg[i].ld % 4 == 0,
+                "q36_fp8_linear: segment %d columns [%d, %d) with row stride %d", i, a->seg[i].col0, end,
+                a->seg[i].ld);
+  }
+  const LinWs L = lin_ws(a->T, a->K);
+  Q36_REQUIRE(a->workspace_bytes >= L.total, "q36_fp8_linear: workspace of %zu bytes < %zu required",
+              a->workspace_bytes, L.total);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(a->workspace);
+  uint8_t* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
+  float* xs = reinterpret_cast<float*>(ws + L.xs);
+  act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr, a->K, xq, xs);
+  GemmDev g = gemm_dev(xq, xs, a->T, a->K, static_cast<const uint8_t*>(a->w), a->ws, a->N, nullptr);
+  g.nseg = a->nseg;
+  g.nout = a->n_out;
+  for (int i = 0; i < 4; ++i) {
+    g.c0[i] = i < a->nseg ? a->seg[i].col0 : a->n_out;
+    g.ld[i] = i < a->nseg ? a->seg[i].ld : 0;
+    g.ys[i] = i < a->nseg ? static_cast<uint16_t*>(a->seg[i].out) : nullptr;
+  }
+  if (a->K == 4096)
+    launch_gemm<1, 32, 4>(g, st);
+  else if (a->T > 16)
+    launch_gemm<2, 16, 2>(g, st);
+  else
+    launch_gemm<1, 16, 4>(g, st);
+  return check_launch("q36_fp8_linear");
 }
 
 extern "C" int q36_pack_frag8(const void* q, int64_t N, int32_t K, void* packed, q36_stream_t stream) {

@@ -1,0 +1,87 @@
+"""The hybrid layer's glue on libq36: the e4m3 block-scaled linear with column-segmented outputs
+(q36_fp8_linear) and the fused residual add + Gemma RMSNorm (q36_add_rmsnorm).
+
+Mirrors the reference's decode projections and add-norm (R = qwen36_nodes_kb34, L = R/qwen36_layer):
+gdn_in_proj / qkv_proj with their outputs split by column (L/qk_proj_decode.cu:409,434; the DENSE8
+seg kernel L/qk_proj_decode.cu:483-1102, L/dense8.py:317-353), the out_proj / o_proj before the
+add-norm and the add-norm itself (L/proj.py:60-112 project_add_norm).  The weights are e4m3 with
+128x128 block scales (the configuration's format), prepared once by prepare_fp8_weight.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from .. import _lib
+from .._lib import AddNormArgs, Fp8LinearArgs, check, ptr
+from .moe import pack_frag8, quantize_blocks_e4m3
+
+
+@dataclass
+class Fp8Weight:
+    q: torch.Tensor    # e4m3 codes [N_pad, K] row-major (rows past n are zero)
+    s: torch.Tensor    # fp32 [N_pad / 128, K / 128]
+    qp: torch.Tensor   # the same codes in MFMA fragment order (what the kernel reads)
+    n: int             # output columns (rows of the unpadded weight)
+
+
+def prepare_fp8_weight(w: torch.Tensor) -> Fp8Weight:
+    """bf16 [N, K] -> e4m3 128x128 blocks, rows padded with zeros to a multiple of 128."""
+    N, K = w.shape
+    npad = (N + 127) // 128 * 128
+    if npad != N:
+        w = torch.cat([w, torch.zeros((npad - N, K), dtype=w.dtype, device=w.device)], dim=0)
+    q, s = quantize_blocks_e4m3(w.contiguous())
+    return Fp8Weight(q, s, pack_frag8(q), N)
+
+
+class LinearWorkspace:
+    """The activation codes and scales of q36_fp8_linear for up to T_max tokens of width K."""
+
+    def __init__(self, T_max: int, K: int, device):
+        self.T_max, self.K = T_max, K
+        self.buf = torch.empty(_lib.lib().q36_fp8_linear_workspace_bytes(T_max, K), dtype=torch.uint8, device=device)
+
+
+def fp8_linear(x: torch.Tensor, w: Fp8Weight, ws: LinearWorkspace, segments=None, stream=None):
+    """y = x . W^T (bf16), x bf16 [T, K].
+
+    segments: None (returns one [T, n] tensor) or a list of (col0, out) with out a bf16 [T, width]
+    view whose rows may be strided (row stride = out.stride(0)); columns col0 .. col0 + width of y
+    land in it.  The segments must tile [0, n) in order.
+    """
+    T, K = x.shape
+    if T > ws.T_max or K != ws.K:
+        raise ValueError(f"fp8_linear: [{T}, {K}] does not fit the workspace ({ws.T_max}, {ws.K})")
+    if segments is None:
+        out = torch.empty((T, w.n), dtype=torch.bfloat16, device=x.device)
+        segments, ret = [(0, out)], out
+    else:
+        ret = None
+    if not 1 <= len(segments) <= 4:
+        raise ValueError("fp8_linear: 1 to 4 segments")
+    end = 0
+    segs = (_lib.LinearSeg * 4)()
+    for i, (c0, o) in enumerate(segments):
+        if c0 != end or o.dtype != torch.bfloat16 or o.shape[0] != T or o.stride(1) != 1:
+            raise ValueError(f"fp8_linear: segment {i} (col0 {c0}) must continue at column {end} as bf16 [T, w]")
+        segs[i] = _lib.LinearSeg(c0, o.stride(0), o.data_ptr())
+        end = c0 + o.shape[1]
+    if end != w.n:
+        raise ValueError(f"fp8_linear: segments cover {end} of {w.n} columns")
+    a = Fp8LinearArgs(T, w.qp.shape[0], K, w.n, ptr(x), ptr(w.qp), ptr(w.s), len(segments), segs,
+                      ptr(ws.buf), ws.buf.numel())
+    check(_lib.lib().q36_fp8_linear(C.byref(a), _lib.stream_handle(stream)), "q36_fp8_linear")
+    return ret
+
+
+def add_rmsnorm(delta, residual: torch.Tensor, norm_w: torch.Tensor, eps: float, out=None, stream=None):
+    """residual += delta (bf16, in place; delta None: residual unchanged); returns the Gemma-normalised
+    rows bf16((z * rstd) * (1 + w)) of z = delta + residual in fp32."""
+    T, H = residual.shape
+    out = torch.empty_like(residual) if out is None else out
+    a = AddNormArgs(T, H, ptr(delta), ptr(residual), ptr(norm_w), eps, ptr(out))
+    check(_lib.lib().q36_add_rmsnorm(C.byref(a), _lib.stream_handle(stream)), "q36_add_rmsnorm")
+    return out

@@ -206,6 +206,50 @@ size_t q36_oproj_workspace_bytes(int32_t T);
 int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream);
 int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream);
 
+/* ---- e4m3 block-scaled linear with column-segmented bf16 outputs: replaces the decode
+ * projections the hybrid layer makes around its mixers, gdn_in_proj / qkv_proj
+ * (L/qk_proj_decode.cu:409,434) with the column split of their outputs (the DENSE8 seg kernel,
+ * L/qk_proj_decode.cu:483-1102; L/dense8.py:317-353) and the out_proj / o_proj GEMM before the
+ * add-norm (L/proj.py:84-112) ----
+ * x bf16 [T, K] (K = 2048 or 4096) is quantized per token x 128 channels to e4m3; w e4m3 [N, K]
+ * in fragment order (q36_pack_frag8), N a multiple of 128 (rows past n_out are padding), ws fp32
+ * [N/128, K/128].  y[t, n] = bf16(sum over 128-blocks kb in order of fma(blocksum, xs * ws, acc)).
+ * Column n < n_out goes to the segment i with seg[i].col0 <= n < seg[i+1].col0 (or n_out), at
+ * seg[i].out[t * seg[i].ld + n - seg[i].col0]; col0 and ld multiples of 4, outputs 8-byte aligned. */
+typedef struct q36_linear_seg {
+  int32_t col0;
+  int32_t ld;
+  void* out;
+} q36_linear_seg;
+typedef struct q36_fp8_linear_args {
+  int32_t T, N, K, n_out;
+  const void* x;
+  const void* w;
+  const float* ws;
+  int32_t nseg;
+  q36_linear_seg seg[4];
+  void* workspace;
+  size_t workspace_bytes;
+} q36_fp8_linear_args;
+size_t q36_fp8_linear_workspace_bytes(int32_t T, int32_t K);
+int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream);
+
+/* ---- Fused residual add + Gemma RMSNorm between the hybrid layer's blocks: replaces the add-norm
+ * of L/proj.py:60-81 (_add_norm_kernel) and the stock fused add-RMSNorm it reproduces ----
+ * z = bf16 delta + residual in fp32 (delta NULL: z = residual); residual <- bf16(z) when delta is
+ * given; out = bf16((z * rstd) * (1 + w)), rstd = 1 / sqrt(sum z^2 / H + eps) with the sum in the
+ * fixed order lane l of 64 owns the 8-element chunks l + 64 j (fma from zero), then an xor
+ * butterfly 32..1.  H = 2048; delta, residual, out and w 16-byte aligned. */
+typedef struct q36_add_norm_args {
+  int32_t T, H;
+  const void* delta;
+  void* residual;
+  const void* norm_w;
+  float eps;
+  void* out;
+} q36_add_norm_args;
+int q36_add_rmsnorm(const q36_add_norm_args* a, q36_stream_t stream);
+
 /* ---- Decode / verify attention over the e4m3 KV cache: replaces attn_verify_kernel
  * (L/qk_attn_verify.cu:354-760) with its split count (L/attn_fused.py:110-124) ----
  * q bf16 [B*NT, HQ, D] (normed, roped, as q36_attn_proj writes it); k_cache, v_cache e4m3

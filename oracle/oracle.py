@@ -89,6 +89,10 @@ def _declare(L):
     L.q36o_quant_rows_i8.argtypes = [P, I32, I32, P, P]
     L.q36o_quant_groups_e4m3.argtypes = [P, I32, I32, I32, P, P]
     L.q36o_quant_blocks_e4m3.argtypes = [P, I32, I32, P, P]
+    L.q36o_fp8_linear.restype = I32
+    L.q36o_fp8_linear.argtypes = [I32, I32, I32, P, P, P, P, I32]
+    L.q36o_add_rmsnorm.restype = I32
+    L.q36o_add_rmsnorm.argtypes = [I32, I32, P, P, P, C.c_float, P]
     L.q36o_route.restype = I32
     L.q36o_route.argtypes = [P, P, P, P, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P]
     for fn, st in (("q36o_moe", MoeArgs), ("q36o_gdn_verify", GdnArgs), ("q36o_attn_proj", AttnArgs),
@@ -286,6 +290,32 @@ def lmhead(h, norm_w, eps, wq, ws, want_logits=False, n_threads=0):
     if lib().q36o_lmhead(C.byref(a)):
         raise ValueError("q36o_lmhead failed")
     return ids, logits
+
+
+# ---------------------------------------------------------------- hybrid-layer glue
+def fp8_linear(x, wq, ws, n_threads=0):
+    """x bf16 bits [T, K]; wq e4m3 codes [N, K] row-major; ws fp32 [N/128, K/128] -> bf16 bits [T, N]."""
+    x = np.ascontiguousarray(x, np.uint16)
+    wq = np.ascontiguousarray(wq, np.uint8)
+    ws = np.ascontiguousarray(ws, np.float32)
+    T, K = x.shape
+    N = wq.shape[0]
+    out = np.empty((T, N), np.uint16)
+    if lib().q36o_fp8_linear(T, N, K, _p(x), _p(wq), _p(ws), _p(out), n_threads):
+        raise ValueError("q36o_fp8_linear failed")
+    return out
+
+
+def add_rmsnorm(delta, residual, w, eps):
+    """delta (or None), residual bf16 bits [T, H], w bf16 bits [H] -> (out, new residual) bf16 bits."""
+    residual = np.array(residual, np.uint16, copy=True, order="C")
+    d = None if delta is None else np.ascontiguousarray(delta, np.uint16)
+    w = np.ascontiguousarray(w, np.uint16)
+    T, H = residual.shape
+    out = np.empty_like(residual)
+    if lib().q36o_add_rmsnorm(T, H, _p(d), _p(residual), _p(w), eps, _p(out)):
+        raise ValueError("q36o_add_rmsnorm failed")
+    return out, residual
 
 
 # ---------------------------------------------------------------- decode attention

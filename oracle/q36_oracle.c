@@ -673,6 +673,51 @@ int q36o_attn_oproj(const q36o_oproj_args* a) {
 }
 
 /* ------------------------------------------------------------------------------------ */
+/* hybrid-layer glue: block-scaled linear, add + Gemma RMSNorm                           */
+/* ------------------------------------------------------------------------------------ */
+
+/* The decode projections around the hybrid layer's mixers (gdn_in_proj, out_proj, o_proj before the
+ * add-norm; L/qk_proj_decode.cu:409,434, L/proj.py:84-112) in the configuration's e4m3 format: x
+ * quantized per token x 128 channels, then the block rule of fp8_linear, all N columns. */
+int q36o_fp8_linear(int T, int N, int K, const uint16_t* x, const uint8_t* wq, const float* ws, uint16_t* out,
+                    int n_threads) {
+  if (K % 128 || N % 128 || T < 1) return -1;
+  if (n_threads > 0) omp_set_num_threads(n_threads);
+  float* xf = (float*)malloc(sizeof(float) * (size_t)T * K);
+  for (size_t i = 0; i < (size_t)T * K; ++i) xf[i] = q36o_bf16_to_f32(x[i]);
+  uint8_t* xq = (uint8_t*)malloc((size_t)T * K);
+  float* xs = (float*)malloc(sizeof(float) * (size_t)T * (K / 128));
+  q36o_quant_groups_e4m3(xf, T, K, 128, xq, xs);
+  float* y = (float*)malloc(sizeof(float) * (size_t)T * N);
+  fp8_linear(xq, xs, T, wq, ws, N, K, y);
+  for (size_t i = 0; i < (size_t)T * N; ++i) out[i] = q36o_f32_to_bf16(y[i]);
+  free(xf); free(xq); free(xs); free(y);
+  return 0;
+}
+
+/* The add-norm between blocks (L/proj.py:60-81): z = bf16 delta + residual in fp32 (no delta:
+ * z = residual); residual <- bf16(z) when delta is given; out = bf16((z * rstd) * (1 + w)),
+ * rstd = 1 / sqrt(ss / H + eps), ss = q36o_dot_canon(z, z) (the kernel's fixed order). */
+int q36o_add_rmsnorm(int T, int H, const uint16_t* delta, uint16_t* residual, const uint16_t* w, float eps,
+                     uint16_t* out) {
+  if (H % 512 || T < 1) return -1;
+  float* z = (float*)malloc(sizeof(float) * H);
+  for (int t = 0; t < T; ++t) {
+    for (int i = 0; i < H; ++i) {
+      float r = q36o_bf16_to_f32(residual[(size_t)t * H + i]);
+      z[i] = delta ? q36o_bf16_to_f32(delta[(size_t)t * H + i]) + r : r;
+      if (delta) residual[(size_t)t * H + i] = q36o_f32_to_bf16(z[i]);
+    }
+    float ss = q36o_dot_canon(z, z, H);
+    float rstd = 1.f / sqrtf(ss / (float)H + eps);
+    for (int i = 0; i < H; ++i)
+      out[(size_t)t * H + i] = q36o_f32_to_bf16((z[i] * rstd) * (1.f + q36o_bf16_to_f32(w[i])));
+  }
+  free(z);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------------------ */
 /* decode / verify attention                                                            */
 /* ------------------------------------------------------------------------------------ */
 

@@ -156,6 +156,13 @@ typedef struct {
 int q36o_attn_decode(const q36o_decode_args* a);
 float q36o_f16_round(float x);
 
+/* hybrid-layer glue: e4m3 block-scaled linear (x bf16 [T, K], wq row-major e4m3 [N, K], ws
+ * [N/128, K/128], out bf16 [T, N]) and the add + Gemma RMSNorm (delta may be NULL) */
+int q36o_fp8_linear(int T, int N, int K, const uint16_t* x, const uint8_t* wq, const float* ws, uint16_t* out,
+                    int n_threads);
+int q36o_add_rmsnorm(int T, int H, const uint16_t* delta, uint16_t* residual, const uint16_t* w, float eps,
+                     uint16_t* out);
+
 #ifdef __cplusplus
 }
 #endif

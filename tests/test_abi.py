@@ -42,7 +42,8 @@ def test_struct_layouts_match_header(tmp_path):
     from bundles_amd import _lib
     structs = {"q36_moe_args": _lib.MoeArgs, "q36_moe_ws_layout": _lib.MoeWsLayout, "q36_gdn_args": _lib.GdnArgs,
                "q36_attn_args": _lib.AttnArgs, "q36_oproj_args": _lib.OprojArgs, "q36_lmhead_args": _lib.LmheadArgs,
-               "q36_decode_args": _lib.DecodeArgs}
+               "q36_decode_args": _lib.DecodeArgs, "q36_linear_seg": _lib.LinearSeg,
+               "q36_fp8_linear_args": _lib.Fp8LinearArgs, "q36_add_norm_args": _lib.AddNormArgs}
     hdr = open(HEADER).read()
     structs = {k: v for k, v in structs.items() if f"typedef struct {k}" in hdr}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
@@ -90,6 +91,17 @@ def test_invalid_arguments_are_rejected(L):
     assert b"NT=5" in L.q36_last_error()
     d.NT = 4
     assert L.q36_attn_decode(C.byref(d), None) == _lib.Q36_EINVAL  # null pointers
+    f = _lib.Fp8LinearArgs()
+    f.T, f.N, f.K, f.n_out = 4, 256, 1024, 256
+    assert L.q36_fp8_linear(C.byref(f), None) == _lib.Q36_EINVAL
+    assert b"K=1024" in L.q36_last_error()
+    f.K, f.N = 2048, 200
+    assert L.q36_fp8_linear(C.byref(f), None) == _lib.Q36_EINVAL
+    assert b"N=200" in L.q36_last_error()
+    n = _lib.AddNormArgs()
+    n.T, n.H = 4, 4096
+    assert L.q36_add_rmsnorm(C.byref(n), None) == _lib.Q36_EINVAL
+    assert b"H=4096" in L.q36_last_error()
 
 
 def test_workspace_layout_is_consistent(L):
