@@ -1,0 +1,225 @@
+"""Config 5's hybrid decoder node on libq36: three gated-delta-net layers and one gated full-attention
+layer, each followed by the fp8 512-expert MoE block, the add-norms between the blocks, then the
+final norm and the int8 lm_head + greedy argmax.  One verify step of B requests x T tokens.
+
+Mirrors the reference's composition (R = qwen36_nodes_kb34, L = R/qwen36_layer, H = R/qwen36_lmhead8):
+the stock decoder layer the node replicates (L/layer.py:486-531): input add-norm, mixer, post add-norm,
+MoE; the projection + add-norm around the mixers (L/proj.py:60-112); the GDN mixer's in_proj split
+and verify (L/proj_fused.py:1-20, L/gdn_fused.py:37-57); the attention verify (L/attn_fused.py:110-124,
+232-273); the lm_head node with the greedy sampler (H/node.py:136-151).  Each layer's input norm is the
+add-norm fed by the previous layer's MoE output (the reference folds it into the combine,
+L/layer.py:66-145; here it is its own launch).  Every launch is a libq36 entry; nothing here computes.
+
+The projections are e4m3 with 128x128 block scales (the configuration's weight format), the KV
+cache e4m3 with one-token pages, the lm_head int8 per channel.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from .. import synth
+from ..qwen36_lmhead8 import lmhead8
+from . import attn_fused, gdn_fused, moe
+from .glue import Fp8Weight, LinearWorkspace, add_rmsnorm, fp8_linear, prepare_fp8_weight
+
+KINDS = ("gdn", "gdn", "gdn", "attn")
+HIDDEN, TOPK = 2048, 10
+GDN_QKV, GDN_Z, GDN_HV = 8192, 4096, 32
+IN_PROJ_N = GDN_QKV + GDN_Z + 2 * GDN_HV  # q|k|v, z, b, a = 12352 columns
+ATTN_SCALE = 1.0 / 16.0  # 1 / sqrt(256)
+
+
+@dataclass
+class GdnLayer:
+    in_proj: Fp8Weight   # [12352 (padded to 12416), 2048]
+    out_proj: Fp8Weight  # [2048, 4096]
+    conv_w: torch.Tensor
+    A_log: torch.Tensor
+    dt_bias: torch.Tensor
+    norm_w: torch.Tensor
+
+
+@dataclass
+class AttnLayer:
+    w: attn_fused.AttnWeights
+    q_norm_w: torch.Tensor
+    k_norm_w: torch.Tensor
+
+
+@dataclass
+class Layer:
+    kind: str
+    input_norm_w: torch.Tensor
+    post_norm_w: torch.Tensor
+    mixer: object
+    experts: moe.ExpertWeights
+    router_w: torch.Tensor
+    router_bias: torch.Tensor
+    gate_w: torch.Tensor
+
+
+@dataclass
+class HybridWeights:
+    layers: list
+    final_norm_w: torch.Tensor
+    lm_q: torch.Tensor
+    lm_s: torch.Tensor
+    E: int
+    eps: float = 1e-6
+
+
+@dataclass
+class HybridState:
+    """One verify step's inputs beside the hidden rows: B requests x T new tokens."""
+    B: int
+    T: int
+    conv_state: list          # per GDN layer bf16 [B, 8192, 3]
+    S: list                   # per GDN layer fp32 [B, 32, 128, 128]
+    k_cache: torch.Tensor     # e4m3 [slots, 2, 256]
+    v_cache: torch.Tensor
+    page_table: torch.Tensor  # int32 [B, stride]
+    seqlens: torch.Tensor     # int32 [B], keys including the T new tokens
+    out_loc: torch.Tensor     # int64 [B*T]: the new tokens' cache slots
+    positions: torch.Tensor   # int32 [B*T]
+    cos_sin: torch.Tensor     # fp32 [max_pos, 64]
+
+
+def make_weights(device, seed: int = 0, E: int = synth.E, V: int = 151936, zipf: float = 1.1) -> HybridWeights:
+    """Random-init weights of the architecture (no checkpoints), quantized once as the node prepares them."""
+    g = synth.gen(device, seed)
+    layers = []
+    for i, kind in enumerate(KINDS):
+        if kind == "gdn":
+            gi = synth.gdn_inputs(1, 1, device, seed=seed * 16 + i)
+            mixer = GdnLayer(prepare_fp8_weight(synth.randn((IN_PROJ_N, HIDDEN), g, device, 0.02)),
+                             prepare_fp8_weight(synth.randn((HIDDEN, GDN_Z), g, device, 0.02)),
+                             gi["conv_w"], gi["A_log"], gi["dt_bias"], gi["norm_w"])
+        else:
+            ai = synth.attn_inputs(1, device, seed=seed * 16 + i)
+            mixer = AttnLayer(attn_fused.prepare_weights(ai["wqg"], ai["wk"], ai["wv"], ai["wo"]), ai["q_norm_w"],
+                              ai["k_norm_w"])
+        mi = synth.moe_inputs(1, device, seed=seed * 16 + 8 + i, E=E, zipf=zipf)
+        ew = moe.prepare_experts(mi["w13"], mi["w2"], mi["sw13"], mi["sw2"], moe.Q36_MOE_FP8)
+        del mi["w13"], mi["w2"]
+        layers.append(Layer(kind, synth.randn((HIDDEN,), g, device, 0.1), synth.randn((HIDDEN,), g, device, 0.1),
+                            mixer, ew, mi["router_w"], mi["router_bias"], mi["gate_w"]))
+    lw = synth.randn((V, HIDDEN), g, device, 0.02)
+    lm_q, lm_s = lmhead8.quantize_rows(lw)
+    del lw
+    return HybridWeights(layers, synth.randn((HIDDEN,), g, device, 0.1), lm_q, lm_s, E)
+
+
+def make_state(B: int, T: int, ctx: int, device, seed: int = 0, extra_slots: int = 64) -> HybridState:
+    """The node's state for one verify step: GDN conv / recurrent states, and an e4m3 KV pool holding
+    ctx cached keys per request (values N(0,1) scaled per KV head) at random one-token slots, with the
+    T new tokens' slots already in the page table (as the engine assigns them)."""
+    g = synth.gen(device, seed)
+    n_gdn = KINDS.count("gdn")
+    conv = [synth.randn((B, GDN_QKV, 3), g, device) for _ in range(n_gdn)]
+    S = [torch.randn((B, GDN_HV, 128, 128), generator=g, device=device) * 0.1 for _ in range(n_gdn)]
+    slots = B * (ctx + T) + extra_slots
+    hs = 0.5 + 1.5 * torch.rand((1, 2, 1), generator=g, device=device)
+    kc = (torch.randn((slots, 2, 256), generator=g, device=device) * hs).to(torch.float8_e4m3fn).view(torch.uint8)
+    vc = (torch.randn((slots, 2, 256), generator=g, device=device) * hs).to(torch.float8_e4m3fn).view(torch.uint8)
+    perm = torch.randperm(slots, generator=g, device=device)[:B * (ctx + T)].to(torch.int32)
+    pt = perm.reshape(B, ctx + T).contiguous()
+    seqlens = torch.full((B,), ctx + T, dtype=torch.int32, device=device)
+    out_loc = pt[:, ctx:].reshape(-1).to(torch.int64).contiguous()
+    positions = (ctx + torch.arange(T, device=device, dtype=torch.int32)).repeat(B).contiguous()
+    return HybridState(B, T, conv, S, kc, vc, pt, seqlens, out_loc, positions,
+                       synth.rope_cos_sin(ctx + T + 1, device=device))
+
+
+@dataclass
+class HybridWorkspace:
+    """Every intermediate of one step of M = B*T rows (allocated once, reused by every step)."""
+    B: int
+    T: int
+    E: int
+    device: object
+    bufs: dict = field(default_factory=dict)
+
+    def __post_init__(self):
+        M, dev, bf = self.B * self.T, self.device, torch.bfloat16
+
+        def e(*shape, dtype=bf):
+            return torch.empty(shape, dtype=dtype, device=dev)
+        n_gdn = KINDS.count("gdn")
+        self.bufs = dict(
+            residual=e(M, HIDDEN), h=e(M, HIDDEN), o=e(M, HIDDEN), m=e(M, HIDDEN),
+            mixed=e(M, GDN_QKV), z=e(M, GDN_Z), b=e(M, GDN_HV), a=e(M, GDN_HV), gout=e(M, GDN_Z),
+            snaps=[e(self.B, self.T, GDN_HV, 128, 128, dtype=torch.float32) for _ in range(n_gdn)],
+            conv_out=[e(self.B, GDN_QKV, 3) for _ in range(n_gdn)],
+            attn=dict(q=e(M, 16, 256), gate=e(M, 16, 256), k=e(M, 2, 256), v=e(M, 2, 256),
+                      k8=e(M, 2, 256, dtype=torch.uint8), v8=e(M, 2, 256, dtype=torch.uint8)),
+            attn_out=e(M, 16, 256), ids=e(M, dtype=torch.int32))
+        self.lin2048 = LinearWorkspace(M, 2048, dev)
+        self.lin4096 = LinearWorkspace(M, 4096, dev)
+        self.attn = attn_fused.Workspace(M, dev)
+        self.decode = attn_fused.DecodeWorkspace(self.B, dev)
+        self.moe = moe.Workspace(self.E, HIDDEN, 512, TOPK, moe.Q36_MOE_FP8, dev, max_tokens=max(M, 1))
+        self.lmhead = lmhead8.Workspace(M, dev)
+
+
+def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorkspace, trace: dict | None = None,
+            stream=None) -> torch.Tensor:
+    """x bf16 [B*T, 2048] (the embedded tokens) -> greedy ids int32 [B*T].  With trace (a dict), the
+    inputs and outputs of every stage are kept there (copies) for stage-by-stage checks."""
+    b = ws.bufs
+    M = st.B * st.T
+    if x.shape != (M, HIDDEN):
+        raise ValueError(f"hybrid.forward: x must be [{M}, {HIDDEN}]")
+
+    def keep(name, t):
+        if trace is not None:
+            trace[name] = t.clone() if isinstance(t, torch.Tensor) else t
+
+    res, h = b["residual"], b["h"]
+    res.copy_(x)
+    add_rmsnorm(None, res, w.layers[0].input_norm_w, w.eps, out=h, stream=stream)
+    keep("x", x)
+    keep("h0", h)
+    gi = 0
+    for i, L in enumerate(w.layers):
+        keep(f"L{i}.in", h)
+        if L.kind == "gdn":
+            g = L.mixer
+            fp8_linear(h, g.in_proj, ws.lin2048, segments=[(0, b["mixed"]), (GDN_QKV, b["z"]),
+                                                           (GDN_QKV + GDN_Z, b["b"]),
+                                                           (GDN_QKV + GDN_Z + GDN_HV, b["a"])], stream=stream)
+            keep(f"L{i}.mixed", b["mixed"]), keep(f"L{i}.z", b["z"]), keep(f"L{i}.a", b["a"]), keep(f"L{i}.b", b["b"])
+            gdn_fused.gdn_verify_fused(b["mixed"], b["z"], b["a"], b["b"], st.conv_state[gi], g.conv_w, g.A_log,
+                                       g.dt_bias, st.S[gi], g.norm_w, w.eps, T=st.T, out=b["gout"],
+                                       snaps=b["snaps"][gi], conv_state_out=b["conv_out"][gi], stream=stream)
+            keep(f"L{i}.gout", b["gout"])
+            fp8_linear(b["gout"], g.out_proj, ws.lin4096, segments=[(0, b["o"])], stream=stream)
+            gi += 1
+        else:
+            a = L.mixer
+            p = attn_fused.attn_proj(h, a.w, a.q_norm_w, a.k_norm_w, w.eps, st.cos_sin, st.positions, ws.attn,
+                                     out=b["attn"], stream=stream)
+            for k in ("q", "gate", "k8", "v8"):
+                keep(f"L{i}.{k}", p[k])
+            attn_fused.attn_decode(p["q"], st.k_cache, st.v_cache, st.page_table, st.seqlens, st.T, ATTN_SCALE,
+                                   ws.decode, out_loc=st.out_loc, k_new=p["k8"], v_new=p["v8"], out=b["attn_out"],
+                                   stream=stream)
+            keep(f"L{i}.attn", b["attn_out"])
+            attn_fused.attn_oproj(b["attn_out"].view(M, 4096), p["gate"].view(M, 4096), a.w, ws.attn, out=b["o"],
+                                  stream=stream)
+        keep(f"L{i}.o", b["o"])
+        keep(f"L{i}.res_in", res)
+        add_rmsnorm(b["o"], res, L.post_norm_w, w.eps, out=h, stream=stream)
+        keep(f"L{i}.post", h)
+        keep(f"L{i}.res_mid", res)
+        moe.moe_row_batch(h, None, L.router_w, L.gate_w, L.experts, TOPK, ws.moe, out=b["m"],
+                          router_bias=L.router_bias, stream=stream)
+        keep(f"L{i}.moe", b["m"])
+        nxt = w.layers[i + 1].input_norm_w if i + 1 < len(w.layers) else w.final_norm_w
+        add_rmsnorm(b["m"], res, nxt, w.eps, out=h, stream=stream)
+        keep(f"L{i}.res_out", res)
+    keep("final", h)
+    lmhead8.w8a8_lmhead_argmax(h, w.lm_q, w.lm_s, ws.lmhead, norm_w=None, eps=w.eps, ids=b["ids"], stream=stream)
+    keep("ids", b["ids"])
+    return b["ids"]
