@@ -6,7 +6,8 @@ MoE layer over one batch of 64 tokens with every input resident in HBM.  value =
 layer.  Beside it: the roofline of the dominant kernel (the expert up-projection, HBM-bound), the
 other nodes' step times, and the CPU oracle timed on this host's cores on the same workload.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only moe,gdn,lmhead,attn,decode] [--copy-calib]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only moe,gdn,lmhead,attn,decode,hybrid]
+                [--copy-calib]
 """
 from __future__ import annotations
 
@@ -227,6 +228,44 @@ def bench_decode(args, torch, dev):
     return res
 
 
+def bench_hybrid(args, torch, dev):
+    """Config 5's hybrid node: 3 GDN layers + 1 attention layer, each + the fp8 512-expert MoE, the
+    add-norms, final norm, int8 lm_head [151936, 2048] + argmax, at 64 requests x 4 verify tokens
+    (256 rows; the attention over 4096 cached keys per request).  One step = one node forward,
+    captured as one graph and replayed; the replay's ids are checked against an eager step."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import hybrid
+
+    B, T, ctx = 64, 4, 4096
+    w = hybrid.make_weights(dev, seed=0)
+    st = hybrid.make_state(B, T, ctx, dev, seed=1)
+    ws = hybrid.HybridWorkspace(B, T, w.E, dev)
+    x = synth.randn((B * T, 2048), synth.gen(dev, 2), dev)
+    ids_eager = hybrid.forward(x, w, st, ws).clone()
+    for _ in range(max(1, args.warmup)):
+        hybrid.forward(x, w, st, ws)
+    torch.cuda.synchronize()
+    ms_eager = events_time(lambda: hybrid.forward(x, w, st, ws), max(3, args.steps // 5), torch)
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        hybrid.forward(x, w, st, ws)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            hybrid.forward(x, w, st, ws)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(ws.bufs["ids"], ids_eager):
+            raise RuntimeError("hybrid node: a graph replay's ids differ from the eager step's")
+    ms = events_time(graph.replay, args.steps, torch)
+    del w, st, ws
+    return dict(us_per_step=ms * 1e3, us_eager=ms_eager * 1e3, rows=B * T, tokens_per_s=B * T / (ms * 1e-3),
+                sequences=B, verify_tokens=T, context=ctx)
+
+
 def _decode_splits(B):
     import torch
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -293,7 +332,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="moe,gdn,lmhead,attn,decode",
+    ap.add_argument("--only", default="moe,gdn,lmhead,attn,decode,hybrid",
                     help="comma list of the nodes to run (the headline needs moe)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 256 MiB device copy (the reference kernel for HBM counters)")
@@ -311,7 +350,7 @@ def main():
     print(f"bench: MoE fp8 batch 64, steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
     moe_res = bench_moe(args, torch, dev)
     print(f"bench: MoE done ({moe_res['ms_graph'] * 1e3:.1f} us/layer)", file=sys.stderr, flush=True)
-    gdn_res = lmh_res = attn_res = dec_res = None
+    gdn_res = lmh_res = attn_res = dec_res = hyb_res = None
     if "gdn" in only:
         print("bench: GDN verify 32 x 5", file=sys.stderr, flush=True)
         gdn_res = bench_gdn(args, torch, dev)
@@ -325,6 +364,11 @@ def main():
     if "decode" in only:
         print("bench: decode / verify attention over a 4096-key e4m3 cache", file=sys.stderr, flush=True)
         dec_res = bench_decode(args, torch, dev)
+    if "hybrid" in only:
+        print("bench: hybrid node (3 GDN + 1 attention, each + MoE, lm_head) at 64 x 4 rows", file=sys.stderr,
+              flush=True)
+        hyb_res = bench_hybrid(args, torch, dev)
+        torch.cuda.empty_cache()
     if args.copy_calib:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -384,6 +428,13 @@ def main():
             for k, v in dec_res.items()}
         line["attn_decode"]["workload"] = ("16 q heads / 2 KV heads x 256, e4m3 KV cache, one-token pages at random "
                                            "slots; verify = 64 seqs x 4 draft tokens, decode = 256 seqs x 1")
+    if hyb_res:
+        line["hybrid_node"] = {
+            "us_per_step": round(hyb_res["us_per_step"], 1), "us_eager": round(hyb_res["us_eager"], 1),
+            "tokens_per_s": round(hyb_res["tokens_per_s"], 1), "rows": hyb_res["rows"],
+            "workload": "config 5: 3 GDN + 1 gated attention layer, each + fp8 MoE (512 experts, top-10, Zipf "
+                        "router), add-norms, final norm, int8 lm_head [151936, 2048] + argmax; 64 seqs x 4 verify "
+                        "tokens, 4096 cached keys; one captured graph per step"}
     if gdn_res:
         line["gdn_verify"] = {
             "us_per_step": round(gdn_res["us_per_step"], 2), "bytes": gdn_res["bytes"],
