@@ -43,7 +43,11 @@ constexpr int kPTR = 8;              // page-table ring entries per wave (one st
 constexpr int kVG = 4 * kDD + 64;    // a group of 4 value rows in LDS (64 bytes of padding)
 constexpr int kVW = 8 * kVG;         // one wave's 32 value rows
 constexpr int kVS = 4 * kVW;         // one stage of the four waves' value rows
-constexpr float kLazy = 8.f;         // rescale when a row max grows past the reference by 2^8
+constexpr float kLazy = 8.f;
+// Key and value reads carry the non-temporal cache policy (nt): each row is read once per call, and
+// inside the hybrid node (after a GDN verify has left ~0.5 GB of snapshot writes dirty in the
+// caches) the plain reads ran at half speed, evicting that data; measured 111 -> 63 us per call.
+constexpr int kKVAux = 2;         // rescale when a row max grows past the reference by 2^8
 static_assert(kPTR >= kPTD && (kPTR & (kPTR - 1)) == 0, "page-table ring");
 static_assert(kVS >= 2 * 16 * kDD * 4, "a stage holds two waves' fp32 output of one row tile at the merge");
 static_assert(kNS == 3, "the stage arrays and the prologue are written out for three stages");
@@ -183,20 +187,20 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
                  : "+v"(ks0), "+v"(ks1), "+v"(vsl0), "+v"(vsl1), "+v"(vsl2), "+v"(vsl3), "+v"(vsl4), "+v"(vsl5),
                    "+v"(vsl6), "+v"(vsl7)::"memory");
     const int kb0 = (ks0 * kKVH + h) * kDD + 32 * lg, kb1 = (ks1 * kKVH + h) * kDD + 32 * lg;
-    kf[Q][0][0] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0, 0, 0);
-    kf[Q][0][1] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0 + 16, 0, 0);
-    kf[Q][0][2] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0 + 128, 0, 0);
-    kf[Q][0][3] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0 + 144, 0, 0);
-    kf[Q][1][0] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1, 0, 0);
-    kf[Q][1][1] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1 + 16, 0, 0);
-    kf[Q][1][2] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1 + 128, 0, 0);
-    kf[Q][1][3] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1 + 144, 0, 0);
+    kf[Q][0][0] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0, 0, kKVAux);
+    kf[Q][0][1] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0 + 16, 0, kKVAux);
+    kf[Q][0][2] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0 + 128, 0, kKVAux);
+    kf[Q][0][3] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb0 + 144, 0, kKVAux);
+    kf[Q][1][0] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1, 0, kKVAux);
+    kf[Q][1][1] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1 + 16, 0, kKVAux);
+    kf[Q][1][2] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1 + 128, 0, kKVAux);
+    kf[Q][1][3] = __builtin_amdgcn_raw_buffer_load_b128(krs, kb1 + 144, 0, kKVAux);
     uint8_t* vb = stage(qc);
     const int vsl[8] = {vsl0, vsl1, vsl2, vsl3, vsl4, vsl5, vsl6, vsl7};
 #pragma unroll
     for (int m = 0; m < 8; ++m)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, vb + m * kVG, 16, (vsl[m] * kKVH + h) * kDD + 16 * (l16 ^ lg), 0, 0,
-                                               0);
+                                               kKVAux);
   };
   // per-lane state: running max (base 2) of query row 16 rt + l16, the lane's share of its weight
   // sum, and O^T (lane: row 16 rt + l16, dims 16 dt + 4 lg + r)
