@@ -6,7 +6,8 @@ MoE layer over one batch of 64 tokens with every input resident in HBM.  value =
 layer.  Beside it: the roofline of the dominant kernel (the expert up-projection, HBM-bound), the
 other nodes' step times, and the CPU oracle timed on this host's cores on the same workload.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only moe,gdn,lmhead,attn,decode,hybrid]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                [--only moe,gdn,gdn_ring,lmhead,attn,decode,hybrid]
                 [--copy-calib]
 """
 from __future__ import annotations
@@ -150,6 +151,52 @@ def bench_gdn(args, torch, dev):
     algo = (state + T * state + R * 8192 * 2 + R * 4096 * 2 + 2 * R * 32 * 2 + 2 * B * 8192 * 3 * 2
             + 8192 * 4 * 2 + R * 4096 * 2)
     return dict(us_per_step=ms * 1e3, bytes=algo, gbs=algo / (ms * 1e-3) / 1e9, sequences=B, positions=T)
+
+
+def bench_gdn_ring(args, torch, dev):
+    """The served ReplaySSM form of config 3's verify step: 32 requests x (1 + 4) positions from a
+    read-only checkpoint with 8 committed ring entries each; the 5 window entries are appended.
+    Four independent request sets with their own pools (4 x 70 MB of checkpoint, more than the
+    256 MB last-level cache) are cycled, so every call reads its checkpoint from HBM; the calls are
+    captured in one graph and replayed."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import gdn_fused
+
+    B, T, WP, SETS, REP = 32, 5, 8, 4, 5
+    sets = [synth.gdn_ring_inputs(B, T, dev, seed=s, wp=WP) for s in range(SETS)]
+    outs = [torch.empty((B * T, 4096), dtype=torch.bfloat16, device=dev) for _ in range(SETS)]
+    keys = ("mixed", "z", "a", "b", "conv_state", "conv_w", "window", "A_log", "dt_bias", "h0", "d_ring", "dlo_ring",
+            "k_ring", "klo_ring", "g_ring", "qsl", "state_idx", "replay_idx", "win_idx", "write_pos", "cache_base",
+            "norm_w")
+
+    def call(i):
+        d = sets[i]
+        gdn_fused.gdn_verify_ring(*(d[k] for k in keys), 1e-6, d["scale"], T=T, out=outs[i])
+
+    for _ in range(max(1, args.warmup)):
+        for i in range(SETS):
+            call(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            for _ in range(REP):
+                for i in range(SETS):
+                    call(i)
+    torch.cuda.current_stream().wait_stream(s)
+    graph.replay()
+    torch.cuda.synchronize()
+    ms = events_time(graph.replay, max(2, args.steps // 5), torch) / (REP * SETS)
+    R = B * T
+    # checkpoint rows read; committed ring entries read (k and d high parts, g); window entries
+    # appended (k and d high + low, g); activations in, conv state in and out, window records, out
+    algo = (B * 32 * 128 * 128 * 4 + B * WP * (16 * 128 * 2 + 32 * 128 * 2 + 32 * 4)
+            + B * T * (16 * 128 * 4 + 32 * 128 * 4 + 32 * 4) + R * 8192 * 2 + R * 4096 * 2 + 2 * R * 32 * 2
+            + 2 * B * 8192 * 3 * 2 + B * 8192 * (T + 2) * 2 + 8192 * 4 * 2 + R * 4096 * 2)
+    return dict(us_per_step=ms * 1e3, bytes=algo, gbs=algo / (ms * 1e-3) / 1e9, requests=B, positions=T,
+                committed=WP)
 
 
 def bench_attn(args, torch, dev):
@@ -332,7 +379,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="moe,gdn,lmhead,attn,decode,hybrid",
+    ap.add_argument("--only", default="moe,gdn,gdn_ring,lmhead,attn,decode,hybrid",
                     help="comma list of the nodes to run (the headline needs moe)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 256 MiB device copy (the reference kernel for HBM counters)")
@@ -350,11 +397,16 @@ def main():
     print(f"bench: MoE fp8 batch 64, steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
     moe_res = bench_moe(args, torch, dev)
     print(f"bench: MoE done ({moe_res['ms_graph'] * 1e3:.1f} us/layer)", file=sys.stderr, flush=True)
-    gdn_res = lmh_res = attn_res = dec_res = hyb_res = None
+    gdn_res = ring_res = lmh_res = attn_res = dec_res = hyb_res = None
     if "gdn" in only:
         print("bench: GDN verify 32 x 5", file=sys.stderr, flush=True)
         gdn_res = bench_gdn(args, torch, dev)
         print(f"bench: GDN done ({gdn_res['us_per_step']:.1f} us/step)", file=sys.stderr, flush=True)
+    if "gdn_ring" in only:
+        print("bench: GDN verify over the ReplaySSM ring 32 x 5", file=sys.stderr, flush=True)
+        ring_res = bench_gdn_ring(args, torch, dev)
+        print(f"bench: GDN ring done ({ring_res['us_per_step']:.1f} us/step)", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
     if "lmhead" in only:
         print("bench: lm_head + argmax 2048 x 151936", file=sys.stderr, flush=True)
         lmh_res = bench_lmhead(args, torch, dev)
@@ -440,6 +492,12 @@ def main():
             "us_per_step": round(gdn_res["us_per_step"], 2), "bytes": gdn_res["bytes"],
             "achieved_gbs": round(gdn_res["gbs"], 1), "frac_hbm": round(gdn_res["gbs"] / HBM_PEAK_GBS, 4),
             "workload": "32 sequences x (1+4) positions, 16 QK / 32 V heads x 128, fp32 state + per-position snapshots"}
+    if ring_res:
+        line["gdn_verify_ring"] = {
+            "us_per_step": round(ring_res["us_per_step"], 2), "bytes": ring_res["bytes"],
+            "achieved_gbs": round(ring_res["gbs"], 1), "frac_hbm": round(ring_res["gbs"] / HBM_PEAK_GBS, 4),
+            "workload": "32 requests x (1+4) positions from a read-only fp32 checkpoint, 8 committed ring entries "
+                        "each, 5 appended (the served ReplaySSM form); 4 request sets cycled in one graph"}
     print(json.dumps(line), flush=True)
 
 

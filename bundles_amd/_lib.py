@@ -39,6 +39,19 @@ class GdnArgs(C.Structure):
                 ("eps", C.c_float), ("out", P), ("snaps", P)]
 
 
+I64 = C.c_int64
+
+
+class GdnRingArgs(C.Structure):
+    _fields_ = [("B", I32), ("T", I32), ("rows", I32), ("slots", I32), ("rslots", I32), ("wslots", I32),
+                ("mixed", P), ("z", P), ("a", P), ("b", P), ("conv_state", P), ("cs_slot", I64), ("conv_w", P),
+                ("window", P), ("win_slot", I64), ("A_log", P), ("dt_bias", P), ("dt_f32", I32), ("h0", P),
+                ("d_ring", P), ("dlo_ring", P), ("d_slot", I64), ("dlo_slot", I64), ("k_ring", P), ("klo_ring", P),
+                ("k_slot", I64), ("klo_slot", I64), ("g_ring", P), ("g_slot", I64), ("qsl", P), ("state_idx", P),
+                ("replay_idx", P), ("win_idx", P), ("idx_i64", I32), ("write_pos", P), ("cache_base", P),
+                ("norm_w", P), ("eps", C.c_float), ("scale", C.c_float), ("out", P)]
+
+
 class AttnArgs(C.Structure):
     _fields_ = [("T", I32), ("max_pos", I32), ("x", P), ("wqkv", P), ("sqkv", P), ("q_norm_w", P),
                 ("k_norm_w", P), ("eps", C.c_float), ("cos_sin", P), ("positions", P), ("q", P), ("gate", P),
@@ -89,6 +102,7 @@ SYMBOLS = [
     ("q36_moe_combine", I32, [C.POINTER(MoeArgs), P]),
     ("q36_moe_forward", I32, [C.POINTER(MoeArgs), P]),
     ("q36_gdn_verify", I32, [C.POINTER(GdnArgs), P]),
+    ("q36_gdn_verify_ring", I32, [C.POINTER(GdnRingArgs), P]),
     ("q36_attn_workspace_bytes", SZ, [I32]),
     ("q36_oproj_workspace_bytes", SZ, [I32]),
     ("q36_attn_proj", I32, [C.POINTER(AttnArgs), P]),

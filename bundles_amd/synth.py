@@ -73,6 +73,52 @@ def gdn_inputs(B: int = 32, T: int = 5, device="cpu", seed: int = 0):
     )
 
 
+def gdn_ring_inputs(B: int = 32, T: int = 4, device="cpu", seed: int = 0, wp=None, padded=()):
+    """A ReplaySSM verify step: the config-3 front of gdn_inputs (mixed, z, a, b, conv weights,
+    gates, norm weight) over the served pools.  Pools have a few spare slots and every index is a
+    distinct random slot: checkpoint h0 [slots, 32, 128, 128] ~ N(0, 0.1), conv state N(0, 1),
+    rings holding write_pos committed entries per request (wp: an int, or None for U[0, 16 - T])
+    at a random cache_base: d ~ N(0, 0.3) bf16 with its low part, unit keys with their low part,
+    g from the gate formula on a ~ N(0, 1).  Requests listed in `padded` get state_idx -1."""
+    f = gdn_inputs(B, T, device, seed)
+    g = gen(device, seed + 7919)
+    slots, rslots, wslots = B + 3, B + 2, B + 1
+
+    def pick(n):
+        return torch.randperm(n, generator=g, device=device)[:B].to(torch.int64)
+
+    state_idx, replay_idx, win_idx = pick(slots), pick(rslots), pick(wslots)
+    for r in padded:
+        state_idx[r] = -1
+    if wp is None:
+        write_pos = torch.randint(0, 16 - T + 1, (rslots,), generator=g, device=device, dtype=torch.int32)
+    else:
+        write_pos = torch.full((rslots,), int(wp), dtype=torch.int32, device=device)
+    cache_base = torch.randint(0, 16, (rslots,), generator=g, device=device, dtype=torch.int32)
+    d32 = torch.randn((rslots, 32, 16, 128), generator=g, device=device) * 0.3
+    k32 = torch.randn((rslots, 16, 16, 128), generator=g, device=device)
+    k32 = k32 / k32.norm(dim=-1, keepdim=True)
+    d_ring = d32.to(torch.bfloat16)
+    k_ring = k32.to(torch.bfloat16)
+    xg = torch.randn((rslots, 32, 16), generator=g, device=device) + f["dt_bias"][None, :, None]
+    g_ring = -torch.exp(f["A_log"])[None, :, None] * torch.nn.functional.softplus(xg)
+    f.update(
+        rows=B * T, slots=slots, rslots=rslots, wslots=wslots,
+        conv_state=randn((slots, 8192, 3), g, device),
+        window=torch.zeros((wslots, 8192, T + 2), dtype=torch.bfloat16, device=device),
+        h0=torch.randn((slots, 32, 128, 128), generator=g, device=device) * 0.1,
+        d_ring=d_ring, dlo_ring=(d32 - d_ring.float()).to(torch.bfloat16),
+        k_ring=k_ring, klo_ring=(k32 - k_ring.float()).to(torch.bfloat16),
+        g_ring=g_ring.contiguous(),
+        qsl=torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=device),
+        state_idx=state_idx, replay_idx=replay_idx, win_idx=win_idx,
+        write_pos=write_pos, cache_base=cache_base,
+        scale=128 ** -0.5,
+    )
+    del f["S0"]
+    return f
+
+
 def rope_cos_sin(max_pos: int, rot_dim: int = 64, theta: float = 1e7, device="cpu") -> torch.Tensor:
     """fp32 [max_pos, rot_dim]: cos | sin of pos * theta^(-2i/rot_dim), i < rot_dim/2, from fp64."""
     inv = theta ** (-torch.arange(0, rot_dim, 2, dtype=torch.float64) / rot_dim)

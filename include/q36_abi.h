@@ -12,6 +12,9 @@
  *                         (L/i8x_decode.py:528-605; L/qk_moe_up16.cu:915; L/qk_moe_dn16.cu:301;
  *                          L/qk_route.cu:1270)
  *   q36_gdn_verify     <- qk_gdn_verify.gdn_verify_fused           (L/qk_gdn_verify.cu:841-849)
+ *                         with per-position state snapshots in place of the replay ring
+ *   q36_gdn_verify_ring <- qk_gdn_verify.gdn_verify_fused over the ReplaySSM ring
+ *                         (L/qk_gdn_verify.cu:841-990; L/gdn_fused.py:37-57)
  *   q36_attn_proj      <- qkv_proj + attn_prefill_front            (L/qk_proj_decode.cu:434;
  *                         L/qk_attn_verify.cu:981)
  *   q36_attn_oproj     <- o_proj of the gated attention output    (L/attn_fused.py:232-273;
@@ -156,6 +159,72 @@ typedef struct q36_gdn_args {
   float* snaps;
 } q36_gdn_args;
 int q36_gdn_verify(const q36_gdn_args* a, q36_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * GDN speculative verify over the ReplaySSM ring: the served form of gdn_verify_fused
+ * (L/qk_gdn_verify.cu:841-849, argument checks :850-919; glue L/gdn_fused.py:37-57).  The
+ * rollback state is not materialised: the fp32 checkpoint h0 is read only, the committed history
+ * is a 16-entry circular ring of (d, k, g) entries, and the window's entries are appended to it.
+ *   Request r (< B) owns rows qsl[r] .. qsl[r] + T - 1 of mixed / z / a / b / out.
+ *   state_idx[r]  checkpoint and conv-state slot; replay_idx[r] ring slot; win_idx[r] draft-window
+ *                 slot.  state_idx < 0 marks a padded request (the reference's rule); so does any
+ *                 index outside [0, slots) / [0, rslots) / [0, wslots): its rows of out are zeroed
+ *                 and nothing else is written.  A request whose rows fall outside [0, rows) is
+ *                 skipped entirely.
+ *   idx_i64 bit 0 / 1 / 2: state_idx / replay_idx / win_idx hold int64 (else int32)
+ *   write_pos[rs] committed entries n (clamped to [0, 16]); cache_base[rs] physical slot of
+ *                 logical entry 0 (entry c lives at (cache_base + c) & 15)
+ *   conv_state bf16 [slots, 8192, 3] (slot stride cs_slot elements), rolled in place to the last
+ *                 three inputs; window bf16 [wslots, 8192, T + 2] (slot stride win_slot): per
+ *                 channel [s1 s2 x0 .. x_{T-1}], whose rows [t, t + 3) are the conv state after
+ *                 draft t
+ *   h0 fp32 [slots, 32, 128 (v), 128 (k)], read only
+ *   d_ring, dlo_ring bf16 [rslots, 32, 16, 128]; k_ring, klo_ring bf16 [rslots, 16, 16, 128];
+ *   g_ring fp32 [rslots, 32, 16] (slot strides *_slot elements).  The verify reads the high
+ *                 parts of the n committed entries and appends the window's d (the delta-rule
+ *                 update beta (v - e^g S k)), unit key k and gate g at logical n + t while
+ *                 n + t < 16, each bf16 value split into high and low parts.
+ *   dt_bias fp32 (dt_f32 = 1) or bf16 [32]; A_log fp32 [32]; norm_w bf16 [128]; scale: the q
+ *                 scale (128^-1/2 for this model)
+ * 1 <= T <= 8; h0, z, conv_state, conv_w, the rings and out 16-byte aligned, the slot strides
+ * multiples of 16 bytes.  Requests must name distinct slots (they write them).  B = 0 launches
+ * nothing. */
+typedef struct q36_gdn_ring_args {
+  int32_t B, T, rows;
+  int32_t slots, rslots, wslots;
+  const void* mixed;
+  const void* z;
+  const void* a;
+  const void* b;
+  void* conv_state;
+  int64_t cs_slot;
+  const void* conv_w;
+  void* window;
+  int64_t win_slot;
+  const float* A_log;
+  const void* dt_bias;
+  int32_t dt_f32;
+  const float* h0;
+  void* d_ring;
+  void* dlo_ring;
+  int64_t d_slot, dlo_slot;
+  void* k_ring;
+  void* klo_ring;
+  int64_t k_slot, klo_slot;
+  float* g_ring;
+  int64_t g_slot;
+  const int32_t* qsl;
+  const void* state_idx;
+  const void* replay_idx;
+  const void* win_idx;
+  int32_t idx_i64;
+  const int32_t* write_pos;
+  const int32_t* cache_base;
+  const void* norm_w;
+  float eps, scale;
+  void* out;
+} q36_gdn_ring_args;
+int q36_gdn_verify_ring(const q36_gdn_ring_args* a, q36_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
  * Fused gated full-attention projections (16 q heads x 256 with an output gate per head,

@@ -50,6 +50,14 @@ class GdnArgs(C.Structure):
                 ("out", P), ("snaps", P), ("use_f64", I32), ("n_threads", I32)]
 
 
+class GdnRingArgs(C.Structure):
+    _fields_ = [("B", I32), ("T", I32), ("mixed", P), ("z", P), ("a", P), ("b", P), ("conv_state", P),
+                ("conv_w", P), ("window", P), ("A_log", P), ("dt_bias", P), ("h0", P), ("d_ring", P),
+                ("dlo_ring", P), ("k_ring", P), ("klo_ring", P), ("g_ring", P), ("qsl", P), ("state_idx", P),
+                ("replay_idx", P), ("win_idx", P), ("write_pos", P), ("cache_base", P), ("norm_w", P),
+                ("eps", C.c_float), ("scale", C.c_float), ("out", P), ("use_f64", I32), ("n_threads", I32)]
+
+
 class AttnArgs(C.Structure):
     _fields_ = [("T", I32), ("x", P), ("wqg", P), ("sqg", P), ("wk", P), ("sk", P), ("wv", P), ("sv", P),
                 ("q_norm_w", P), ("k_norm_w", P), ("eps", C.c_float), ("cos_sin", P), ("positions", P),
@@ -95,7 +103,8 @@ def _declare(L):
     L.q36o_add_rmsnorm.argtypes = [I32, I32, P, P, P, C.c_float, P]
     L.q36o_route.restype = I32
     L.q36o_route.argtypes = [P, P, P, P, I32, I32, I32, I32, P, P, P, P, P, P, P, P, P]
-    for fn, st in (("q36o_moe", MoeArgs), ("q36o_gdn_verify", GdnArgs), ("q36o_attn_proj", AttnArgs),
+    for fn, st in (("q36o_moe", MoeArgs), ("q36o_gdn_verify", GdnArgs), ("q36o_gdn_verify_ring", GdnRingArgs),
+                   ("q36o_attn_proj", AttnArgs),
                    ("q36o_attn_oproj", OprojArgs), ("q36o_lmhead", LmheadArgs), ("q36o_attn_decode", DecodeArgs)):
         f = getattr(L, fn)
         f.restype = I32
@@ -244,6 +253,37 @@ def gdn_verify(B, T, mixed, z, a, b, conv_state, conv_w, A_log, dt_bias, S0, nor
     if rc:
         raise ValueError("q36o_gdn_verify rejected the shapes")
     return out, snaps, cs
+
+
+def gdn_verify_ring(B, T, mixed, z, a, b, conv_state, conv_w, window, A_log, dt_bias, h0, d_ring, dlo_ring,
+                    k_ring, klo_ring, g_ring, qsl, state_idx, replay_idx, win_idx, write_pos, cache_base, norm_w,
+                    eps=1e-6, scale=128 ** -0.5, use_f64=False, n_threads=0):
+    """The ring verify (q36o_gdn_verify_ring) on copies of the mutable pools.
+
+    Returns a dict: out bf16 [rows, 4096] and the updated conv_state, window, d/dlo/k/klo/g rings."""
+    res = {k: np.array(v, copy=True, order="C") for k, v in (
+        ("conv_state", conv_state), ("window", window), ("d_ring", d_ring), ("dlo_ring", dlo_ring),
+        ("k_ring", k_ring), ("klo_ring", klo_ring), ("g_ring", g_ring))}
+    rows = np.ascontiguousarray(mixed).shape[0]
+    res["out"] = np.empty((rows, 4096), np.uint16)
+    keep = {k: np.ascontiguousarray(v) for k, v in (("mixed", mixed), ("z", z), ("a", a), ("b", b))}
+    cw = np.ascontiguousarray(conv_w, np.uint16)
+    al = np.ascontiguousarray(A_log, np.float32)
+    dt = np.ascontiguousarray(dt_bias, np.float32)
+    hh = np.ascontiguousarray(h0, np.float32)
+    nw = np.ascontiguousarray(norm_w, np.uint16)
+    q = np.ascontiguousarray(qsl, np.int32)
+    si, ri, wi = (np.ascontiguousarray(v, np.int64) for v in (state_idx, replay_idx, win_idx))
+    wpos = np.ascontiguousarray(write_pos, np.int32)
+    cbase = np.ascontiguousarray(cache_base, np.int32)
+    args = GdnRingArgs(B, T, _p(keep["mixed"]), _p(keep["z"]), _p(keep["a"]), _p(keep["b"]), _p(res["conv_state"]),
+                       _p(cw), _p(res["window"]), _p(al), _p(dt), _p(hh), _p(res["d_ring"]), _p(res["dlo_ring"]),
+                       _p(res["k_ring"]), _p(res["klo_ring"]), _p(res["g_ring"]), _p(q), _p(si), _p(ri), _p(wi),
+                       _p(wpos), _p(cbase), _p(nw), eps, scale, _p(res["out"]), int(use_f64), n_threads)
+    rc = lib().q36o_gdn_verify_ring(C.byref(args))
+    if rc:
+        raise ValueError("q36o_gdn_verify_ring rejected the shapes")
+    return res
 
 
 # ---------------------------------------------------------------- attention projections

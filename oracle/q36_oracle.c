@@ -577,6 +577,188 @@ int q36o_gdn_verify(const q36o_gdn_args* a) {
   return 0;
 }
 
+/* ---- GDN verify over the ReplaySSM ring ---- */
+enum { GRING = 16 };
+
+/* One (request, value head) unit of the ring verify (L/qk_gdn_verify.cu:575-791 restated
+ * sequentially).  The history state is materialised first:
+ *   pre_c = g_0 + .. + g_c (logical order, sequential), total = pre_{n-1},
+ *   decay_c = exp(total - pre_c), td = exp(total)                        (:634-648)
+ *   S = td * h0, then S += (decay_c * dhat_c) khat_c^T for c = 0 .. n-1   (:709-721, :745-751)
+ * with the ring's bf16 high parts (the verify never reads the low parts, :598-605, :711).  The
+ * window then runs the sequential delta rule of gdn_unit; d_t = beta_t (v_t - e^{g_t} S_{t-1} k_t)
+ * is the ring's d entry (the WY form's D of :752-755). */
+static void gdn_ring_unit(const q36o_gdn_ring_args* a, int r, int hv, const float* convd /* [T][8192] */) {
+  const int T = a->T, hk = hv / 2;
+  const int64_t slot = a->state_idx[r], rp = a->replay_idx[r];
+  const size_t bos = (size_t)a->qsl[r];
+  int wp = a->write_pos[rp], cb = a->cache_base[rp];
+  const int nv = wp < 0 ? 0 : wp > GRING ? GRING : wp;
+  float q[8][GK], kk[8][GK], vv[8][GV], g[8], beta[8];
+  for (int t = 0; t < T; ++t) {
+    const float* row = convd + (size_t)t * GQKV;
+    float nq = 0.f, nk = 0.f;
+    for (int i = 0; i < GK; ++i) {
+      float xq = row[hk * GK + i], xk = row[GHK * GK + hk * GK + i];
+      nq = nq + xq * xq;
+      nk = nk + xk * xk;
+    }
+    float rq = (1.f / sqrtf(nq + 1e-6f)) * a->scale, rk = 1.f / sqrtf(nk + 1e-6f);
+    for (int i = 0; i < GK; ++i) {
+      q[t][i] = row[hk * GK + i] * rq;
+      kk[t][i] = row[GHK * GK + hk * GK + i] * rk;
+    }
+    for (int i = 0; i < GV; ++i) vv[t][i] = row[2 * GHK * GK + hv * GV + i];
+    const size_t rr = bos + t;
+    float av = q36o_bf16_to_f32(a->a[rr * GHV + hv]), bv = q36o_bf16_to_f32(a->b[rr * GHV + hv]);
+    float xg = av + a->dt_bias[hv];
+    float sp = xg <= 20.f ? logf(1.f + q36o_expf(xg)) : xg;
+    g[t] = -q36o_expf(a->A_log[hv]) * sp;
+    beta[t] = sigmoidf_q(bv);
+  }
+  /* committed history, logical order */
+  const uint16_t* kr = a->k_ring + ((size_t)rp * GHK + hk) * GRING * GK;
+  const uint16_t* dr = a->d_ring + ((size_t)rp * GHV + hv) * GRING * GV;
+  const float* gr = a->g_ring + ((size_t)rp * GHV + hv) * GRING;
+  float pre[GRING], decay[GRING], total = 0.f;
+  for (int c = 0; c < nv; ++c) {
+    total = total + gr[(cb + c) & (GRING - 1)];
+    pre[c] = total;
+  }
+  for (int c = 0; c < nv; ++c) decay[c] = q36o_expf(total - pre[c]);
+  const float td = q36o_expf(total);
+  const float* H = a->h0 + ((size_t)slot * GHV + hv) * GV * GK;
+  float nw[GV];
+  for (int i = 0; i < GV; ++i) nw[i] = q36o_bf16_to_f32(a->norm_w[i]);
+  float o[8][GV], d[8][GV];
+  if (a->use_f64) {
+    double* S = (double*)malloc(sizeof(double) * GV * GK);
+    for (int i = 0; i < GV * GK; ++i) S[i] = (double)td * H[i];
+    for (int c = 0; c < nv; ++c) {
+      const int p = (cb + c) & (GRING - 1);
+      for (int v = 0; v < GV; ++v) {
+        double dc = (double)decay[c] * q36o_bf16_to_f32(dr[p * GV + v]);
+        for (int j = 0; j < GK; ++j) S[v * GK + j] += dc * q36o_bf16_to_f32(kr[p * GK + j]);
+      }
+    }
+    for (int t = 0; t < T; ++t) {
+      double eg = exp((double)g[t]);
+      for (int v = 0; v < GV; ++v) {
+        double* Sr = S + (size_t)v * GK;
+        double kv = 0.0;
+        for (int c = 0; c < GK; ++c) kv += Sr[c] * kk[t][c];
+        double u = beta[t] * (vv[t][v] - eg * kv), ov = 0.0;
+        for (int c = 0; c < GK; ++c) {
+          Sr[c] = eg * Sr[c] + u * kk[t][c];
+          ov += Sr[c] * q[t][c];
+        }
+        d[t][v] = (float)u;
+        o[t][v] = bf((float)ov);
+      }
+    }
+    free(S);
+  } else {
+    float* S = (float*)malloc(sizeof(float) * GV * GK);
+    for (int i = 0; i < GV * GK; ++i) S[i] = td * H[i];
+    for (int c = 0; c < nv; ++c) {
+      const int p = (cb + c) & (GRING - 1);
+      for (int v = 0; v < GV; ++v) {
+        float dc = decay[c] * q36o_bf16_to_f32(dr[p * GV + v]);
+        for (int j = 0; j < GK; ++j) S[v * GK + j] = fmaf(dc, q36o_bf16_to_f32(kr[p * GK + j]), S[v * GK + j]);
+      }
+    }
+    for (int t = 0; t < T; ++t) {
+      float eg = q36o_expf(g[t]);
+      for (int v = 0; v < GV; ++v) {
+        float* Sr = S + (size_t)v * GK;
+        float kv = 0.f;
+        for (int c = 0; c < GK; ++c) kv = fmaf(Sr[c], kk[t][c], kv);
+        float u = beta[t] * (vv[t][v] - eg * kv), ov = 0.f;
+        for (int c = 0; c < GK; ++c) {
+          Sr[c] = fmaf(eg, Sr[c], u * kk[t][c]);
+          ov = fmaf(Sr[c], q[t][c], ov);
+        }
+        d[t][v] = u;
+        o[t][v] = bf(ov);
+      }
+    }
+    free(S);
+  }
+  /* ring appends at logical nv + t while they fit (k :583-596, g :631, d :770-781) */
+  for (int t = 0; t < T && nv + t < GRING; ++t) {
+    const int p = (cb + nv + t) & (GRING - 1);
+    uint16_t* dh = a->d_ring + (((size_t)rp * GHV + hv) * GRING + p) * GV;
+    uint16_t* dl = a->dlo_ring + (((size_t)rp * GHV + hv) * GRING + p) * GV;
+    for (int v = 0; v < GV; ++v) {
+      dh[v] = q36o_f32_to_bf16(d[t][v]);
+      dl[v] = q36o_f32_to_bf16(d[t][v] - q36o_bf16_to_f32(dh[v]));
+    }
+    a->g_ring[((size_t)rp * GHV + hv) * GRING + p] = g[t];
+    if ((hv & 1) == 0) {
+      uint16_t* kh = a->k_ring + (((size_t)rp * GHK + hk) * GRING + p) * GK;
+      uint16_t* kl = a->klo_ring + (((size_t)rp * GHK + hk) * GRING + p) * GK;
+      for (int j = 0; j < GK; ++j) {
+        kh[j] = q36o_f32_to_bf16(kk[t][j]);
+        kl[j] = q36o_f32_to_bf16(kk[t][j] - q36o_bf16_to_f32(kh[j]));
+      }
+    }
+  }
+  for (int t = 0; t < T; ++t) {
+    float ss = 0.f;
+    for (int v = 0; v < GV; ++v) ss = ss + o[t][v] * o[t][v];
+    float rstd = 1.f / sqrtf(ss / (float)GV + a->eps);
+    const size_t rr = bos + t;
+    for (int v = 0; v < GV; ++v) {
+      float zz = q36o_bf16_to_f32(a->z[rr * GZ + hv * GV + v]);
+      a->out[rr * GZ + hv * GV + v] = q36o_f32_to_bf16(((o[t][v] * rstd) * nw[v]) * (zz * sigmoidf_q(zz)));
+    }
+  }
+}
+
+int q36o_gdn_verify_ring(const q36o_gdn_ring_args* a) {
+  const int B = a->B, T = a->T;
+  if (B < 0 || T < 1 || T > 8) return -1;
+  if (a->n_threads > 0) omp_set_num_threads(a->n_threads);
+  float* convd = (float*)malloc(sizeof(float) * ((size_t)B * T * GQKV + 1));
+  /* conv per request: window record [s1 s2 x0 .. x_{T-1}], state rolled to the last three inputs
+   * (L/qk_gdn_verify.cu:277-291 record layout, :607-613 the roll after every read) */
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < B; ++r) {
+    const int64_t slot = a->state_idx[r];
+    const size_t bos = (size_t)a->qsl[r];
+    if (slot < 0) {
+      for (int t = 0; t < T; ++t)
+        for (int c = 0; c < GZ; ++c) a->out[(bos + t) * GZ + c] = 0;
+      continue;
+    }
+    const int64_t ws = a->win_idx[r];
+    for (int c = 0; c < GQKV; ++c) {
+      float w[8 + 3];
+      uint16_t* st = a->conv_state + ((size_t)slot * GQKV + c) * 3;
+      for (int i = 0; i < 3; ++i) w[i] = q36o_bf16_to_f32(st[i]);
+      for (int t = 0; t < T; ++t) w[3 + t] = q36o_bf16_to_f32(a->mixed[(bos + t) * GQKV + c]);
+      float cw[4];
+      for (int i = 0; i < 4; ++i) cw[i] = q36o_bf16_to_f32(a->conv_w[(size_t)c * 4 + i]);
+      for (int t = 0; t < T; ++t) {
+        float acc = bf(w[t] * cw[0]);
+        acc = acc + bf(w[t + 1] * cw[1]);
+        acc = acc + bf(w[t + 2] * cw[2]);
+        acc = acc + bf(w[t + 3] * cw[3]);
+        convd[((size_t)r * T + t) * GQKV + c] = bf(acc / (1.f + q36o_expf(-acc)));
+      }
+      uint16_t* rec = a->window + ((size_t)ws * GQKV + c) * (T + 2);
+      for (int i = 0; i < T + 2; ++i) rec[i] = q36o_f32_to_bf16(w[1 + i]);
+      for (int i = 0; i < 3; ++i) st[i] = q36o_f32_to_bf16(w[T + i]);
+    }
+  }
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  for (int r = 0; r < B; ++r)
+    for (int hv = 0; hv < GHV; ++hv)
+      if (a->state_idx[r] >= 0) gdn_ring_unit(a, r, hv, convd + (size_t)r * T * GQKV);
+  free(convd);
+  return 0;
+}
+
 /* ------------------------------------------------------------------------------------ */
 /* attention projections                                                                */
 /* ------------------------------------------------------------------------------------ */

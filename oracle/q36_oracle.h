@@ -90,6 +90,46 @@ typedef struct {
 } q36o_gdn_args;
 int q36o_gdn_verify(const q36o_gdn_args* a);
 
+/* ---- GDN speculative verify over the ReplaySSM ring (read-only checkpoint + 16-entry ring) ----
+ * L/qk_gdn_verify.cu:1-20 (design), :586-593 (ring keys), :616-634 (gates, g ring), :636-651
+ * (history decay), :684-762 (window recurrence), :770-781 (d ring); host checks :850-919.
+ * Request r owns rows qsl[r] .. qsl[r] + T - 1; state_idx < 0 marks a padded request (zero output,
+ * nothing else written).  The history state is td * h0 + sum_c decay_c dhat_c khat_c^T over the
+ * committed entries c < write_pos (logical order, physical slot (cache_base + c) & 15), with the
+ * bf16 high parts only; the window's d, k (high and low bf16 parts) and g are appended at logical
+ * positions write_pos + t while they fit the ring.  conv_state is rolled in place and the draft
+ * windows [s1 s2 x0 .. x_{T-1}] are written per channel. */
+typedef struct {
+  int B, T;                 /* requests, tokens per request (1..8) */
+  const uint16_t* mixed;    /* bf16 [rows, 8192] */
+  const uint16_t* z;        /* bf16 [rows, 4096] */
+  const uint16_t* a;        /* bf16 [rows, 32] */
+  const uint16_t* b;        /* bf16 [rows, 32] */
+  uint16_t* conv_state;     /* bf16 [slots, 8192, 3], rolled in place */
+  const uint16_t* conv_w;   /* bf16 [8192, 4] */
+  uint16_t* window;         /* bf16 [wslots, 8192, T + 2] */
+  const float* A_log;       /* [32] */
+  const float* dt_bias;     /* [32] */
+  const float* h0;          /* fp32 [slots, 32, 128 (V), 128 (K)] checkpoint, read only */
+  uint16_t* d_ring;         /* bf16 [rslots, 32, 16, 128] */
+  uint16_t* dlo_ring;
+  uint16_t* k_ring;         /* bf16 [rslots, 16, 16, 128] */
+  uint16_t* klo_ring;
+  float* g_ring;            /* fp32 [rslots, 32, 16] */
+  const int32_t* qsl;       /* [B + 1] */
+  const int64_t* state_idx; /* [B] checkpoint / conv-state slot, < 0: padded */
+  const int64_t* replay_idx;/* [B] ring slot */
+  const int64_t* win_idx;   /* [B] window slot */
+  const int32_t* write_pos; /* [rslots] committed entries */
+  const int32_t* cache_base;/* [rslots] physical slot of logical entry 0 */
+  const uint16_t* norm_w;   /* bf16 [128] */
+  float eps, scale;
+  uint16_t* out;            /* bf16 [rows, 4096] */
+  int use_f64;              /* 1: history state and recurrence in double (check variant) */
+  int n_threads;
+} q36o_gdn_ring_args;
+int q36o_gdn_verify_ring(const q36o_gdn_ring_args* a);
+
 /* ---- fused gated full-attention projections (fp8 128x128 block weights) ---- */
 typedef struct {
   int T;                    /* tokens */

@@ -41,6 +41,7 @@ def test_every_declared_symbol_is_exported(L):
 def test_struct_layouts_match_header(tmp_path):
     from bundles_amd import _lib
     structs = {"q36_moe_args": _lib.MoeArgs, "q36_moe_ws_layout": _lib.MoeWsLayout, "q36_gdn_args": _lib.GdnArgs,
+               "q36_gdn_ring_args": _lib.GdnRingArgs,
                "q36_attn_args": _lib.AttnArgs, "q36_oproj_args": _lib.OprojArgs, "q36_lmhead_args": _lib.LmheadArgs,
                "q36_decode_args": _lib.DecodeArgs, "q36_linear_seg": _lib.LinearSeg,
                "q36_fp8_linear_args": _lib.Fp8LinearArgs, "q36_add_norm_args": _lib.AddNormArgs}
@@ -82,6 +83,15 @@ def test_invalid_arguments_are_rejected(L):
     g.B, g.T = 2, 9
     assert L.q36_gdn_verify(C.byref(g), None) == _lib.Q36_EINVAL
     assert b"T=9" in L.q36_last_error()
+    gr = _lib.GdnRingArgs()
+    gr.B, gr.T = 2, 9
+    assert L.q36_gdn_verify_ring(C.byref(gr), None) == _lib.Q36_EINVAL
+    assert b"T=9" in L.q36_last_error()
+    gr.T = 4
+    assert L.q36_gdn_verify_ring(C.byref(gr), None) == _lib.Q36_EINVAL  # null pointers
+    assert b"null" in L.q36_last_error()
+    gr.B = 0
+    assert L.q36_gdn_verify_ring(C.byref(gr), None) == _lib.Q36_OK  # an empty batch launches nothing
     d = _lib.DecodeArgs()
     d.B, d.NT, d.HQ, d.HKV, d.D = 4, 4, 32, 4, 128
     assert L.q36_attn_decode(C.byref(d), None) == _lib.Q36_EINVAL
