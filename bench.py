@@ -496,6 +496,7 @@ def main():
         line["gdn_verify_ring"] = {
             "us_per_step": round(ring_res["us_per_step"], 2), "bytes": ring_res["bytes"],
             "achieved_gbs": round(ring_res["gbs"], 1), "frac_hbm": round(ring_res["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic("gdn_ring_kernel<5>"),
             "workload": "32 requests x (1+4) positions from a read-only fp32 checkpoint, 8 committed ring entries "
                         "each, 5 appended (the served ReplaySSM form); 4 request sets cycled in one graph"}
     print(json.dumps(line), flush=True)
