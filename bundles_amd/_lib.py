@@ -115,6 +115,10 @@ SYMBOLS = [
     ("q36_lmhead_workspace_bytes", SZ, [I32]),
     ("q36_lmhead_argmax", I32, [C.POINTER(LmheadArgs), P]),
     ("q36_quant_rows_i8", I32, [P, C.c_int64, I32, P, P, P]),
+    ("q36_q8_block_v1_bytes", SZ, [I32, I32]),
+    ("q36_quant_q8_block_v1", I32, [P, P, I32, I32, I32, I32, P, P]),
+    ("q36_import_q8_block_v1", I32, [P, I32, I32, I32, P, P, P, P, P]),
+    ("q36_quant_dense8", I32, [P, C.c_int64, I32, P, P, C.c_int64, P]),
     ("q36_quant_blocks_e4m3", I32, [P, C.c_int64, I32, P, P, P]),
     ("q36_pack_frag8", I32, [P, C.c_int64, I32, P, P]),
 ]

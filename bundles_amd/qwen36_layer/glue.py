@@ -37,6 +37,22 @@ def prepare_fp8_weight(w: torch.Tensor) -> Fp8Weight:
     return Fp8Weight(q, s, pack_frag8(q), N)
 
 
+def fp8_weight_from_blocks(q: torch.Tensor, s: torch.Tensor) -> Fp8Weight:
+    """An fp8 checkpoint's e4m3 weight [N, K] (uint8 codes or float8_e4m3fn) and its 128x128 block
+    weight_scale_inv [ceil(N/128), K/128] as they are (the same pair prepare_fp8_weight makes from bf16);
+    rows padded with zero codes to a multiple of 128, the codes reordered for the MFMA."""
+    q = q.view(torch.uint8) if q.dtype == torch.float8_e4m3fn else q
+    N, K = q.shape
+    npad = (N + 127) // 128 * 128
+    if q.dtype != torch.uint8 or K % 128 or tuple(s.shape) != (npad // 128, K // 128):
+        raise ValueError(f"fp8_weight_from_blocks: codes [N, K] and scales [N/128, K/128], got {tuple(q.shape)} "
+                         f"{q.dtype} / {tuple(s.shape)}")
+    if npad != N:
+        q = torch.cat([q, torch.zeros((npad - N, K), dtype=torch.uint8, device=q.device)], dim=0)
+    q = q.contiguous()
+    return Fp8Weight(q, s.float().contiguous(), pack_frag8(q), N)
+
+
 class LinearWorkspace:
     """The activation codes and scales of q36_fp8_linear for up to T_max tokens of width K."""
 

@@ -113,6 +113,29 @@ def prepare_experts(w13: torch.Tensor, w2: torch.Tensor, sw13: torch.Tensor, sw2
     return ExpertWeights(dtype, pack_frag8(q13), s13, pack_frag8(q2), s2, pack_frag8(qs13), ss13, pack_frag8(qs2), ss2)
 
 
+def prepare_experts_q8_block_v1(blocks: torch.Tensor, H: int, I: int, sw13: torch.Tensor,  # noqa: E741
+                                sw2: torch.Tensor) -> ExpertWeights:
+    """The routed experts from the reference's channel-mode q8-block-v1 copy (L/i8x_kernels.py:69-141),
+    read as they are (no re-quantization: the int8 codes and fp16 scales are the copy's); the shared
+    expert, which the copy does not hold, quantized per channel as prepare_experts does."""
+    from .formats import import_q8_block_v1
+    w13, s13, w2, s2 = import_q8_block_v1(blocks, H, I)
+    qs13, ss13 = quantize_rows_i8(sw13)
+    qs2, ss2 = quantize_rows_i8(sw2)
+    return ExpertWeights(Q36_MOE_INT8, w13, s13, w2, s2, pack_frag8(qs13), ss13, pack_frag8(qs2), ss2)
+
+
+def prepare_experts_fp8_blocks(q13, s13, q2, s2, qs13, ss13, qs2, ss2) -> ExpertWeights:
+    """The experts from already-quantized e4m3 128x128 blocks (an fp8 checkpoint's weight and
+    weight_scale_inv: codes uint8 / float8_e4m3fn [.., N, K], fp32 scales [.., N/128, K/128]); only the
+    codes are reordered for the MFMA."""
+    def codes(t):
+        return (t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t).contiguous()
+    return ExpertWeights(Q36_MOE_FP8, pack_frag8(codes(q13)), s13.float().contiguous(), pack_frag8(codes(q2)),
+                         s2.float().contiguous(), pack_frag8(codes(qs13)), ss13.float().contiguous(),
+                         pack_frag8(codes(qs2)), ss2.float().contiguous())
+
+
 def workspace_layout(M: int, E: int, H: int, I: int, topk: int, dtype: int) -> MoeWsLayout:  # noqa: E741
     L = MoeWsLayout()
     check(_lib.lib().q36_moe_workspace_layout(M, E, H, I, topk, dtype, C.byref(L)), "q36_moe_workspace_layout")

@@ -22,6 +22,11 @@
  *   q36_lmhead_argmax  <- lmh8_w8a8x2 / w8a8_linear + the stock greedy sampler
  *                         (L/qk_proj_decode.cu:1354; H/w8a8.py:116-120; H/node.py:136-151)
  *   q36_quant_rows_i8  <- lmhead8.quantize_rows / w8a8.quantize_act (H/lmhead8.py:111; H/w8a8.py:77)
+ *   q36_quant_q8_block_v1 <- i8x_kernels.fill_expert / quantize_channel (L/i8x_kernels.py:119-141):
+ *                         the q8-block-v1 expert copy
+ *   q36_import_q8_block_v1 <- i8x_kernels.block_parts (L/i8x_kernels.py:99-103): a channel-mode copy
+ *                         read back as the decode MoE's int8 experts
+ *   q36_quant_dense8   <- dense8.quantize (L/dense8.py:168-188): the DENSE8 copy
  *   q36_quant_blocks_e4m3 <- (no reference counterpart: the 128x128 block-scaled e4m3 weight
  *                         format the configuration asks for)
  *   q36_pack_frag8     <- (no reference counterpart: a prepare-time reordering of the 8-bit
@@ -386,6 +391,33 @@ int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream);
 int q36_quant_rows_i8(const void* w, int64_t N, int32_t K, int8_t* q, float* s, q36_stream_t stream);
 int q36_quant_blocks_e4m3(const void* w, int64_t N, int32_t K, uint8_t* q, float* s, q36_stream_t stream);
 int q36_pack_frag8(const void* q, int64_t N, int32_t K, void* packed, q36_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * The reference's prepare-time int8 weight formats (read only weights in, copies out).
+ * Scale rule (both formats): s16 = fp16(fp32(amax / 127) * (1 + 2^-10)) per row or 128-group,
+ * q = clamp(round_half_away(w / (s16 > 0 ? s16 : 1)), +-127).
+ *
+ * q8-block-v1 (L/i8x_kernels.py:12,69-110): per routed expert e one block of
+ * q36_q8_block_v1_bytes(H, I) bytes at blocks + e * bytes:
+ *   [q13 int8 [2I, H] | q2 int8 [H, I] | c13 fp16 [2I, H/128] | c2 fp16 [H, I/128]]
+ * from bf16 w13 [E, 2I, H] (gate rows 0..I-1, up rows I..2I-1) and w2 [E, H, I].
+ * channel = 1: one scale per row, written into all of the row's group slots (the reference's
+ * SCALES = 'channel'); channel = 0: one scale per 128-group.  H, I multiples of 512 up to 4096.
+ *
+ * q36_import_q8_block_v1 reads a channel-mode copy back as the decode MoE's int8 experts
+ * (q36_moe_args with dtype Q36_MOE_INT8): w13 [E, 2I, H] and w2 [E, H, I] codes in MFMA fragment
+ * order (as q36_pack_frag8 writes them), s13 [E, 2I] and s2 [E, H] fp32 (each row's first group
+ * slot widened exactly).  The shared expert is not part of the copy.
+ *
+ * DENSE8 (L/dense8.py:1-9,140-188): q int8 [N, K] row-major and fp16 scales group-major, scale of
+ * row n and group g at s[g * s_ld + n] (s_ld >= N: s may be a column block of a wider buffer).
+ * K a multiple of 512 up to 4096. */
+size_t q36_q8_block_v1_bytes(int32_t H, int32_t I);
+int q36_quant_q8_block_v1(const void* w13, const void* w2, int32_t E, int32_t H, int32_t I, int32_t channel,
+                          void* blocks, q36_stream_t stream);
+int q36_import_q8_block_v1(const void* blocks, int32_t E, int32_t H, int32_t I, void* w13, float* s13, void* w2,
+                           float* s2, q36_stream_t stream);
+int q36_quant_dense8(const void* w, int64_t N, int32_t K, void* q, void* s, int64_t s_ld, q36_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -90,6 +90,14 @@ def _declare(L):
     L.q36o_e4m3_to_f32.argtypes = [C.c_uint8]
     L.q36o_expf.restype = C.c_float
     L.q36o_expf.argtypes = [C.c_float]
+    L.q36o_f32_to_f16.restype = C.c_uint16
+    L.q36o_f32_to_f16.argtypes = [C.c_float]
+    L.q36o_f16_to_f32.restype = C.c_float
+    L.q36o_f16_to_f32.argtypes = [C.c_uint16]
+    L.q36o_q8_block_bytes.restype = C.c_size_t
+    L.q36o_q8_block_bytes.argtypes = [I32, I32]
+    L.q36o_quant_q8_block_v1.argtypes = [P, P, I32, I32, I32, I32, P]
+    L.q36o_quant_dense8.argtypes = [P, I32, I32, P, P, I32]
     L.q36o_f16_round.restype = C.c_float
     L.q36o_f16_round.argtypes = [C.c_float]
     L.q36o_dot_canon.restype = C.c_float
@@ -232,6 +240,48 @@ def moe(mode, x, wr, w13, s13, w2, s2, sw13, ss13, sw2, ss2, gate_w, k, bias=Non
     if rc:
         raise ValueError("q36o_moe rejected the shapes")
     return res
+
+
+# ---------------------------------------------------------------- reference weight formats
+def f32_to_f16_bits(x) -> np.ndarray:
+    """float32 -> IEEE binary16 bit patterns (uint16) through the oracle's codec."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    f = lib().q36o_f32_to_f16
+    return np.array([f(float(v)) for v in x], dtype=np.uint16)
+
+
+def q8_block_bytes(H: int, I: int) -> int:  # noqa: E741
+    return int(lib().q36o_q8_block_bytes(H, I))
+
+
+def quant_q8_block_v1(w13, w2, channel=True):
+    """q8-block-v1 expert blocks uint8 [E, block_bytes] from float32 w13 [E, 2I, H], w2 [E, H, I]."""
+    w13 = np.ascontiguousarray(w13, np.float32)
+    w2 = np.ascontiguousarray(w2, np.float32)
+    E, I2, H = w13.shape
+    out = np.zeros((E, q8_block_bytes(H, I2 // 2)), np.uint8)
+    lib().q36o_quant_q8_block_v1(_p(w13), _p(w2), E, H, I2 // 2, int(channel), _p(out))
+    return out
+
+
+def q8_block_parts(block, H: int, I: int):  # noqa: E741
+    """(q13 int8 [2I, H], q2 int8 [H, I], c13 fp16 bits [2I, H/128], c2 fp16 bits [H, I/128]) of one block."""
+    o2, oc13 = 2 * I * H, 3 * I * H
+    oc2 = oc13 + 2 * I * (H // 128) * 2
+    eb = q8_block_bytes(H, I)
+    return (block[:o2].view(np.int8).reshape(2 * I, H), block[o2:oc13].view(np.int8).reshape(H, I),
+            block[oc13:oc2].view(np.uint16).reshape(2 * I, H // 128), block[oc2:eb].view(np.uint16).reshape(H, I // 128))
+
+
+def quant_dense8(w, s_stride=None):
+    """DENSE8 copy of float32 w [N, K]: (q int8 [N, K], s fp16 bits [K/128, s_stride])."""
+    w = np.ascontiguousarray(w, np.float32)
+    N, K = w.shape
+    s_stride = N if s_stride is None else s_stride
+    q = np.zeros((N, K), np.int8)
+    s = np.zeros((K // 128, s_stride), np.uint16)
+    lib().q36o_quant_dense8(_p(w), N, K, _p(q), _p(s), s_stride)
+    return q, s
 
 
 # ---------------------------------------------------------------- GDN

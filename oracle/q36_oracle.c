@@ -166,6 +166,80 @@ void q36o_quant_blocks_e4m3(const float* w, int N, int K, uint8_t* q, float* s) 
 }
 
 /* ------------------------------------------------------------------------------------ */
+/* prepare-time weight formats of the reference                                         */
+/* ------------------------------------------------------------------------------------ */
+
+uint16_t q36o_f32_to_f16(float f) {
+  uint32_t u = f2u(f), sign = (u >> 16) & 0x8000u, a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);            /* NaN */
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);           /* >= 65520: rounds to inf */
+  if (a < 0x38800000u) {                                             /* below 2^-14: subnormal grid 2^-24 */
+    double q = (double)u2f(a) * 16777216.0, fl = floor(q), r = q - fl;
+    if (r > 0.5 || (r == 0.5 && fmod(fl, 2.0) != 0.0)) fl += 1.0;
+    return (uint16_t)(sign | (uint32_t)fl);                          /* 1024 is the smallest normal */
+  }
+  uint32_t keep = a >> 13, rest = a & 0x1fffu;
+  if (rest > 0x1000u || (rest == 0x1000u && (keep & 1u))) keep++;
+  return (uint16_t)(sign | (keep - ((127u - 15u) << 10)));
+}
+float q36o_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
+  if (e == 0) return u2f(sign) + (sign ? -1.f : 1.f) * ldexpf((float)m, -24);
+  if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+  return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* One row (or one 128-group) of n weights: the scale rule of L/i8x_kernels.py:119-131 and
+ * L/dense8.py:153-166 (one fp16 ulp of headroom above amax / 127), codes rounded half away. */
+static uint16_t quant_f16_scaled(const float* w, int n, int8_t* q) {
+  float amax = 0.f;
+  for (int i = 0; i < n; ++i) amax = fmaxf(amax, fabsf(w[i]));
+  const uint16_t s16 = q36o_f32_to_f16((amax / 127.f) * 1.0009765625f);
+  const float sc = q36o_f16_to_f32(s16), safe = sc > 0.f ? sc : 1.f;
+  for (int i = 0; i < n; ++i) {
+    float v = w[i] / safe;
+    float r = v >= 0.f ? floorf(v + 0.5f) : -floorf(0.5f - v);
+    q[i] = (int8_t)fminf(fmaxf(r, -127.f), 127.f);
+  }
+  return s16;
+}
+
+size_t q36o_q8_block_bytes(int H, int I) {
+  return (size_t)2 * I * H + (size_t)H * I + (size_t)2 * I * (H / 128) * 2 + (size_t)H * (I / 128) * 2;
+}
+
+void q36o_quant_q8_block_v1(const float* w13, const float* w2, int E, int H, int I, int channel, uint8_t* blocks) {
+  const size_t eb = q36o_q8_block_bytes(H, I), o2 = (size_t)2 * I * H, oc13 = o2 + (size_t)H * I,
+               oc2 = oc13 + (size_t)2 * I * (H / 128) * 2;
+#pragma omp parallel for schedule(static)
+  for (int e = 0; e < E; ++e) {
+    uint8_t* b = blocks + (size_t)e * eb;
+    for (int part = 0; part < 2; ++part) {
+      const int rows = part ? H : 2 * I, K = part ? I : H;
+      const float* w = part ? w2 + (size_t)e * H * I : w13 + (size_t)e * 2 * I * H;
+      int8_t* q = (int8_t*)(b + (part ? o2 : 0));
+      uint16_t* c = (uint16_t*)(b + (part ? oc2 : oc13));
+      for (int r = 0; r < rows; ++r) {
+        if (channel) {
+          const uint16_t s16 = quant_f16_scaled(w + (size_t)r * K, K, q + (size_t)r * K);
+          for (int g = 0; g < K / 128; ++g) c[(size_t)r * (K / 128) + g] = s16;
+        } else {
+          for (int g = 0; g < K / 128; ++g)
+            c[(size_t)r * (K / 128) + g] = quant_f16_scaled(w + (size_t)r * K + g * 128, 128, q + (size_t)r * K + g * 128);
+        }
+      }
+    }
+  }
+}
+
+void q36o_quant_dense8(const float* w, int N, int K, int8_t* q, uint16_t* s, int s_stride) {
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; ++n)
+    for (int g = 0; g < K / 128; ++g)
+      s[(size_t)g * s_stride + n] = quant_f16_scaled(w + (size_t)n * K + g * 128, 128, q + (size_t)n * K + g * 128);
+}
+
+/* ------------------------------------------------------------------------------------ */
 /* routing                                                                              */
 /* ------------------------------------------------------------------------------------ */
 

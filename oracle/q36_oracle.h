@@ -34,6 +34,20 @@ void q36o_quant_rows_i8(const float* x, int rows, int K, int8_t* q, float* s);
 void q36o_quant_groups_e4m3(const float* x, int rows, int K, int group, uint8_t* q, float* s);
 void q36o_quant_blocks_e4m3(const float* w, int N, int K, uint8_t* q, float* s);
 
+/* ---- prepare-time weight formats of the reference ----
+ * q8-block-v1 (L/i8x_kernels.py:12,69-110,119-141): per expert one block of
+ *   [q13 int8 (2I x H) | q2 int8 (H x I) | c13 fp16 (2I x H/128) | c2 fp16 (H x I/128)]
+ * q36o_q8_block_bytes(H, I) bytes apart.  A row's scale s16 = fp16(fp32(amax / 127) * (1 + 2^-10)),
+ * q = clamp(round_half_away(w / (s16 > 0 ? s16 : 1)), +-127); channel = 1: one scale per row written
+ * into every 128-group slot of the row; channel = 0: one scale per 128-group (the DENSE8 rule).
+ * DENSE8 (L/dense8.py:140-188): q int8 [N, K] and fp16 scales group-major s [K/128][s_stride]
+ * (element (g, n) at s[g * s_stride + n]), one per row and 128-group. */
+uint16_t q36o_f32_to_f16(float f);           /* IEEE round-to-nearest-even, overflow to inf, NaN kept */
+float q36o_f16_to_f32(uint16_t h);
+size_t q36o_q8_block_bytes(int H, int I);
+void q36o_quant_q8_block_v1(const float* w13, const float* w2, int E, int H, int I, int channel, uint8_t* blocks);
+void q36o_quant_dense8(const float* w, int N, int K, int8_t* q, uint16_t* s, int s_stride);
+
 /* ---- routing: router GEMV + softmax + top-k + renorm + expert lists ---- */
 int q36o_route(const uint16_t* x, const uint16_t* wr, const float* bias, const int32_t* pos, int M, int E,
                int H, int k, float* logits, int32_t* ids, float* wts, int32_t* counts, int32_t* offsets,
@@ -91,7 +105,7 @@ typedef struct {
 int q36o_gdn_verify(const q36o_gdn_args* a);
 
 /* ---- GDN speculative verify over the ReplaySSM ring (read-only checkpoint + 16-entry ring) ----
- * L/qk_gdn_verify.cu:1-20 (design), :586-593 (ring keys), :616-634 (gates, g ring), :636-651
+ * L/qk_gdn_verify.cu:1-20 (design), :583-605 (ring keys), :616-632 (gates, g ring), :634-648
  * (history decay), :684-762 (window recurrence), :770-781 (d ring); host checks :850-919.
  * Request r owns rows qsl[r] .. qsl[r] + T - 1; state_idx < 0 marks a padded request (zero output,
  * nothing else written).  The history state is td * h0 + sum_c decay_c dhat_c khat_c^T over the
