@@ -29,9 +29,6 @@ namespace {
 constexpr int RK = 128, RV = 128, RHK = 16, RHV = 32, RQKV = 8192, RZ = RHV * RV, RL = 16, RTMAX = 8;
 constexpr int KW_STRIDE = 132;  // padded fp32 key rows: the 16 rows a tile step reads hit distinct banks
 constexpr int HX_STRIDE = 20;  // 16 dots + pad: 16-byte aligned rows, read as four v4f
-// checkpoint steps (of 8 per tile) requested before the conv: measured 34.3 / 32.4 / 31.6 us per
-// 32 x 5 step for 0 / 1 / 3
-constexpr int HEARLY = 3;
 
 struct GdnRingDev {
   int B, T, rows, slots, rslots, wslots;
@@ -143,15 +140,31 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   // z: position tid >> 6 (rows past T read row T - 1), columns 4 (tid & 63) .. + 3 of the unit's 256
   const v2i zraw = *reinterpret_cast<const v2i*>(d.z + (bos + min(tid >> 6, T - 1)) * RZ + hk * 2 * RV + (tid & 63) * 4);
   const uint32_t nwraw = d.norm_w[tid & (RV - 1)];
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // the checkpoint: wave w holds head w >> 2, rows 32 (w & 3) .. + 31 as two 16-row tiles; lane l
+  // reads row l & 15 of a tile, columns 16 s + 4 (l >> 4) .. + 3 at step s.  Its 8 steps are
+  // requested two at a time through the phases below (about 64 KB in flight a CU: enough to keep
+  // HBM busy, little enough that a phase's own stores, issued before its next request, do not queue
+  // behind a deep stream in the CU's in-order memory pipe)
+  const int hh = wave >> 2, rb = (wave & 3) * 32;
+  const float* hp = d.h0 + ((slot * RHV + 2 * hk + hh) * RV + rb + (lane & 15)) * RK + 4 * (lane >> 4);
+  v4f hr[2][8];
+  auto request = [&](int s0) {
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int s = s0; s < s0 + 2; ++s)
+        hr[i][s] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(hp + i * 16 * RK + 16 * s));
+    asm volatile("" ::: "memory");
+  };
+  request(0);
+  asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // the small operands (the 4 row requests may fly)
   if ((tid >> 6) < T) *reinterpret_cast<v2i*>(&zs[tid >> 6][(tid & 63) * 4]) = zraw;
   if (tid < RV) nws[tid] = bf2f(nwraw);
   const int nv = min(max(__builtin_amdgcn_readfirstlane(cur_wp), 0), RL);
   const int cb = __builtin_amdgcn_readfirstlane(cur_cb);
-  // round two: the committed ring entries (logical entry c of the key / d rows; entries past the
-  // history read entry 0's slot and are zeroed later) and gates, then the checkpoint: wave w holds
-  // head w >> 2, rows 32 (w & 3) .. + 31 as two 16-row tiles; lane l reads row l & 15 of a tile,
-  // columns 16 s + 4 (l >> 4) .. + 3 at step s
+  // the committed ring entries (logical entry c of the key / d rows; entries past the history read
+  // entry 0's slot and are zeroed later) and gates
   const int kc = tid >> 5, kcol = (tid & 31) * 4;  // keys: 16 entries x 32 x 4 columns
   const v2i kraw = *reinterpret_cast<const v2i*>(d.k_ring + rp * d.k_slot +
                                                  ((int64_t)hk * RL + ((cb + (kc < nv ? kc : 0)) & 15)) * RK + kcol);
@@ -159,16 +172,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   const v4i draw = *reinterpret_cast<const v4i*>(d.d_ring + rp * d.d_slot +
                                                  ((int64_t)(2 * hk + dhd) * RL + ((cb + (dc < nv ? dc : 0)) & 15)) * RV + dv);
   const float graw = d.g_ring[rp * d.g_slot + (2 * hk + ((tid >> 4) & 1)) * RL + ((cb + tid) & 15)];
-  const int hh = wave >> 2, rb = (wave & 3) * 32;
-  const float* hp = d.h0 + ((slot * RHV + 2 * hk + hh) * RV + rb + (lane & 15)) * RK + 4 * (lane >> 4);
-  v4f hr[2][8];
-  // the first HEARLY steps of both tiles now (64 KB a CU: within what a CU keeps in flight, so the
-  // conv below does not stall behind their issue), the rest once the window's vectors are ready
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int s = 0; s < HEARLY; ++s)
-      hr[i][s] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(hp + i * 16 * RK + 16 * s));
 
   // ---- conv + SiLU (bf16 tap products, oldest first), the rolled state and the window record
   {
@@ -213,6 +216,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     gbeta[h][t] = sigmoid_q(bv);
     geg[h][t] = expf_q(g);
   }
+  request(2);
   __syncthreads();
 
   // ---- the committed entries into LDS: keys into key rows 0-15 (logical order, zero past the
@@ -254,6 +258,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
       }
     }
   }
+  request(4);
   __syncthreads();
 
   // ---- dots that need no checkpoint row, while the early rows stream: ring keys (wave 0) and window
@@ -284,6 +289,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     dec[h][c] = c < nv ? expf_q(tot - pre) : 0.f;
     if (c == 0) tdec[h] = expf_q(tot);
   }
+  request(6);
   __syncthreads();
   // The history's part of each row's dots: R_x = sum_c decay_c dhat_c (khat_c . x).  Lanes 2j and
   // 2j + 1 share row tid >> 1: the even lane keeps the q-vectors (x < 8), the odd lane the k-vectors
@@ -301,14 +307,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     }
   }
 
-  // ---- the remaining checkpoint rows, all requested before the first dot (left alone, the
-  // compiler interleaves them with the MFMAs and keeps only a few in flight); then the rows' dots
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int s = HEARLY; s < 8; ++s)
-      hr[i][s] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(hp + i * 16 * RK + 16 * s));
-  asm volatile("" ::: "memory");
+  // ---- the checkpoint rows' dots, step by step as they arrive
   {
     v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
