@@ -285,30 +285,49 @@ def bench_hybrid(args, torch, dev):
 
     B, T, ctx = 64, 4, 4096
     w = hybrid.make_weights(dev, seed=0)
-    st = hybrid.make_state(B, T, ctx, dev, seed=1)
-    ws = hybrid.HybridWorkspace(B, T, w.E, dev)
+    res = {}
+    for form in ("ring", "snapshot"):
+        res[form] = _hybrid_form(args, torch, dev, hybrid, synth, w, B, T, ctx, form)
+        torch.cuda.empty_cache()
+    out = dict(res["ring"])
+    out["us_per_step_snapshot"] = res["snapshot"]["us_per_step"]
+    return out
+
+
+def _hybrid_form(args, torch, dev, hybrid, synth, w, B, T, ctx, form):
+    st = hybrid.make_state(B, T, ctx, dev, seed=1, gdn_form=form)
+    ws = hybrid.HybridWorkspace(B, T, w.E, dev, snapshots=form == "snapshot")
     x = synth.randn((B * T, 2048), synth.gen(dev, 2), dev)
-    ids_eager = hybrid.forward(x, w, st, ws).clone()
+    # the ring form rolls the GDN conv states in place: every step starts from the same committed
+    # states (the copies run inside the timed graph, as the engine's rollback to the accepted window)
+    saved = [c.clone() for c in st.conv_state] if form == "ring" else []
+
+    def step():
+        for c, c0 in zip(st.conv_state, saved):
+            c.copy_(c0)
+        return hybrid.forward(x, w, st, ws)
+
+    ids_eager = step().clone()
     for _ in range(max(1, args.warmup)):
-        hybrid.forward(x, w, st, ws)
+        step()
     torch.cuda.synchronize()
-    ms_eager = events_time(lambda: hybrid.forward(x, w, st, ws), max(3, args.steps // 5), torch)
+    ms_eager = events_time(step, max(3, args.steps // 5), torch)
     graph = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        hybrid.forward(x, w, st, ws)
+        step()
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=s):
-            hybrid.forward(x, w, st, ws)
+            step()
     torch.cuda.synchronize()
     for _ in range(3):
         graph.replay()
         torch.cuda.synchronize()
         if not torch.equal(ws.bufs["ids"], ids_eager):
-            raise RuntimeError("hybrid node: a graph replay's ids differ from the eager step's")
+            raise RuntimeError(f"hybrid node ({form}): a graph replay's ids differ from the eager step's")
     ms = events_time(graph.replay, args.steps, torch)
-    del w, st, ws
+    del st, ws
     return dict(us_per_step=ms * 1e3, us_eager=ms_eager * 1e3, rows=B * T, tokens_per_s=B * T / (ms * 1e-3),
                 sequences=B, verify_tokens=T, context=ctx)
 
@@ -483,10 +502,13 @@ def main():
     if hyb_res:
         line["hybrid_node"] = {
             "us_per_step": round(hyb_res["us_per_step"], 1), "us_eager": round(hyb_res["us_eager"], 1),
+            "us_per_step_snapshot": round(hyb_res["us_per_step_snapshot"], 1),
             "tokens_per_s": round(hyb_res["tokens_per_s"], 1), "rows": hyb_res["rows"],
             "workload": "config 5: 3 GDN + 1 gated attention layer, each + fp8 MoE (512 experts, top-10, Zipf "
                         "router), add-norms, final norm, int8 lm_head [151936, 2048] + argmax; 64 seqs x 4 verify "
-                        "tokens, 4096 cached keys; one captured graph per step"}
+                        "tokens, 4096 cached keys; one captured graph per step; us_per_step with the GDN verify "
+                        "in the served ring form (8 committed entries, conv states restored each step inside the "
+                        "graph), us_per_step_snapshot with per-position snapshots"}
     if gdn_res:
         line["gdn_verify"] = {
             "us_per_step": round(gdn_res["us_per_step"], 2), "bytes": gdn_res["bytes"],

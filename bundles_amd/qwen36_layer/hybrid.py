@@ -84,6 +84,11 @@ class HybridState:
     out_loc: torch.Tensor     # int64 [B*T]: the new tokens' cache slots
     positions: torch.Tensor   # int32 [B*T]
     cos_sin: torch.Tensor     # fp32 [max_pos, 64]
+    # "snapshot": the GDN verify writes every position's state (q36_gdn_verify, config 3's form);
+    # "ring": the served ReplaySSM form (q36_gdn_verify_ring): S is the read-only checkpoint, conv_state
+    # rolls in place, and each GDN layer has the ring pools in `ring` (request r on slot r)
+    gdn_form: str = "snapshot"
+    ring: list | None = None
 
 
 def make_weights(device, seed: int = 0, E: int = synth.E, V: int = 151936, zipf: float = 1.1) -> HybridWeights:
@@ -111,10 +116,32 @@ def make_weights(device, seed: int = 0, E: int = synth.E, V: int = 151936, zipf:
     return HybridWeights(layers, synth.randn((HIDDEN,), g, device, 0.1), lm_q, lm_s, E)
 
 
-def make_state(B: int, T: int, ctx: int, device, seed: int = 0, extra_slots: int = 64) -> HybridState:
+def _ring_pools(B: int, T: int, device, g, wp: int) -> dict:
+    """One GDN layer's ReplaySSM pools for B requests on slots 0..B-1: a committed history of wp entries
+    per request at a random cache base (d ~ N(0, 0.3), unit keys, gates of a typical magnitude, each
+    bf16 value with its low part), the draft-window records, the cursors and the request indices."""
+    d32 = torch.randn((B, GDN_HV, 16, 128), generator=g, device=device) * 0.3
+    k32 = torch.randn((B, GDN_HV // 2, 16, 128), generator=g, device=device)
+    k32 = k32 / k32.norm(dim=-1, keepdim=True)
+    dh, kh = d32.to(torch.bfloat16), k32.to(torch.bfloat16)
+    return dict(
+        window=torch.zeros((B, GDN_QKV, T + 2), dtype=torch.bfloat16, device=device),
+        d=dh, dlo=(d32 - dh.float()).to(torch.bfloat16), k=kh, klo=(k32 - kh.float()).to(torch.bfloat16),
+        g=(-0.05 * torch.rand((B, GDN_HV, 16), generator=g, device=device)).contiguous(),
+        wp=torch.full((B,), wp, dtype=torch.int32, device=device),
+        cb=torch.randint(0, 16, (B,), generator=g, device=device, dtype=torch.int32),
+        qsl=torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=device),
+        idx=torch.arange(B, dtype=torch.int64, device=device))
+
+
+def make_state(B: int, T: int, ctx: int, device, seed: int = 0, extra_slots: int = 64, gdn_form: str = "snapshot",
+               ring_wp: int = 8) -> HybridState:
     """The node's state for one verify step: GDN conv / recurrent states, and an e4m3 KV pool holding
     ctx cached keys per request (values N(0,1) scaled per KV head) at random one-token slots, with the
-    T new tokens' slots already in the page table (as the engine assigns them)."""
+    T new tokens' slots already in the page table (as the engine assigns them).  gdn_form "ring" adds
+    each GDN layer's ReplaySSM pools with ring_wp committed entries per request."""
+    if gdn_form not in ("snapshot", "ring"):
+        raise ValueError(f"gdn_form must be 'snapshot' or 'ring', not {gdn_form!r}")
     g = synth.gen(device, seed)
     n_gdn = KINDS.count("gdn")
     conv = [synth.randn((B, GDN_QKV, 3), g, device) for _ in range(n_gdn)]
@@ -128,18 +155,21 @@ def make_state(B: int, T: int, ctx: int, device, seed: int = 0, extra_slots: int
     seqlens = torch.full((B,), ctx + T, dtype=torch.int32, device=device)
     out_loc = pt[:, ctx:].reshape(-1).to(torch.int64).contiguous()
     positions = (ctx + torch.arange(T, device=device, dtype=torch.int32)).repeat(B).contiguous()
+    ring = [_ring_pools(B, T, device, g, ring_wp) for _ in range(n_gdn)] if gdn_form == "ring" else None
     return HybridState(B, T, conv, S, kc, vc, pt, seqlens, out_loc, positions,
-                       synth.rope_cos_sin(ctx + T + 1, device=device))
+                       synth.rope_cos_sin(ctx + T + 1, device=device), gdn_form, ring)
 
 
 @dataclass
 class HybridWorkspace:
-    """Every intermediate of one step of M = B*T rows (allocated once, reused by every step)."""
+    """Every intermediate of one step of M = B*T rows (allocated once, reused by every step).  With
+    snapshots=False (the ring form) the per-position GDN state buffers are not allocated."""
     B: int
     T: int
     E: int
     device: object
     bufs: dict = field(default_factory=dict)
+    snapshots: bool = True
 
     def __post_init__(self):
         M, dev, bf = self.B * self.T, self.device, torch.bfloat16
@@ -150,7 +180,8 @@ class HybridWorkspace:
         self.bufs = dict(
             residual=e(M, HIDDEN), h=e(M, HIDDEN), o=e(M, HIDDEN), m=e(M, HIDDEN),
             mixed=e(M, GDN_QKV), z=e(M, GDN_Z), b=e(M, GDN_HV), a=e(M, GDN_HV), gout=e(M, GDN_Z),
-            snaps=[e(self.B, self.T, GDN_HV, 128, 128, dtype=torch.float32) for _ in range(n_gdn)],
+            snaps=[e(self.B, self.T, GDN_HV, 128, 128, dtype=torch.float32) for _ in range(n_gdn)] if self.snapshots
+            else None,
             conv_out=[e(self.B, GDN_QKV, 3) for _ in range(n_gdn)],
             attn=dict(q=e(M, 16, 256), gate=e(M, 16, 256), k=e(M, 2, 256), v=e(M, 2, 256),
                       k8=e(M, 2, 256, dtype=torch.uint8), v8=e(M, 2, 256, dtype=torch.uint8)),
@@ -190,9 +221,19 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
                                                            (GDN_QKV + GDN_Z, b["b"]),
                                                            (GDN_QKV + GDN_Z + GDN_HV, b["a"])], stream=stream)
             keep(f"L{i}.mixed", b["mixed"]), keep(f"L{i}.z", b["z"]), keep(f"L{i}.a", b["a"]), keep(f"L{i}.b", b["b"])
-            gdn_fused.gdn_verify_fused(b["mixed"], b["z"], b["a"], b["b"], st.conv_state[gi], g.conv_w, g.A_log,
-                                       g.dt_bias, st.S[gi], g.norm_w, w.eps, T=st.T, out=b["gout"],
-                                       snaps=b["snaps"][gi], conv_state_out=b["conv_out"][gi], stream=stream)
+            if st.gdn_form == "ring":
+                R = st.ring[gi]
+                keep(f"L{i}.conv_state_in", st.conv_state[gi])
+                for k in ("d", "dlo", "k", "klo", "g"):
+                    keep(f"L{i}.ring_{k}_in", R[k])
+                gdn_fused.gdn_verify_ring(b["mixed"], b["z"], b["a"], b["b"], st.conv_state[gi], g.conv_w, R["window"],
+                                          g.A_log, g.dt_bias, st.S[gi], R["d"], R["dlo"], R["k"], R["klo"], R["g"],
+                                          R["qsl"], R["idx"], R["idx"], R["idx"], R["wp"], R["cb"], g.norm_w, w.eps,
+                                          128 ** -0.5, T=st.T, out=b["gout"], stream=stream)
+            else:
+                gdn_fused.gdn_verify_fused(b["mixed"], b["z"], b["a"], b["b"], st.conv_state[gi], g.conv_w, g.A_log,
+                                           g.dt_bias, st.S[gi], g.norm_w, w.eps, T=st.T, out=b["gout"],
+                                           snaps=b["snaps"][gi], conv_state_out=b["conv_out"][gi], stream=stream)
             keep(f"L{i}.gout", b["gout"])
             fp8_linear(b["gout"], g.out_proj, ws.lin4096, segments=[(0, b["o"])], stream=stream)
             gi += 1
