@@ -29,7 +29,7 @@ namespace q36 {
 namespace {
 
 constexpr int kLH = 2048;       // hidden (K)
-constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBM = 256, kBN = 256, kBK = 64, kNK = kLH / kBK;  // 32 K steps
 
 struct LmhDev {
   int R, V;
@@ -99,9 +99,10 @@ __global__ __launch_bounds__(256) void lmh_prep_kernel(LmhDev d) {
 }
 
 // LDS position of 16-byte chunk kc (0..3) of tile row c in one K step: rows are 64 bytes, unpadded,
-// with the chunk order xor-swizzled by (c >> 1) & 3, so that the eight lanes of a fragment read
-// (chunk kc of eight consecutive rows) touch eight distinct 16-byte bank windows.
-__device__ __forceinline__ int bswz(int c, int kc) { return c * kBK + ((kc ^ ((c >> 1) & 3)) << 4); }
+// with the chunk order xor-swizzled by ((c >> 1) & 3) ^ ((c >> 3) & 1).  A fragment read takes chunk
+// kc of consecutive rows; LDS serves a 16-byte read 16 lanes at a time over 64 banks, and with this
+// swizzle any 16 consecutive rows (and any 8) land in distinct 16-byte bank windows.
+__device__ __forceinline__ int bswz(int c, int kc) { return c * kBK + ((kc ^ ((c >> 1) & 3) ^ ((c >> 3) & 1)) << 4); }
 
 template <int N>
 using ic = std::integral_constant<int, N>;
@@ -114,13 +115,40 @@ __device__ __forceinline__ float round_bf16(float x) {
   return __builtin_bit_cast(float, __builtin_convertvector((v2f){0.f, x}, v2bf));
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lmh_gemm_kernel(LmhDev d) {
-  // Four LDS stages per operand, one object each: the compiler tracks the buffer-to-LDS loads of
-  // each object separately and waits only for those of the stage being read.
+// s_waitcnt with only the vector-memory count constrained (gfx9 encoding: vmcnt bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Persistent GEMM + argmax: one 256-thread workgroup per CU walks its XCD's tiles.  The XCDs form
+// ngrp row groups (2 when the row tiles split evenly, else 1): XCD x serves the rpg = nrt / ngrp
+// row tiles of group x % ngrp and the vocab tiles v = x / ngrp (mod 8 / ngrp).  Its workgroups take
+// tiles j = loc, loc + nloc, ... (loc = blockIdx / 8, nloc = gridDim / 8), tile j being row tile
+// (x % ngrp) * rpg + j % rpg of vocab tile (j / rpg) * (8 / ngrp) + x / ngrp: the row tiles of one
+// vocab tile run side by side on one XCD (its weight tile comes from HBM once per XCD), and an
+// XCD's activations (rpg row tiles, 2 MB at 2048 rows) stay resident in its L2 while the weights
+// stream through.
+//
+// Per tile, 32 K steps of 64 bytes through a 4-stage LDS ring filled by buffer loads straight into
+// LDS (no register staging).  Each wave owns a 128 x 128 block (32x32x32 int8 MFMAs, weights as
+// operand A, int32 accumulators in AGPRs) and keeps two register sets of fragments: while the 32
+// MFMAs of step ks run on one set, the 16 LDS reads of step ks + 1 fill the other and the loads of
+// step ks + 4 go out, so the matrix pipe never waits on LDS.  One barrier per step: before it, each
+// wave waits for its own loads of step ks + 1 and its LDS reads of step ks (the stage the loads of
+// step ks + 4 then overwrite).  The last step of a tile first issues the next tile's scales and its
+// first four K steps, so the epilogue runs while they land.
+// row groups of XCDs (see lmh_gemm_body): two when there are at least 4 row tiles, evenly split
+__host__ __device__ __forceinline__ int lmh_groups(int nrt) { return nrt >= 4 && nrt % 2 == 0 ? 2 : 1; }
+
+template <bool STORE>
+__device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
+  // one object per LDS stage: the compiler tracks the buffer-to-LDS loads of each object apart
   __shared__ __align__(1024) int8_t a_s0[kBM * kBK], a_s1[kBM * kBK], a_s2[kBM * kBK], a_s3[kBM * kBK];
   __shared__ __align__(1024) int8_t b_s0[kBN * kBK], b_s1[kBN * kBK], b_s2[kBN * kBK], b_s3[kBN * kBK];
+  __shared__ __align__(16) float sc_l[2][2][kBN];  // [tile parity][weight scales | row scales]
   __shared__ uint32_t rkey[2][kBM];
-  __shared__ __align__(16) float ws_l[kBN];  // the tile's weight scales
   auto a_st = [&](auto st) -> int8_t* {
     if constexpr (decltype(st)::value == 0) return a_s0;
     else if constexpr (decltype(st)::value == 1) return a_s1;
@@ -134,155 +162,222 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     else return b_s3;
   };
   const int nvt = (d.V + kBN - 1) / kBN, nrt = (d.R + kBM - 1) / kBM;
-  // XCD-aware mapping (block b -> XCD b % 8): consecutive blocks of an XCD sweep the row tiles of
-  // one vocab tile, which is then fetched from HBM once per XCD and served from its L2
-  const int b = blockIdx.x, xcd = b & 7, j = b >> 3;
-  const int rt = j % nrt, vt = (j / nrt) * 8 + xcd;
-  if (vt >= nvt) return;
+  const int xcd = blockIdx.x & 7, loc = blockIdx.x >> 3, nloc = gridDim.x >> 3;
+  const int ngrp = lmh_groups(nrt), rpg = nrt / ngrp, vstep = 8 / ngrp;
+  const int rbase = (xcd % ngrp) * rpg, vres = xcd / ngrp;
+  auto vt_of = [&](int jj) { return (jj / rpg) * vstep + vres; };
+  int j = loc;
+  if (vt_of(j) >= nvt) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves of 128 x 128
-  const int r0 = rt * kBM, v0 = vt * kBN;
-  // global -> LDS by buffer loads with the LDS bit (no registers; rows past R or V read as zero).
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   // Load i of wave w fills 1 KB chunk q = 4 w + i of a stage (tile rows 16 q .. 16 q + 15); lane l
   // writes bytes 16 l .. 16 l + 15 of the chunk, which bswz assigns to row 16 q + l / 4, logical
-  // 16-byte chunk (l % 4) ^ ((l / 8) % 4).
-  const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(d.xq + (size_t)r0 * kLH), (short)0, min(d.R - r0, kBM) * kLH, 0x00020000);
-  const __amdgpu_buffer_rsrc_t brsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(d.wq + (size_t)v0 * kLH), (short)0, min(d.V - v0, kBN) * kLH, 0x00020000);
-  if (tid < kBN / 4)
-    *reinterpret_cast<float4*>(&ws_l[4 * tid]) =
-        v0 + 4 * tid < d.V ? *reinterpret_cast<const float4*>(d.ws + v0 + 4 * tid) : make_float4(0.f, 0.f, 0.f, 0.f);
-  const int voff = (lane >> 2) * kLH + (((lane & 3) ^ ((lane >> 3) & 3)) << 4);
-  const int wq4 = __builtin_amdgcn_readfirstlane(wave) * 4;
-  auto issue_to = [&](int ks, int8_t* as, int8_t* bs) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = wq4 + i;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, as + q * 1024, 16, voff, q * 16 * kLH + ks * kBK, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(brsrc, bs + q * 1024, 16, voff, q * 16 * kLH + ks * kBK, 0, 2);
-    }
+  // 16-byte chunk (l % 4) ^ ((l / 8) % 4) ^ (l / 32).  Rows past R or V read as zero (buffer bounds).
+  const int voff = (lane >> 2) * kLH + (((lane & 3) ^ ((lane >> 3) & 3) ^ (lane >> 5)) << 4);
+  struct Tile {
+    int r0, v0;
+    __amdgpu_buffer_rsrc_t a, b;
   };
-  auto issue = [&](int ks, auto st) { issue_to(ks, a_st(st), b_st(st)); };
-  constexpr int NK = kLH / kBK;
-  static_assert(NK % 4 == 0 && NK >= 8, "K steps");
-  // 32x32x32 int8 MFMA (twice the rate of 16x16x64 on gfx950): the weight rows are operand A, the
-  // token rows operand B.  Lane l reads tile row 32 t + l % 32, K bytes 16 (l / 32) of each 32-byte
-  // half step (LDS chunk 2 h + l / 32); the result gives lane l token l % 32 and vocab rows
+  auto tile = [&](int jj) {
+    Tile t;
+    t.r0 = (rbase + jj % rpg) * kBM;
+    t.v0 = vt_of(jj) * kBN;
+    t.a = __builtin_amdgcn_make_buffer_rsrc((void*)(d.xq + (size_t)t.r0 * kLH), (short)0,
+                                            min(d.R - t.r0, kBM) * kLH, 0x00020000);
+    t.b = __builtin_amdgcn_make_buffer_rsrc((void*)(d.wq + (size_t)t.v0 * kLH), (short)0,
+                                            min(d.V - t.v0, kBN) * kLH, 0x00020000);
+    return t;
+  };
+  // The row offset rides in the VGPR offset, the K offset in the SGPR offset: the buffer range
+  // check covers only the former, so rows past the tile's last valid row read zero.
+  const int vrow[4] = {voff + (4 * wv) * 16 * kLH, voff + (4 * wv + 1) * 16 * kLH,
+                       voff + (4 * wv + 2) * 16 * kLH, voff + (4 * wv + 3) * 16 * kLH};
+  auto issue_to = [&](const Tile& t, int ks, int8_t* as, int8_t* bs, int i) {
+    const int q = wv * 4 + i;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(t.a, as + q * 1024, 16, vrow[i], ks * kBK, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(t.b, bs + q * 1024, 16, vrow[i], ks * kBK, 0, 2);
+  };
+  auto issue_step = [&](const Tile& t, int ks, auto st, int i) { issue_to(t, ks, a_st(st), b_st(st), i); };
+  // the tile's weight and row scales (wave w: entries 64 w .. 64 w + 63 of each; past V or R: zero)
+  auto issue_scales = [&](const Tile& t, int par) {
+    const __amdgpu_buffer_rsrc_t ws = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(d.ws + t.v0), (short)0, min(d.V - t.v0, kBN) * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(d.xs + t.r0), (short)0, min(d.R - t.r0, kBM) * 4, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, &sc_l[par][0][64 * wv], 4, 4 * lane + 256 * wv, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, &sc_l[par][1][64 * wv], 4, 4 * lane + 256 * wv, 0, 0, 0);
+  };
+  // Fragments: lane l reads tile row 32 t + l % 32, K bytes 16 (l / 32) of each 32-byte half step
+  // (LDS chunk 2 h + l / 32); the MFMA gives lane l token l % 32 and vocab rows
   // 8 (j / 4) + 4 (l / 32) + j % 4 of register j.
   const int l32 = lane & 31, lh = lane >> 5;
-  const int fx0 = bswz(wm * 128 + l32, lh), fx1 = bswz(wm * 128 + l32, 2 + lh);  // + 32 kBK per tile
+  const int fx0 = bswz(wm * 128 + l32, lh), fx1 = bswz(wm * 128 + l32, 2 + lh);  // + 32 kBK per t
   const int fw0 = bswz(wn * 128 + l32, lh), fw1 = bswz(wn * 128 + l32, 2 + lh);
-  v16i acc[4][4];  // [vocab tile][token tile]
-  // One K step.  The wait leaves the 16 loads of steps ks + 1 and ks + 2 in flight, so this wave's
-  // loads of step ks are in LDS and its LDS reads of step ks - 1 are done; after the barrier both
-  // hold for all four waves.  Step ks + 3 then refills the stage step ks - 1 used (past the end the
-  // loads repeat step NK - 1 into stages nobody reads again, keeping the count in flight uniform).
-  // The first step starts the accumulators from zero inside the MFMA (a zero-initialised
-  // accumulator array carried into the loop makes the register allocator shuffle it every step).
-  auto body = [&](int ks, auto cur, auto nxt, auto first) {
-    asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)" ::: "memory");
+  v16i acc[4][4];     // [vocab block][token block]
+  v4i fx[2][2][4], fw[2][2][4];  // [register set][half step][block]
+  auto read_one = [&](auto st, auto fb, int k) {  // fragment k (0..15) of a step
+    const int8_t* as = a_st(st);
+    const int8_t* bs = b_st(st);
+    constexpr int f = decltype(fb)::value;
+    const int h = (k >> 2) & 1, t = k & 3;
+    if (k < 8) fx[f][h][t] = *reinterpret_cast<const v4i*>(as + (h ? fx1 : fx0) + t * 32 * kBK);
+    else fw[f][h][t] = *reinterpret_cast<const v4i*>(bs + (h ? fw1 : fw0) + t * 32 * kBK);
+  };
+  auto mfma_one = [&](auto fb, auto first, int k) {  // MFMA k (0..31) of a step
+    constexpr int f = decltype(fb)::value;
+    const int h = k >> 4, vi = (k >> 2) & 3, ti = k & 3;
+    acc[vi][ti] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+        fw[f][h][vi], fx[f][h][ti], (decltype(first)::value && h == 0) ? v16i{} : acc[vi][ti], 0, 0, 0);
+  };
+  // Step ks on register set FB (already read).  WAITN: this wave's loads allowed in flight once
+  // step ks + 1 has landed (16 in the steady state; 8 and 0 over the last steps, which load
+  // nothing).  LOADS: issue step ks + 4 into stage ks % 4.  NEXT: read step ks + 1 into the other set.
+  auto step = [&](const Tile& t, int ks, auto cur, auto fb, auto first, auto waitn, auto loads, auto next) {
+    wait_vm<decltype(waitn)::value>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    issue(min(ks + 3, NK - 1), nxt);
-    const int8_t* as = a_st(cur);
-    const int8_t* bs = b_st(cur);
-    v4i xf[2][4], wf[2][4];
+    using nb = ic<1 - decltype(fb)::value>;
+    using nst = ic<(decltype(cur)::value + 1) & 3>;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      xf[0][t] = *reinterpret_cast<const v4i*>(as + fx0 + t * 32 * kBK);
-      xf[1][t] = *reinterpret_cast<const v4i*>(as + fx1 + t * 32 * kBK);
-      wf[0][t] = *reinterpret_cast<const v4i*>(bs + fw0 + t * 32 * kBK);
-      wf[1][t] = *reinterpret_cast<const v4i*>(bs + fw1 + t * 32 * kBK);
+    for (int k = 0; k < 32; ++k) {
+      mfma_one(fb, first, k);
+      if constexpr (decltype(next)::value)
+        if (k < 16) read_one(nst{}, nb{}, k);
+      if constexpr (decltype(loads)::value)
+        if (k >= 16 && k < 20) issue_step(t, ks + 4, cur, k - 16);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // all 16 fragment reads go out before the first MFMA (left alone, the scheduler reuses one
-    // fragment register and waits out a full LDS latency per row of MFMAs)
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int vi = 0; vi < 4; ++vi)
-#pragma unroll
-        for (int ti = 0; ti < 4; ++ti)
-          acc[vi][ti] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-              wf[h][vi], xf[h][ti], (decltype(first)::value && h == 0) ? v16i{} : acc[vi][ti], 0, 0, 0);
   };
-  issue(0, ic<0>{});
-  issue(1, ic<1>{});
-  issue(2, ic<2>{});
-  body(0, ic<0>{}, ic<3>{}, std::true_type{});
-  body(1, ic<1>{}, ic<0>{}, std::false_type{});
-  body(2, ic<2>{}, ic<1>{}, std::false_type{});
-  body(3, ic<3>{}, ic<2>{}, std::false_type{});
-  for (int ks = 4; ks < NK; ks += 4) {
-    body(ks, ic<0>{}, ic<3>{}, std::false_type{});
-    body(ks + 1, ic<1>{}, ic<0>{}, std::false_type{});
-    body(ks + 2, ic<2>{}, ic<1>{}, std::false_type{});
-    body(ks + 3, ic<3>{}, ic<2>{}, std::false_type{});
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  // Epilogue: lane l holds tokens r0 + wm*128 + 32 ti + l % 32 and, per token, vocab columns
-  // cb + 32 vi + 8 (j / 4) + 4 (l / 32) + j % 4.  Each logit is rounded to bf16 once (hardware
-  // round-to-nearest-even) and folded into a 32-bit key (order-preserving bf16 bits << 16 |
-  // 0xffff - column in the tile; -0 and +0 share a key, as in the bf16 argmax): the lane's max key
-  // over its 64 columns, one exchange with lane l ^ 32, the two column waves through LDS, and the
-  // tile through one 64-bit atomic max per row.  Columns past V are skipped.
-  auto epilogue = [&](auto store, auto partial) {
+  int par = 0;
+  Tile t = tile(j);
+  issue_scales(t, 0);
+  issue_step(t, 0, ic<0>{}, 0), issue_step(t, 0, ic<0>{}, 1), issue_step(t, 0, ic<0>{}, 2), issue_step(t, 0, ic<0>{}, 3);
+  issue_step(t, 1, ic<1>{}, 0), issue_step(t, 1, ic<1>{}, 1), issue_step(t, 1, ic<1>{}, 2), issue_step(t, 1, ic<1>{}, 3);
+  issue_step(t, 2, ic<2>{}, 0), issue_step(t, 2, ic<2>{}, 1), issue_step(t, 2, ic<2>{}, 2), issue_step(t, 2, ic<2>{}, 3);
+  issue_step(t, 3, ic<3>{}, 0), issue_step(t, 3, ic<3>{}, 1), issue_step(t, 3, ic<3>{}, 2), issue_step(t, 3, ic<3>{}, 3);
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  for (;;) {
+    // the scales and step 0 of this tile: the oldest loads in flight (the epilogue's row atomics,
+    // issued after them, may finish first, hence 23 rather than 24)
+    if constexpr (STORE) wait_vm<0>(); else wait_vm<23>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-      const int rl = wm * 128 + ti * 32 + l32;
-      const int row = r0 + rl;
-      const float xsr = row < d.R ? d.xs[row] : 0.f;
-      uint32_t best = 0u;
+    for (int k = 0; k < 16; ++k) read_one(ic<0>{}, ic<0>{}, k);
+    step(t, 0, ic<0>{}, ic<0>{}, T_{}, ic<16>{}, T_{}, T_{});
+    step(t, 1, ic<1>{}, ic<1>{}, F_{}, ic<16>{}, T_{}, T_{});
+    step(t, 2, ic<2>{}, ic<0>{}, F_{}, ic<16>{}, T_{}, T_{});
+    step(t, 3, ic<3>{}, ic<1>{}, F_{}, ic<16>{}, T_{}, T_{});
+    for (int ks = 4; ks < kNK - 4; ks += 4) {
+      step(t, ks, ic<0>{}, ic<0>{}, F_{}, ic<16>{}, T_{}, T_{});
+      step(t, ks + 1, ic<1>{}, ic<1>{}, F_{}, ic<16>{}, T_{}, T_{});
+      step(t, ks + 2, ic<2>{}, ic<0>{}, F_{}, ic<16>{}, T_{}, T_{});
+      step(t, ks + 3, ic<3>{}, ic<1>{}, F_{}, ic<16>{}, T_{}, T_{});
+    }
+    step(t, kNK - 4, ic<0>{}, ic<0>{}, F_{}, ic<16>{}, F_{}, T_{});
+    step(t, kNK - 3, ic<1>{}, ic<1>{}, F_{}, ic<8>{}, F_{}, T_{});
+    step(t, kNK - 2, ic<2>{}, ic<0>{}, F_{}, ic<0>{}, F_{}, T_{});
+    // last step: once every wave has read the ring, the next tile's loads go out first
+    j += nloc;
+    const bool more = vt_of(j) < nvt;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const Tile tn = more ? tile(j) : t;
+    if (more) {
+      issue_scales(tn, par ^ 1);
 #pragma unroll
-      for (int vi = 0; vi < 4; ++vi)
+      for (int i = 0; i < 4; ++i) issue_step(tn, 0, ic<0>{}, i), issue_step(tn, 1, ic<1>{}, i),
+                                  issue_step(tn, 2, ic<2>{}, i), issue_step(tn, 3, ic<3>{}, i);
+    }
+    asm volatile("" ::: "memory");
 #pragma unroll
-        for (int jg = 0; jg < 4; ++jg) {
-          const int cl = wn * 128 + vi * 32 + 8 * jg + 4 * lh;  // first of the 4 columns, in the tile
-          const float4 w4 = *reinterpret_cast<const float4*>(&ws_l[cl]);
-          const float wq[4] = {w4.x, w4.y, w4.z, w4.w};
-          float lg[4];
+    for (int k = 0; k < 32; ++k) mfma_one(ic<1>{}, F_{}, k);
+    // Epilogue: lane l holds tokens r0 + wm*128 + 32 ti + l % 32 and, per token, vocab columns
+    // cb + 32 vi + 8 (j / 4) + 4 (l / 32) + j % 4, visited in increasing order.  Each logit
+    // (acc * xs) * ws is rounded to bf16 once (hardware round-to-nearest-even); the lane keeps the
+    // first column of its largest value (-0 and +0 compare equal, as in the bf16 argmax), folds it
+    // into a 32-bit key (order-preserving bf16 bits << 16 | 0xffff - column in the tile), exchanges
+    // it with lane l ^ 32 and the other column wave through LDS, and the tile's best per row goes
+    // out as one 64-bit atomic max.  Columns past V are skipped (nin: the lane's columns in range,
+    // counted from its first; V % 16 == 0 keeps each group of 4 all in or all out).
+    const float* wsl = sc_l[par][0];
+    const float* xsl = sc_l[par][1];
+    const int nin = d.V - t.v0 - (wn * 128 + 4 * lh);
+    {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            lg[q] = round_bf16(((float)acc[vi][ti][4 * jg + q] * xsr) * wq[q]);
-            uint32_t b16 = __float_as_uint(lg[q] + 0.f) >> 16;
-            b16 = (b16 & 0x8000u) ? (~b16 & 0xffffu) : (b16 | 0x8000u);
-            const uint32_t key = (b16 << 16) | (0xffffu - (uint32_t)(cl + q));
-            if (!decltype(partial)::value || v0 + cl + q < d.V) best = max(best, key);
+      for (int ti = 0; ti < 4; ++ti) {
+        const int rl = wm * 128 + ti * 32 + l32;
+        const int row = t.r0 + rl;
+        const float xsr = xsl[rl];
+        float bv = -__builtin_inff();
+        int bi = 0;  // column offset from cbase
+#pragma unroll
+        for (int vi = 0; vi < 4; ++vi)
+#pragma unroll
+          for (int jg = 0; jg < 4; ++jg) {
+            const int co = vi * 32 + 8 * jg;
+            const int cl = wn * 128 + co + 4 * lh;  // first of the lane's 4 columns, in the tile
+            const float4 w4 = *reinterpret_cast<const float4*>(&wsl[cl]);
+            const float wq[4] = {w4.x, w4.y, w4.z, w4.w};
+            float lg[4];
+            const bool in = co < nin;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              lg[q] = round_bf16(((float)acc[vi][ti][4 * jg + q] * xsr) * wq[q]);
+              if (in && lg[q] > bv) bv = lg[q], bi = co + q;
+            }
+            if constexpr (STORE)
+              if (row < d.R && in)
+                *reinterpret_cast<uint2*>(d.logits + (size_t)row * d.V + t.v0 + cl) =
+                    make_uint2((__float_as_uint(lg[0]) >> 16) | (__float_as_uint(lg[1]) & 0xffff0000u),
+                               (__float_as_uint(lg[2]) >> 16) | (__float_as_uint(lg[3]) & 0xffff0000u));
           }
-          if constexpr (decltype(store)::value)
-            if (row < d.R && v0 + cl < d.V)  // V % 16 == 0: the 4 columns are all in or all out
-              *reinterpret_cast<uint2*>(d.logits + (size_t)row * d.V + v0 + cl) =
-                  make_uint2((__float_as_uint(lg[0]) >> 16) | (__float_as_uint(lg[1]) & 0xffff0000u),
-                             (__float_as_uint(lg[2]) >> 16) | (__float_as_uint(lg[3]) & 0xffff0000u));
-        }
-      best = max(best, (uint32_t)__shfl_xor((int)best, 32));
-      if (lh == 0) rkey[wn][rl] = best;
+        uint32_t b16 = __float_as_uint(bv + 0.f) >> 16;
+        b16 = (b16 & 0x8000u) ? (~b16 & 0xffffu) : (b16 | 0x8000u);
+        uint32_t best = (b16 << 16) | (0xffffu - (uint32_t)(wn * 128 + 4 * lh + bi));
+        best = max(best, (uint32_t)__shfl_xor((int)best, 32));
+        if (lh == 0) rkey[wn][rl] = best;
+      }
     }
-  };
-  // the column checks only in the last vocab tile
-  if (v0 + kBN <= d.V) {
-    if (d.logits)
-      epilogue(std::true_type{}, std::false_type{});
-    else
-      epilogue(std::false_type{}, std::false_type{});
-  } else {
-    if (d.logits)
-      epilogue(std::true_type{}, std::true_type{});
-    else
-      epilogue(std::false_type{}, std::true_type{});
+    __syncthreads();
+    if (t.r0 + tid < d.R) {
+      const uint32_t k = max(rkey[0][tid], rkey[1][tid]);
+      const uint32_t col = (uint32_t)t.v0 + (0xffffu - (k & 0xffffu));
+      atomicMax(&d.keys[t.r0 + tid], ((unsigned long long)(k >> 16) << 32) | (unsigned long long)(0xffffffffu - col));
+    }
+    if (!more) break;
+    t = tn;
+    par ^= 1;
   }
-  __syncthreads();
-  if (r0 + tid < d.R) {
-    const uint32_t k = max(rkey[0][tid], rkey[1][tid]);
-    const uint32_t col = (uint32_t)v0 + (0xffffu - (k & 0xffffu));
-    atomicMax(&d.keys[r0 + tid], ((unsigned long long)(k >> 16) << 32) | (unsigned long long)(0xffffffffu - col));
-  }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lmh_gemm_kernel(LmhDev d) {
+  lmh_gemm_body<false>(d);
+}
+// the same with the bf16 logits written out
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lmh_gemm_logits_kernel(LmhDev d) {
+  lmh_gemm_body<true>(d);
 }
 
 __global__ __launch_bounds__(256) void lmh_ids_kernel(LmhDev d) {
   const int r = blockIdx.x * 256 + threadIdx.x;
   if (r < d.R) d.ids[r] = (int32_t)(0xffffffffu - (uint32_t)(d.keys[r] & 0xffffffffull));
+}
+
+int lmh_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    cached[dev] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus >= 8
+                      ? cus : 256;
+  }
+  return cached[dev];
 }
 
 struct LmhWs {
@@ -330,8 +425,14 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
   hipStream_t st = static_cast<hipStream_t>(stream);
   lmh_prep_kernel<<<(a->R + 3) / 4, 256, 0, st>>>(d);
   const int nvt = (a->V + kBN - 1) / kBN, nrt = (a->R + kBM - 1) / kBM;
-  const int blocks = ((nvt + 7) / 8) * 8 * nrt;
-  lmh_gemm_kernel<<<blocks, 256, 0, st>>>(d);
+  // persistent: one workgroup per CU (a multiple of 8, one XCD in eight), never more than the
+  // busiest XCD's tiles
+  const int ngrp = lmh_groups(nrt), vstep = 8 / ngrp;
+  const int blocks = 8 * std::max(1, std::min(lmh_cus() / 8, ((nvt + vstep - 1) / vstep) * (nrt / ngrp)));
+  if (d.logits)
+    lmh_gemm_logits_kernel<<<blocks, 256, 0, st>>>(d);
+  else
+    lmh_gemm_kernel<<<blocks, 256, 0, st>>>(d);
   lmh_ids_kernel<<<(a->R + 255) / 256, 256, 0, st>>>(d);
   return check_launch("q36_lmhead_argmax");
 }

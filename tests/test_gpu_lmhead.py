@@ -26,7 +26,8 @@ def _setup(lmh, dev, R, V, seed):
     return d, q, s
 
 
-@pytest.mark.parametrize("R,V,norm", [(1, 2048, True), (37, 4096, True), (256, 8192, False), (300, 4112, True)])
+@pytest.mark.parametrize("R,V,norm", [(1, 2048, True), (37, 4096, True), (256, 8192, False), (300, 4112, True),
+                                      (1024, 4112, True), (1536, 2320, False)])
 def test_lmhead_logits_and_ids_exact(lmh, oracle_mod, dev, R, V, norm):
     O = oracle_mod
     print(f"lmhead R={R} V={V} norm={norm}", flush=True)
