@@ -482,6 +482,8 @@ def main():
             "us_per_step": round(lmh_res["us_per_step"], 2), "ops": lmh_res["ops"],
             "achieved_tops": round(lmh_res["tops"], 1), "peak_tops": MFMA_I8_PEAK_TOPS,
             "frac_mfma": round(lmh_res["tops"] / MFMA_I8_PEAK_TOPS, 4),
+            # HBM bytes per call of the GEMM (weights twice: two XCD row groups), committed counter run
+            "traffic": measured_traffic("lmh_gemm_kernel"), "weight_bytes": 151936 * 2048,
             "workload": "2048 rows x 151936 vocab x 2048, int8 W8A8 + final RMSNorm + argmax"}
     if attn_res:
         line["attn_proj"] = {
