@@ -193,10 +193,12 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   // check covers only the former, so rows past the tile's last valid row read zero.
   const int vrow[4] = {voff + (4 * wv) * 16 * kLH, voff + (4 * wv + 1) * 16 * kLH,
                        voff + (4 * wv + 2) * 16 * kLH, voff + (4 * wv + 3) * 16 * kLH};
+  // Both operands with the default cache policy: the four workgroups of a row group read each weight
+  // line in turn, and a streaming hint on the weights (measured) lets lines go before the last reader.
   auto issue_to = [&](const Tile& t, int ks, int8_t* as, int8_t* bs, int i) {
     const int q = wv * 4 + i;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(t.a, as + q * 1024, 16, vrow[i], ks * kBK, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(t.b, bs + q * 1024, 16, vrow[i], ks * kBK, 0, 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(t.b, bs + q * 1024, 16, vrow[i], ks * kBK, 0, 0);
   };
   auto issue_step = [&](const Tile& t, int ks, auto st, int i) { issue_to(t, ks, a_st(st), b_st(st), i); };
   // the tile's weight and row scales (wave w: entries 64 w .. 64 w + 63 of each; past V or R: zero)
