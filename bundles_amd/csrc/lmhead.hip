@@ -10,16 +10,17 @@
 // Kernels:
 //   lmh_prep   one wave per row: norm (sum of squares in the fixed 64-lane order), int8 quant,
 //              and the row's argmax key reset to 0.
-//   lmh_gemm   256 x 256 output tile per workgroup (4 waves, 128 x 128 each, 32x32x32 int8 MFMAs
-//              with the weights as operand A, int32 accumulators in AGPRs), K in 64-byte steps
-//              through a 4-stage LDS ring filled by buffer loads straight into LDS, three steps
-//              ahead (no register staging).  Epilogue: bf16 logits, per-row max of the 64-bit key
-//              (order-preserving bf16 bits << 32 | ~index) over the tile, one 64-bit atomic max per
-//              row and tile: the result does not depend on the order the workgroups finish in.
+//   lmh_gemm   persistent, one 256-thread workgroup per CU walking 256 x 256 output tiles (4 waves
+//              of 128 x 128, 32x32x32 int8 MFMAs with the weights as operand A, int32 accumulators
+//              in AGPRs); K in 64-byte steps through a 4-stage LDS ring filled by buffer loads
+//              straight into LDS four steps ahead, fragments double-buffered in registers, and the
+//              next tile's first steps requested before the epilogue.  Epilogue: bf16 logits, the
+//              first column of each row's largest value folded into an order-preserving key, and one
+//              64-bit atomic max per row and tile: the result does not depend on the order the
+//              workgroups finish in.  lmh_gemm_logits: the same, writing the bf16 logits too.
 //   lmh_ids    key -> token id.
-// Block -> tile mapping: block b runs on XCD b % 8; the eight row tiles of one vocab tile are
-// consecutive blocks of the same XCD, so the weight tile is fetched from HBM once and served to
-// the eight from that XCD's L2.
+// Tile order: two row groups of XCDs (see lmh_gemm_body); the row tiles of one vocab tile run side
+// by side on one XCD, whose L2 serves them the weight tile and keeps their activations resident.
 #include <type_traits>
 
 #include "q36_device.h"
