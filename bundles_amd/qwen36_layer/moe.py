@@ -51,8 +51,16 @@ class ExpertWeights:
         return self.w13.shape[1] // 2
 
 
+def _bf16_weight(w: torch.Tensor, what: str) -> None:
+    """The quantizers read 2-byte bf16 elements: any other dtype would be misread (an fp8 tensor
+    would also be read past its end)."""
+    if w.dtype != torch.bfloat16 or not w.is_cuda:
+        raise ValueError(f"{what}: w must be a bf16 device tensor, got {w.dtype} on {w.device}")
+
+
 def quantize_rows_i8(w: torch.Tensor, stream=None):
     """Per-row int8 (s = amax/127, round half away): w bf16 [N, K] -> (q int8 [N, K], s fp32 [N])."""
+    _bf16_weight(w, "quantize_rows_i8")
     w2 = w.reshape(-1, w.shape[-1]).contiguous()
     N, K = w2.shape
     q = torch.empty((N, K), dtype=torch.int8, device=w.device)
@@ -64,6 +72,7 @@ def quantize_rows_i8(w: torch.Tensor, stream=None):
 
 def quantize_blocks_e4m3(w: torch.Tensor, stream=None):
     """128x128 block e4m3: w bf16 [..., N, K] -> (q uint8 [..., N, K], s fp32 [..., N/128, K/128])."""
+    _bf16_weight(w, "quantize_blocks_e4m3")
     N, K = w.shape[-2:]
     lead = w.shape[:-2]
     w2 = w.reshape(-1, K).contiguous()

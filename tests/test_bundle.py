@@ -2,6 +2,7 @@
 that exist, and point at entries the node modules define (CPU, no GPU)."""
 import json
 import os
+import types
 
 import pytest
 
@@ -55,3 +56,44 @@ def test_layer_prepare_rejects_unsupported_blocks():
         mlp = Block()
     with pytest.raises(RuntimeError):
         layer.prepare(Layer())
+
+
+def test_layer_prepare_rejects_non_bf16_experts():
+    """An fp8 or strided expert tensor is refused before anything reads it (the quantizers read bf16)."""
+    import torch
+    from bundles_amd.qwen36_layer import layer
+
+    def holder(**kw):
+        return types.SimpleNamespace(**kw)
+    E, H, I = 64, 2048, 512
+    bf = torch.bfloat16
+    for w13 in (torch.zeros((E, 2 * I, H), dtype=torch.float8_e4m3fn),
+                torch.zeros((E, H, 2 * I), dtype=bf).transpose(1, 2)):
+        block = holder(gate=holder(weight=torch.zeros((E, H), dtype=bf), bias=None),
+                       experts=holder(w13_weight=w13, w2_weight=torch.zeros((E, H, I), dtype=bf)),
+                       shared_expert=holder(gate_up_proj=holder(weight=torch.zeros((2 * I, H), dtype=bf)),
+                                            down_proj=holder(weight=torch.zeros((H, I), dtype=bf))),
+                       shared_expert_gate=holder(weight=torch.zeros((1, H), dtype=bf)))
+        with pytest.raises(RuntimeError, match="bf16"):
+            layer._MoeNode(block, 1, 10, 256)
+
+
+def test_row_batch_rule():
+    """Only decode and target-verify batches are row batches (the MoE path treats position-0 rows as
+    padding, so a prefill chunk must never reach it)."""
+    from bundles_amd.qwen36_layer import layer
+
+    class Mode:
+        def __init__(self, name):
+            self.name = name
+
+        def is_decode(self):
+            return self.name == "decode"
+
+        def is_target_verify(self):
+            return self.name == "verify"
+    for name, want in (("decode", True), ("verify", True), ("extend", False), ("idle", False)):
+        fb = types.SimpleNamespace(forward_mode=Mode(name))
+        assert layer.row_batch(fb) is want
+        assert layer.verify_batch(fb) is (name == "verify")
+    assert not layer.row_batch(types.SimpleNamespace(positions=None)) and not layer.row_batch(None)
