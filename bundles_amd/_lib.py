@@ -101,6 +101,7 @@ SYMBOLS = [
     ("q36_moe_down", I32, [C.POINTER(MoeArgs), P]),
     ("q36_moe_combine", I32, [C.POINTER(MoeArgs), P]),
     ("q36_moe_forward", I32, [C.POINTER(MoeArgs), P]),
+    ("q36_moe_forward_static", I32, [C.POINTER(MoeArgs), P]),
     ("q36_gdn_verify", I32, [C.POINTER(GdnArgs), P]),
     ("q36_gdn_verify_ring", I32, [C.POINTER(GdnRingArgs), P]),
     ("q36_attn_workspace_bytes", SZ, [I32]),

@@ -24,6 +24,8 @@
 // The shared expert is unit 0 of the up/down grids and covers every token.
 #include <string.h>
 
+#include <mutex>
+
 #include <type_traits>
 
 #include "q36_device.h"
@@ -1281,6 +1283,63 @@ extern "C" int q36_moe_forward(const q36_moe_args* a, q36_stream_t stream) {
   if ((rc = launch_up(d, a->dtype, st))) return rc;
   if ((rc = launch_down(d, a->dtype, st))) return rc;
   return launch_combine(d, st);
+}
+
+// ------------------------------------------------------------------------------------------
+// The no-allocation MoE entry: the workspace is a file-scope device array of fixed size instead of
+// a caller buffer.  Its host-side name is not a device address: the address is looked up once per
+// device (hipGetSymbolAddress, with that device current) and only that address is used.
+// ------------------------------------------------------------------------------------------
+namespace q36 {
+namespace {
+constexpr size_t kMoeStaticBytes = (size_t)Q36_MOE_STATIC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kMoeStaticBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// The calling thread's current device's copy of `scratch` (looked up on the first call per device).
+int static_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("q36_moe_forward_static: no current HIP device (or device id %d >= %d)", dev, kMaxDevices);
+    return Q36_ELAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("q36_moe_forward_static: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                hipGetErrorString(e));
+      return Q36_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return Q36_OK;
+}
+}  // namespace
+}  // namespace q36
+
+extern "C" int q36_moe_forward_static(const q36_moe_args* a, q36_stream_t stream) {
+  Q36_REQUIRE(a != nullptr, "q36_moe_forward_static: null args");
+  Q36_REQUIRE(a->workspace == nullptr && a->workspace_bytes == 0,
+              "q36_moe_forward_static: the workspace is the library's own; pass workspace = NULL, workspace_bytes = 0");
+  q36_moe_ws_layout L;
+  const bool shape_ok = a->M >= 1 && a->M <= kMaxM && a->E >= 1 && a->E <= kMaxE && a->topk >= 1 && a->topk <= 16;
+  if (shape_ok) layout(a->M, a->E, a->H, a->I, a->topk, a->dtype, &L);
+  Q36_REQUIRE(!shape_ok || L.total <= kMoeStaticBytes,
+              "q36_moe_forward_static: M=%d E=%d topk=%d needs %zu bytes of scratch, more than the library's %zu "
+              "(M <= 256 with E <= 512 and topk <= 10 fit)", a->M, a->E, a->topk, L.total, kMoeStaticBytes);
+  void* ws = nullptr;
+  int rc = static_scratch(&ws);
+  if (rc) return rc;
+  q36_moe_args b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = kMoeStaticBytes;
+  return q36_moe_forward(&b, stream);
 }
 
 extern "C" int q36_quant_rows_i8(const void* w, int64_t N, int32_t K, int8_t* q, float* s, q36_stream_t stream) {

@@ -134,6 +134,17 @@ int q36_moe_combine(const q36_moe_args* a, q36_stream_t stream);
 /* The whole MoE block: route, up, down, combine. */
 int q36_moe_forward(const q36_moe_args* a, q36_stream_t stream);
 
+/* q36_moe_forward without a caller workspace (no reference counterpart: for callers that cannot
+ * allocate, e.g. code under graph capture or a serving loop that forbids hipMalloc).  The workspace
+ * is a device array inside the library of Q36_MOE_STATIC_SCRATCH_BYTES bytes, one per GPU, held until
+ * the process ends; pass workspace = NULL and workspace_bytes = 0.  A call whose
+ * q36_moe_workspace_bytes(M, E, H, I, topk, dtype) exceeds it returns Q36_EINVAL (M <= 256 with
+ * E <= 512 and topk <= 10 fit).  Nothing is allocated or freed.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (two streams, two threads) race.  The array keeps the
+ * last call's contents; no call needs initial contents. */
+#define Q36_MOE_STATIC_SCRATCH_BYTES (16u << 20)
+int q36_moe_forward_static(const q36_moe_args* a, q36_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------
  * GDN speculative-verify step (L/qk_gdn_verify.cu:841-849 gdn_verify_fused), fixed head
  * geometry: 16 key heads x 128, 32 value heads x 128 (value head h reads key head h/2).
