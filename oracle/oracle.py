@@ -41,7 +41,8 @@ class MoeArgs(C.Structure):
     _fields_ = [("mode", I32), ("M", I32), ("E", I32), ("H", I32), ("I", I32), ("k", I32),
                 ("x", P), ("wr", P), ("bias", P), ("pos", P), ("w13", P), ("s13", P), ("w2", P),
                 ("s2", P), ("sw13", P), ("ss13", P), ("sw2", P), ("ss2", P), ("gate_w", P), ("out", P),
-                ("ids", P), ("wts", P), ("acc13", P), ("acc2", P), ("h", P), ("n_threads", I32)]
+                ("ids", P), ("wts", P), ("acc13", P), ("acc2", P), ("h", P), ("n_threads", I32),
+                ("h_in", P), ("y_in", P), ("y", P)]
 
 
 class GdnArgs(C.Structure):
@@ -217,8 +218,10 @@ def route(x_bf16, wr_bf16, k, bias=None, pos=None):
 
 # ---------------------------------------------------------------- MoE
 def moe(mode, x, wr, w13, s13, w2, s2, sw13, ss13, sw2, ss2, gate_w, k, bias=None, pos=None, debug=False,
-        n_threads=0):
-    """mode 0: int8 W8A8, mode 1: fp8 e4m3 block-scaled.  Returns dict(out, ids, wts[, acc13, acc2, h])."""
+        n_threads=0, h_in=None, y_in=None):
+    """mode 0: int8 W8A8, mode 1: fp8 e4m3 block-scaled.  Returns dict(out, ids, wts[, acc13, acc2, h, y]).
+    h_in / y_in (bf16 bits [M*k+M, I] / [M*k+M, H]) feed the down stage / the combine with another
+    implementation's intermediate rows (teacher forcing)."""
     x = np.ascontiguousarray(x, np.uint16)
     M, H = x.shape
     E = wr.shape[0]
@@ -227,15 +230,19 @@ def moe(mode, x, wr, w13, s13, w2, s2, sw13, ss13, sw2, ss2, gate_w, k, bias=Non
     res = dict(out=np.empty((M, H), np.uint16), ids=np.empty((M, k), np.int32), wts=np.empty((M, k), np.float32))
     if debug:
         res["h"] = np.zeros((S + M, I), np.uint16)
+        res["y"] = np.zeros((S + M, H), np.uint16)
         if mode == 0:
             res["acc13"] = np.zeros((S + M, 2 * I), np.int32)
             res["acc2"] = np.zeros((S + M, H), np.int32)
     keep = [np.ascontiguousarray(v) for v in (wr, w13, s13, w2, s2, sw13, ss13, sw2, ss2, gate_w)]
     b = None if bias is None else np.ascontiguousarray(bias, np.float32)
     ps = None if pos is None else np.ascontiguousarray(pos, np.int32)
+    hin = None if h_in is None else np.ascontiguousarray(h_in, np.uint16).reshape(S + M, I)
+    yin = None if y_in is None else np.ascontiguousarray(y_in, np.uint16).reshape(S + M, H)
     a = MoeArgs(mode, M, E, H, I, k, _p(x), *(_p(v) for v in keep[:1]), _p(b), _p(ps),
                 *(_p(v) for v in keep[1:]), _p(res["out"]), _p(res["ids"]), _p(res["wts"]),
-                _p(res.get("acc13")), _p(res.get("acc2")), _p(res.get("h")), n_threads)
+                _p(res.get("acc13")), _p(res.get("acc2")), _p(res.get("h")), n_threads, _p(hin), _p(yin),
+                _p(res.get("y")))
     rc = lib().q36o_moe(C.byref(a))
     if rc:
         raise ValueError("q36o_moe rejected the shapes")

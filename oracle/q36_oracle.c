@@ -378,10 +378,12 @@ typedef struct {
 } expert_t;
 
 static void expert_rows(const expert_t* ex, const void* xq, const float* xs, float wt, uint16_t* y_out,
-                        int32_t* acc13, int32_t* acc2, uint16_t* h_out) {
+                        int32_t* acc13, int32_t* acc2, uint16_t* h_out, const uint16_t* h_in) {
   int H = ex->H, I = ex->I;
   float* hf = (float*)malloc(sizeof(float) * I);
-  if (ex->mode == 0) {
+  if (h_in) {
+    for (int n = 0; n < I; ++n) hf[n] = q36o_bf16_to_f32(h_in[n]);
+  } else if (ex->mode == 0) {
     const int8_t* w = (const int8_t*)ex->w13;
     for (int n = 0; n < I; ++n) {
       int32_t ag = i8_row_dot((const int8_t*)xq, w + (size_t)n * H, H);
@@ -486,8 +488,10 @@ int q36o_moe(const q36o_moe_args* a) {
     }
     expert_rows(&ex, (const char*)xq + (size_t)t * H, xs + (size_t)t * ng, wt, y + (size_t)p * H,
                 a->acc13 ? a->acc13 + (size_t)p * 2 * I : NULL, a->acc2 ? a->acc2 + (size_t)p * H : NULL,
-                a->h ? a->h + (size_t)p * I : NULL);
+                a->h ? a->h + (size_t)p * I : NULL, a->h_in ? a->h_in + (size_t)p * I : NULL);
   }
+  if (a->y) memcpy(a->y, y, sizeof(uint16_t) * (size_t)(S + M) * H);
+  if (a->y_in) memcpy(y, a->y_in, sizeof(uint16_t) * (size_t)(S + M) * H);
   float* gw = (float*)malloc(sizeof(float) * H);
   for (int i = 0; i < H; ++i) gw[i] = q36o_bf16_to_f32(a->gate_w[i]);
 #pragma omp parallel for schedule(static)

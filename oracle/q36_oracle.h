@@ -80,6 +80,12 @@ typedef struct {
   int32_t* acc2;           /* optional */
   uint16_t* h;             /* optional */
   int n_threads;           /* 0 = OpenMP default */
+  /* Teacher forcing (NULL: off).  h_in bf16 [M*k+M, I]: the down stage reads these SwiGLU rows
+   * instead of its own; y_in bf16 [M*k+M, H]: the combine reads these weighted expert rows instead
+   * of its own.  Each stage can then be judged on the other implementation's inputs. */
+  const uint16_t* h_in;
+  const uint16_t* y_in;
+  uint16_t* y;             /* optional: the weighted expert rows by slot [M*k+M, H] */
 } q36o_moe_args;
 int q36o_moe(const q36o_moe_args* a);
 

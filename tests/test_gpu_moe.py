@@ -161,6 +161,55 @@ def test_moe_config2_fp8_full(q36, oracle_mod, dev):
     print(f"config 2 out: row err {wo:.2e} elem {ao:.2e} exact fraction {eo:.4f}", flush=True)
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_moe_config2_fp8_stages(q36, oracle_mod, dev, seed):
+    """Config 2 stage by stage, three seeds: the x quantization bit-exact; the gate/up stage (h) and
+    the down stage fed the GPU's own h (teacher forcing) each within the bf16 bar, with elementwise
+    errors and the number of re-quantization group scales that differ reported; the combine fed the
+    GPU's own weighted expert rows bit-exact; and the block end to end."""
+    from bundles_amd import synth
+    O = oracle_mod
+    M, E = 64, 512
+    print(f"moe config2 stages seed={seed}", flush=True)
+    d = synth.moe_inputs(M, dev, seed=seed, E=E, zipf=1.1)
+    ew = q36.prepare_experts(d["w13"], d["w2"], d["sw13"], d["sw2"], q36.Q36_MOE_FP8)
+    ws = q36.Workspace(E, 2048, 512, 10, q36.Q36_MOE_FP8, dev)
+    S = M * 10
+    dbg = {"h": torch.zeros((S + M, 512), dtype=torch.bfloat16, device=dev)}
+    out = q36.moe_row_batch(d["x"], None, d["router_w"], d["gate_w"], ew, 10, ws, router_bias=d["router_bias"],
+                            debug=dbg)
+    torch.cuda.synchronize()
+    v = ws.views(M)
+    hw = _host_weights(ew)
+    args = (1, bits16(d["x"]), bits16(d["router_w"]), hw["w13"], hw["s13"], hw["w2"], hw["s2"], hw["sw13"],
+            hw["ss13"], hw["sw2"], hw["ss2"], bits16(d["gate_w"]), 10)
+    kw = dict(bias=np_(d["router_bias"]), debug=True)
+    r = O.moe(*args, **kw)
+    assert np.array_equal(np_(v["ids"]), r["ids"])
+    # x quantization: e4m3 codes and per-(token, 128-group) scales
+    xq, xs = O.quant_groups_e4m3(O.bf16_to_f32(bits16(d["x"])))
+    assert np.array_equal(bits8(v["xq"]), xq) and np.array_equal(np_(v["xs"]).view(np.uint32), xs.view(np.uint32))
+    # up + SwiGLU
+    h_gpu, y_gpu = bits16(dbg["h"]), bits16(v["y"])
+    up = assert_bf16_close(h_gpu, r["h"], 1e-2, "up stage h")
+    # the down stage's re-quantization of h: scale of each (slot, 128-group)
+    _, hs_gpu = O.quant_groups_e4m3(O.bf16_to_f32(h_gpu))
+    _, hs_ref = O.quant_groups_e4m3(O.bf16_to_f32(r["h"]))
+    n_scale = int(np.sum(hs_gpu.view(np.uint32) != hs_ref.view(np.uint32)))
+    # down fed the GPU's h
+    rd = O.moe(*args, **kw, h_in=h_gpu)
+    dn = assert_bf16_close(y_gpu, rd["y"], 1e-2, "down stage y (teacher forced)")
+    # combine fed the GPU's y: the same fp32 sums in the same order
+    rc = O.moe(*args, **kw, y_in=y_gpu)
+    assert np.array_equal(bits16(out), rc["out"]), "combine (teacher forced) must be bit-exact"
+    e2e = assert_bf16_close(bits16(out), r["out"], 1e-2, "config 2 out")
+    print(f"seed {seed}: h exact {up[2]:.4f} row {up[0]:.2e} elem {up[1]:.2e}; group scales differing "
+          f"{n_scale}/{hs_ref.size}; down(tf) row {dn[0]:.2e} elem {dn[1]:.2e} exact {dn[2]:.4f}; "
+          f"end-to-end row {e2e[0]:.2e} elem {e2e[1]:.2e} exact {e2e[2]:.4f}", flush=True)
+    # elementwise bars (|g - r| / (|r| + rms of the row)): the stages one at a time are tight
+    assert up[1] <= 2e-2 and dn[1] <= 2e-2, (up, dn)
+
+
 def test_moe_repeat_deterministic(q36, dev):
     """Two calls on one workspace give identical bits (the self-resetting ticket, no races)."""
     from bundles_amd import synth

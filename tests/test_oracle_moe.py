@@ -109,3 +109,39 @@ def test_moe_padding_rows_are_zero(oracle_mod):
     r = O.moe(0, x, wr, w13, s13, w2, s2, sw13, ss13, sw2, ss2, gw, k, pos=pos)
     assert not r["out"][1].any() and r["out"][0].any() and r["out"][2].any()
     assert np.all(r["ids"][1] == -1)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_moe_teacher_forcing(oracle_mod, mode):
+    """The oracle's teacher-forced stages: fed its own h and y it reproduces itself bit for bit; a
+    changed h row moves only its own slot's y (and its token's output); a changed y row moves only its
+    token's output, by the float64 sum the combine restates."""
+    O = oracle_mod
+    rng = np.random.default_rng(60 + mode)
+    M, E, H, I, k = 3, 64, 2048, 512, 4
+    x = O.f32_to_bf16(rng.standard_normal((M, H)).astype(np.float32))
+    wr = O.f32_to_bf16((rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+    gw = O.f32_to_bf16((rng.standard_normal(H) * 0.02).astype(np.float32))
+    w13, s13, w2, s2 = _weights(O, mode, E, H, I, rng)
+    sw13, ss13, sw2, ss2 = (a[0].copy() for a in _weights(O, mode, 1, H, I, rng))
+    args = (mode, x, wr, w13, s13, w2, s2, sw13, ss13, sw2, ss2, gw, k)
+    r = O.moe(*args, debug=True)
+    r_h = O.moe(*args, debug=True, h_in=r["h"])
+    r_y = O.moe(*args, debug=True, y_in=r["y"])
+    for key in ("out", "y"):
+        assert np.array_equal(r_h[key], r[key]) and np.array_equal(r_y[key], r[key]), key
+    h2 = r["h"].copy()
+    slot = 1 * k + 2  # token 1, pick 2
+    h2[slot] = O.f32_to_bf16(O.bf16_to_f32(h2[slot]) * np.float32(1.5))
+    r2 = O.moe(*args, debug=True, h_in=h2)
+    changed = np.any(r2["y"] != r["y"], axis=1)
+    assert changed[slot] and changed.sum() == 1
+    assert np.array_equal(r2["out"][[0, 2]], r["out"][[0, 2]]) and np.any(r2["out"][1] != r["out"][1])
+    y2 = r["y"].copy()
+    y2[0 * k + 1] = O.f32_to_bf16(O.bf16_to_f32(y2[0 * k + 1]) + np.float32(0.25))
+    r3 = O.moe(*args, debug=True, y_in=y2)
+    assert np.array_equal(r3["out"][1:], r["out"][1:])
+    yf = O.bf16_to_f32(y2).astype(np.float64)
+    gate = 1.0 / (1.0 + np.exp(-np.dot(O.bf16_to_f32(x[0]).astype(np.float64), O.bf16_to_f32(gw).astype(np.float64))))
+    ref0 = yf[0:k].sum(0) + gate * yf[M * k + 0]
+    assert_bf16_close(r3["out"][:1], O.f32_to_bf16(ref0[None].astype(np.float32)), 1e-2, "combine of y_in")
