@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(HERE, "libq36.so")
 
 Q36_OK, Q36_EINVAL, Q36_ELAUNCH = 0, 1, 2
 Q36_MOE_INT8, Q36_MOE_FP8 = 0, 1
+Q36_LMH_W8A8, Q36_LMH_W8A8X2 = 0, 1
 
 P = C.c_void_p
 I32 = C.c_int32
@@ -65,7 +66,7 @@ class OprojArgs(C.Structure):
 
 class LmheadArgs(C.Structure):
     _fields_ = [("R", I32), ("H", I32), ("V", I32), ("h", P), ("norm_w", P), ("eps", C.c_float), ("wq", P),
-                ("ws", P), ("ids", P), ("logits", P), ("workspace", P), ("workspace_bytes", SZ)]
+                ("ws", P), ("ids", P), ("logits", P), ("workspace", P), ("workspace_bytes", SZ), ("mode", I32)]
 
 
 class LinearSeg(C.Structure):

@@ -3,7 +3,9 @@
 // Reference behaviour (R = qwen36_nodes_kb34, H = R/qwen36_lmhead8): per-row int8 activations
 // (H/w8a8.py:16-23), per-channel int8 weights with fp32 scales (H/lmhead8.py:95-143), int32
 // accumulation, logit = (acc * xs) * ws (H/w8a8.py:66-71) rounded to bf16 (the node's output
-// dtype); the greedy token is the first index of the largest bf16 logit (torch.argmax order; the
+// dtype); in the two-term form (H/w8a8.py:25-37, the reference's rule from 64 rows on) a second
+// int8 term quantizes the residual x - q1 s1 and logit = bf16(fma(acc1, s1, acc2 * s2) * ws)
+// (H/w8a8.py:66-70; L/qk_proj_decode.cu:1103-1107); the greedy token is the first index of the largest bf16 logit (torch.argmax order; the
 // reference leaves the argmax to the stock sampler, H/node.py:136-151).  A final Gemma RMSNorm
 // y = bf16((x * rstd) * (1 + w)) precedes the quantization (L/proj.py:60-81 restates the form).
 //
@@ -34,6 +36,8 @@ constexpr int kBM = 256, kBN = 256, kBK = 64, kNK = kLH / kBK;  // 32 K steps
 
 struct LmhDev {
   int R, V;
+  int Rs;   // activation rows in xq: R (one term) or 64 * ceil(R / 32) (two terms, see act_row)
+  int x2;   // two activation terms (Q36_LMH_W8A8X2)
   const uint16_t* h;
   const uint16_t* norm_w;
   float eps;
@@ -45,6 +49,14 @@ struct LmhDev {
   float* xs;
   unsigned long long* keys;
 };
+
+// Row of the activation codes holding term `term` of token r.  One term: row r.  Two terms: the
+// tokens go in groups of 32, each group's term-1 rows followed by its term-2 rows (row 64 (r / 32) +
+// 32 term + r % 32), so one lane of the GEMM holds both terms of the same token in its accumulators.
+__host__ __device__ __forceinline__ int act_row(int r, int term, int x2) {
+  return x2 ? 64 * (r >> 5) + 32 * term + (r & 31) : r;
+}
+__host__ __device__ __forceinline__ int act_rows(int R, int x2) { return x2 ? 64 * ((R + 31) >> 5) : R; }
 
 __global__ __launch_bounds__(256) void lmh_prep_kernel(LmhDev d) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -79,24 +91,31 @@ __global__ __launch_bounds__(256) void lmh_prep_kernel(LmhDev d) {
       }
     }
   }
-  float m = 0.f;
+  // one int8 term per row; with two terms the second quantizes the residual y - q1 s1 (formed as
+  // one fma) by the same rule, so y = q1 s1 + q2 s2 to within s2 / 2
+  for (int term = 0; term < (d.x2 ? 2 : 1); ++term) {
+    float m = 0.f;
 #pragma unroll
-  for (int j = 0; j < NJ; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(y[j][i]));
-  m = wave_max(m);
-  const float sc = m / 127.f, safe = m > 0.f ? sc : 1.f;
+      for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(y[j][i]));
+    m = wave_max(m);
+    const float sc = m / 127.f, safe = m > 0.f ? sc : 1.f;
+    const int row = act_row(r, term, d.x2);
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    uint32_t wd[2] = {0u, 0u};
+    for (int j = 0; j < NJ; ++j) {
+      uint32_t wd[2] = {0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) wd[i >> 2] |= ((uint32_t)round_i8(y[j][i] / safe) & 0xffu) << (8 * (i & 3));
-    *reinterpret_cast<uint2*>(d.xq + (size_t)r * kLH + 8 * (lane + 64 * j)) = make_uint2(wd[0], wd[1]);
+      for (int i = 0; i < 8; ++i) {
+        const int qv = round_i8(y[j][i] / safe);
+        wd[i >> 2] |= ((uint32_t)qv & 0xffu) << (8 * (i & 3));
+        y[j][i] = __builtin_fmaf(-(float)qv, sc, y[j][i]);
+      }
+      *reinterpret_cast<uint2*>(d.xq + (size_t)row * kLH + 8 * (lane + 64 * j)) = make_uint2(wd[0], wd[1]);
+    }
+    if (lane == 0) d.xs[row] = sc;
   }
-  if (lane == 0) {
-    d.xs[r] = sc;
-    d.keys[r] = 0ull;
-  }
+  if (lane == 0) d.keys[r] = 0ull;
 }
 
 // LDS position of 16-byte chunk kc (0..3) of tile row c in one K step: rows are 64 bytes, unpadded,
@@ -143,13 +162,13 @@ __device__ __forceinline__ void wait_vm() {
 // row groups of XCDs (see lmh_gemm_body): two when there are at least 4 row tiles, evenly split
 __host__ __device__ __forceinline__ int lmh_groups(int nrt) { return nrt >= 4 && nrt % 2 == 0 ? 2 : 1; }
 
-template <bool STORE>
+template <bool STORE, bool X2>
 __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   // one object per LDS stage: the compiler tracks the buffer-to-LDS loads of each object apart
   __shared__ __align__(1024) int8_t a_s0[kBM * kBK], a_s1[kBM * kBK], a_s2[kBM * kBK], a_s3[kBM * kBK];
   __shared__ __align__(1024) int8_t b_s0[kBN * kBK], b_s1[kBN * kBK], b_s2[kBN * kBK], b_s3[kBN * kBK];
   __shared__ __align__(16) float sc_l[2][2][kBN];  // [tile parity][weight scales | row scales]
-  __shared__ uint32_t rkey[2][kBM];
+  __shared__ uint32_t rkey[2][kBM];  // [column wave][row of the tile] (two terms: [token of the tile])
   auto a_st = [&](auto st) -> int8_t* {
     if constexpr (decltype(st)::value == 0) return a_s0;
     else if constexpr (decltype(st)::value == 1) return a_s1;
@@ -162,7 +181,7 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     else if constexpr (decltype(st)::value == 2) return b_s2;
     else return b_s3;
   };
-  const int nvt = (d.V + kBN - 1) / kBN, nrt = (d.R + kBM - 1) / kBM;
+  const int nvt = (d.V + kBN - 1) / kBN, nrt = (d.Rs + kBM - 1) / kBM;
   const int xcd = blockIdx.x & 7, loc = blockIdx.x >> 3, nloc = gridDim.x >> 3;
   const int ngrp = lmh_groups(nrt), rpg = nrt / ngrp, vstep = 8 / ngrp;
   const int rbase = (xcd % ngrp) * rpg, vres = xcd / ngrp;
@@ -185,7 +204,7 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     t.r0 = (rbase + jj % rpg) * kBM;
     t.v0 = vt_of(jj) * kBN;
     t.a = __builtin_amdgcn_make_buffer_rsrc((void*)(d.xq + (size_t)t.r0 * kLH), (short)0,
-                                            min(d.R - t.r0, kBM) * kLH, 0x00020000);
+                                            min(d.Rs - t.r0, kBM) * kLH, 0x00020000);
     t.b = __builtin_amdgcn_make_buffer_rsrc((void*)(d.wq + (size_t)t.v0 * kLH), (short)0,
                                             min(d.V - t.v0, kBN) * kLH, 0x00020000);
     return t;
@@ -207,7 +226,7 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     const __amdgpu_buffer_rsrc_t ws = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(d.ws + t.v0), (short)0, min(d.V - t.v0, kBN) * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(d.xs + t.r0), (short)0, min(d.R - t.r0, kBM) * 4, 0x00020000);
+        (void*)(d.xs + t.r0), (short)0, min(d.Rs - t.r0, kBM) * 4, 0x00020000);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, &sc_l[par][0][64 * wv], 4, 4 * lane + 256 * wv, 0, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, &sc_l[par][1][64 * wv], 4, 4 * lane + 256 * wv, 0, 0, 0);
   };
@@ -310,12 +329,18 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     const float* wsl = sc_l[par][0];
     const float* xsl = sc_l[par][1];
     const int nin = d.V - t.v0 - (wn * 128 + 4 * lh);
+    // One term: token block ti is rows wm*128 + 32 ti of the tile.  Two terms: blocks 2b and 2b + 1
+    // hold the two terms of the same 32 tokens (act_row), token wm*64 + 32 b + l32 of the tile.
+    constexpr int NTB = X2 ? 2 : 4;
+    const int tok0 = X2 ? t.r0 / 2 : t.r0;
     {
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti) {
-        const int rl = wm * 128 + ti * 32 + l32;
-        const int row = t.r0 + rl;
-        const float xsr = xsl[rl];
+      for (int tb = 0; tb < NTB; ++tb) {
+        const int ti = X2 ? 2 * tb : tb;
+        const int rl = X2 ? wm * 64 + tb * 32 + l32 : wm * 128 + ti * 32 + l32;  // token of the tile
+        const int row = tok0 + rl;
+        const float xsr = xsl[wm * 128 + ti * 32 + l32];
+        const float xs2 = X2 ? xsl[wm * 128 + (ti + 1) * 32 + l32] : 0.f;
         float bv = -__builtin_inff();
         int bi = 0;  // column offset from cbase
 #pragma unroll
@@ -330,7 +355,11 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
             const bool in = co < nin;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              lg[q] = round_bf16(((float)acc[vi][ti][4 * jg + q] * xsr) * wq[q]);
+              if constexpr (X2)
+                lg[q] = round_bf16(__builtin_fmaf((float)acc[vi][ti][4 * jg + q], xsr,
+                                                  (float)acc[vi][ti + 1][4 * jg + q] * xs2) * wq[q]);
+              else
+                lg[q] = round_bf16(((float)acc[vi][ti][4 * jg + q] * xsr) * wq[q]);
               if (in && lg[q] > bv) bv = lg[q], bi = co + q;
             }
             if constexpr (STORE)
@@ -347,10 +376,10 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
       }
     }
     __syncthreads();
-    if (t.r0 + tid < d.R) {
+    if (tid < (X2 ? kBM / 2 : kBM) && tok0 + tid < d.R) {
       const uint32_t k = max(rkey[0][tid], rkey[1][tid]);
       const uint32_t col = (uint32_t)t.v0 + (0xffffu - (k & 0xffffu));
-      atomicMax(&d.keys[t.r0 + tid], ((unsigned long long)(k >> 16) << 32) | (unsigned long long)(0xffffffffu - col));
+      atomicMax(&d.keys[tok0 + tid], ((unsigned long long)(k >> 16) << 32) | (unsigned long long)(0xffffffffu - col));
     }
     if (!more) break;
     t = tn;
@@ -358,12 +387,14 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   }
 }
 
+template <bool X2>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lmh_gemm_kernel(LmhDev d) {
-  lmh_gemm_body<false>(d);
+  lmh_gemm_body<false, X2>(d);
 }
 // the same with the bf16 logits written out
+template <bool X2>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lmh_gemm_logits_kernel(LmhDev d) {
-  lmh_gemm_body<true>(d);
+  lmh_gemm_body<true, X2>(d);
 }
 
 __global__ __launch_bounds__(256) void lmh_ids_kernel(LmhDev d) {
@@ -394,8 +425,9 @@ LmhWs lmh_ws(int R) {
     o = align_up(o + b, 256);
     return r;
   };
-  w.xq = take((size_t)R * kLH);
-  w.xs = take(sizeof(float) * (size_t)R);
+  const size_t rows = (size_t)act_rows(R, 1);  // room for two activation terms, whatever the mode
+  w.xq = take(rows * kLH);
+  w.xs = take(sizeof(float) * rows);
   w.keys = take(sizeof(unsigned long long) * (size_t)R);
   w.total = o;
   return w;
@@ -413,6 +445,7 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
   Q36_REQUIRE(a->H == kLH, "q36_lmhead_argmax: H=%d unsupported (this build is specialised to 2048)", a->H);
   Q36_REQUIRE(a->R >= 1 && a->R <= (1 << 20), "q36_lmhead_argmax: R=%d out of range", a->R);
   Q36_REQUIRE(a->V >= 16 && a->V % 16 == 0, "q36_lmhead_argmax: V=%d must be a positive multiple of 16", a->V);
+  Q36_REQUIRE(a->mode == Q36_LMH_W8A8 || a->mode == Q36_LMH_W8A8X2, "q36_lmhead_argmax: mode %d unknown", a->mode);
   Q36_REQUIRE(a->h && a->wq && a->ws && a->ids && a->workspace, "q36_lmhead_argmax: a required pointer is null");
   Q36_REQUIRE(aligned16(a->h) && aligned16(a->wq) && aligned16(a->ws) && aligned16(a->norm_w) &&
                   (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0,
@@ -421,21 +454,26 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
   Q36_REQUIRE(a->workspace_bytes >= L.total, "q36_lmhead_argmax: workspace of %zu bytes < %zu required",
               a->workspace_bytes, L.total);
   char* ws = static_cast<char*>(a->workspace);
-  LmhDev d{a->R, a->V, static_cast<const uint16_t*>(a->h), static_cast<const uint16_t*>(a->norm_w), a->eps,
+  const int x2 = a->mode == Q36_LMH_W8A8X2;
+  LmhDev d{a->R, a->V, act_rows(a->R, x2), x2, static_cast<const uint16_t*>(a->h), static_cast<const uint16_t*>(a->norm_w), a->eps,
            static_cast<const int8_t*>(a->wq), a->ws, a->ids, static_cast<uint16_t*>(a->logits),
            reinterpret_cast<int8_t*>(ws + L.xq), reinterpret_cast<float*>(ws + L.xs),
            reinterpret_cast<unsigned long long*>(ws + L.keys)};
   hipStream_t st = static_cast<hipStream_t>(stream);
   lmh_prep_kernel<<<(a->R + 3) / 4, 256, 0, st>>>(d);
-  const int nvt = (a->V + kBN - 1) / kBN, nrt = (a->R + kBM - 1) / kBM;
+  const int nvt = (a->V + kBN - 1) / kBN, nrt = (d.Rs + kBM - 1) / kBM;
   // persistent: one workgroup per CU (a multiple of 8, one XCD in eight), never more than the
   // busiest XCD's tiles
   const int ngrp = lmh_groups(nrt), vstep = 8 / ngrp;
   const int blocks = 8 * std::max(1, std::min(lmh_cus() / 8, ((nvt + vstep - 1) / vstep) * (nrt / ngrp)));
-  if (d.logits)
-    lmh_gemm_logits_kernel<<<blocks, 256, 0, st>>>(d);
+  if (d.logits && x2)
+    lmh_gemm_logits_kernel<true><<<blocks, 256, 0, st>>>(d);
+  else if (d.logits)
+    lmh_gemm_logits_kernel<false><<<blocks, 256, 0, st>>>(d);
+  else if (x2)
+    lmh_gemm_kernel<true><<<blocks, 256, 0, st>>>(d);
   else
-    lmh_gemm_kernel<<<blocks, 256, 0, st>>>(d);
+    lmh_gemm_kernel<false><<<blocks, 256, 0, st>>>(d);
   lmh_ids_kernel<<<(a->R + 255) / 256, 256, 0, st>>>(d);
   return check_launch("q36_lmhead_argmax");
 }

@@ -28,8 +28,9 @@ class Workspace:
 
 
 def w8a8_lmhead_argmax(h, q, scale, ws: Workspace, norm_w=None, eps: float = 1e-6, want_logits: bool = False,
-                       ids=None, stream=None):
-    """h bf16 [R, 2048] -> ids int32 [R] (and bf16 logits [R, V] when want_logits)."""
+                       ids=None, stream=None, two_term: bool = False, logits=None):
+    """h bf16 [R, 2048] -> ids int32 [R] (and bf16 logits [R, V] when want_logits, into `logits` when
+    given).  two_term: the reference's two-term activation form (H/w8a8.py:25-37)."""
     R, H = h.shape
     V = q.shape[0]
     if R > ws.R_max:
@@ -38,8 +39,12 @@ def w8a8_lmhead_argmax(h, q, scale, ws: Workspace, norm_w=None, eps: float = 1e-
         if t.dtype != dt or not t.is_contiguous():
             raise ValueError(f"w8a8_lmhead_argmax: {name} must be contiguous {dt}")
     ids = torch.empty(R, dtype=torch.int32, device=h.device) if ids is None else ids
-    logits = torch.empty((R, V), dtype=torch.bfloat16, device=h.device) if want_logits else None
+    if want_logits and logits is None:
+        logits = torch.empty((R, V), dtype=torch.bfloat16, device=h.device)
+    if logits is not None and (logits.dtype != torch.bfloat16 or tuple(logits.shape) != (R, V) or
+                               not logits.is_contiguous()):
+        raise ValueError(f"w8a8_lmhead_argmax: logits must be contiguous bf16 [{R}, {V}]")
     a = LmheadArgs(R, H, V, ptr(h), ptr(norm_w), eps, ptr(q), ptr(scale), ptr(ids), ptr(logits), ptr(ws.buf),
-                   ws.buf.numel())
+                   ws.buf.numel(), _lib.Q36_LMH_W8A8X2 if two_term else _lib.Q36_LMH_W8A8)
     check(_lib.lib().q36_lmhead_argmax(C.byref(a), _lib.stream_handle(stream)), "q36_lmhead_argmax")
-    return (ids, logits) if want_logits else ids
+    return (ids, logits) if (want_logits or logits is not None) else ids

@@ -1,99 +1,152 @@
-"""lm_head node: prepare(module) / forward(prepared, *args, **kwargs).
+"""Logits-processor node: prepare(module) / forward(prepared, *args, **kwargs).
 
-Mirrors the reference's logits-processor node (R = qwen36_nodes_kb34, H = R/qwen36_lmhead8):
-  prepare  <- H/node.py:169-170: wrap the served logits processor.
-  forward  <- H/node.py:172-173: run the stock processor with the lm_head swapped for a stand-in
-              whose apply() computes the logits on the int8 path (H/node.py:100-110, :154-167).
-The int8 copy of the head weight is built once per weight (H/node.py:123-134: keyed on the
-weight's pointer, shape, dtype and device, never while a graph is being captured), rows are
-quantized per row at call time, and the logits come from q36_lmhead_argmax with the logits
-output enabled (bf16, as the reference's w8a8_linear returns them).  The greedy ids of the same
-launch are kept on the node (last_ids) for a sampler that reads them instead of taking the
-argmax again.  Anything the int8 path does not cover (an embedding bias, non-bf16 or strided
-hidden states, more rows than MAX_ROWS, a weight shape other than [V, 2048]) goes to the stock
-matmul, as in the reference (H/node.py:150-151).
+The slot (R = qwen36_nodes_kb34, H = R/qwen36_lmhead8; entries H/node.py:169-173) wraps the served
+logits processor.  The processor computes logits through its lm_head argument: a head with a dense
+`weight` is multiplied directly, any other head through `head.quant_method.apply(head, hidden_states,
+embedding_bias)`.  The node hands the processor an Int8Head in place of a plain bf16 head: an object
+without a `weight` whose quant_method is itself, so the processor's own code calls Int8Head.apply,
+which runs q36_lmhead_argmax on an int8 copy of the served weight.  Everything else the processor does
+(pruning, gathering, sampling metadata) is untouched.
+
+Design:
+  HeadCopy     the int8 copy of one served weight (codes + per-row fp32 scales, H/lmhead8.py:95-143),
+               built on the first eligible call outside graph capture and rebuilt only when the served
+               weight's storage, shape or version changes.
+  row policy   the arithmetic follows the reference's choice by row count (H/node.py:9-11,144-151),
+               within what this build has: at most MAX_TWO_TERM rows run the two-term W8A8 form
+               (H/w8a8.py:25-37; the reference's rule from 64 rows, and its nearest form below 64,
+               where it runs W8A16); more rows, up to MAX_ROWS, run the one-term W8A8 form (config 5's
+               int8 lm_head over 2048 rows; the reference hands more than 256 rows to a bf16 matmul).
+  greedy ids   the same launch finds each row's first largest logit; Int8Head keeps them on the node
+               (last_ids) for a sampler that reads them instead of taking the argmax again.
+Heads the int8 path does not serve (no dense 2-D bf16 CUDA weight of width 2048, LoRA-wrapped heads, an
+embedding bias, strided or non-bf16 hidden states, more than MAX_ROWS rows) reach the processor as they
+came, so its stock code runs.
 """
 from __future__ import annotations
+
+from dataclasses import dataclass
 
 import torch
 
 from . import lmhead8
 
-MAX_ROWS = 4096
 HIDDEN = 2048
+MAX_ROWS = 4096       # rows a call may carry on the int8 path (the workspace is sized once for this)
+MAX_TWO_TERM = 256    # row batches up to this size take the two-term activation form
 
 
-class _Apply:
-    __slots__ = ("node", "lm_head")
-
-    def __init__(self, node, lm_head):
-        self.node, self.lm_head = node, lm_head
-
-    def apply(self, _stand_in, hidden_states, embedding_bias=None):
-        return self.node.logits(self.lm_head, hidden_states, embedding_bias)
+def row_mode(rows: int) -> str:
+    """The activation form for a row batch of `rows` rows: 'two_term' or 'one_term'."""
+    return "two_term" if rows <= MAX_TWO_TERM else "one_term"
 
 
-class _StandInHead:
-    __slots__ = ("quant_method",)
-
-    def __init__(self, apply):
-        self.quant_method = apply
+def _servable_weight(w) -> bool:
+    return (isinstance(w, torch.Tensor) and w.dim() == 2 and w.is_cuda and w.dtype == torch.bfloat16
+            and w.shape[1] == HIDDEN and w.shape[0] % 16 == 0 and w.stride(1) == 1)
 
 
-def _plain_head(lm_head) -> bool:
-    w = getattr(lm_head, "weight", None)
-    return isinstance(w, torch.Tensor) and w.dim() == 2
+def _version(w: torch.Tensor):
+    try:
+        return w._version
+    except RuntimeError:  # inference tensors track no version; storage, shape and device still bind
+        return None
 
 
-class _Node:
-    def __init__(self, module):
-        self.module = module
-        self.stock_forward = type(module).forward
-        self.q = self.scale = None
-        self.source = None
-        self.ws = None
-        self.last_ids = None
+@dataclass
+class HeadCopy:
+    q: torch.Tensor        # int8 [V, 2048]
+    scale: torch.Tensor    # fp32 [V]
+    ident: tuple           # (storage pointer, shape, device, version) of the weight it was built from
 
-    def _ready(self, weight) -> bool:
-        key = (weight.data_ptr(), tuple(weight.shape), weight.dtype, weight.device)
-        if self.q is not None and self.source == key:
-            return True
+    @staticmethod
+    def ident_of(w: torch.Tensor) -> tuple:
+        return (w.data_ptr(), tuple(w.shape), w.device, _version(w))
+
+
+class LogitsNode:
+    """The prepared node: call it as the served processor would be called."""
+
+    def __init__(self, processor):
+        self.processor = processor
+        self.stock_forward = type(processor).forward
+        self.copy: HeadCopy | None = None
+        self.workspace: lmhead8.Workspace | None = None
+        self.last_ids: torch.Tensor | None = None
+
+    # -- the int8 copy and scratch, made outside capture only --
+    def copy_for(self, w: torch.Tensor) -> HeadCopy | None:
+        ident = HeadCopy.ident_of(w)
+        if self.copy is not None and self.copy.ident == ident:
+            return self.copy
         if torch.cuda.is_current_stream_capturing():
-            return False
+            return None
+        self.copy = None  # free the stale copy before building the new one
         with torch.no_grad():
-            self.q, self.scale = lmhead8.quantize_rows(weight.to(torch.bfloat16).contiguous())
-        self.source = key
-        return True
+            q, s = lmhead8.quantize_rows(w.contiguous())
+        self.copy = HeadCopy(q, s, ident)
+        return self.copy
 
-    def logits(self, lm_head, hidden_states, embedding_bias=None):
-        weight = lm_head.weight
-        rows = hidden_states.shape[0] if hidden_states.dim() == 2 else 0
-        if (embedding_bias is None and hidden_states.dtype == torch.bfloat16 and 0 < rows <= MAX_ROWS
-                and hidden_states.shape[1] == HIDDEN == weight.shape[1] and weight.shape[0] % 16 == 0
-                and hidden_states.stride(1) == 1 and hidden_states.device == weight.device
-                and weight.device.type == "cuda" and self._ready(weight)):
-            if self.ws is None or self.ws.R_max < rows:
-                if torch.cuda.is_current_stream_capturing():
-                    return torch.matmul(hidden_states.to(weight.dtype), weight.T)
-                self.ws = lmhead8.Workspace(MAX_ROWS, hidden_states.device)
-            ids, out = lmhead8.w8a8_lmhead_argmax(hidden_states.contiguous(), self.q, self.scale, self.ws,
-                                                  want_logits=True)
-            self.last_ids = ids
-            return out
+    def workspace_for(self, device) -> lmhead8.Workspace | None:
+        if self.workspace is None:
+            if torch.cuda.is_current_stream_capturing():
+                return None
+            self.workspace = lmhead8.Workspace(MAX_ROWS, device)
+        return self.workspace
+
+    # -- one call of the int8 head; None: not served here --
+    def int8_logits(self, weight, hidden_states, embedding_bias):
         self.last_ids = None
-        return torch.matmul(hidden_states.to(weight.dtype), weight.T)
+        h = hidden_states
+        if (embedding_bias is not None or not isinstance(h, torch.Tensor) or h.dim() != 2
+                or h.dtype != torch.bfloat16 or h.shape[1] != HIDDEN or not 0 < h.shape[0] <= MAX_ROWS
+                or h.device != weight.device or h.stride(1) != 1):
+            return None
+        hc = self.copy_for(weight)
+        ws = self.workspace_for(h.device) if hc is not None else None
+        if ws is None:
+            return None
+        ids, logits = lmhead8.w8a8_lmhead_argmax(h.contiguous(), hc.q, hc.scale, ws, want_logits=True,
+                                                 two_term=row_mode(h.shape[0]) == "two_term")
+        self.last_ids = ids
+        return logits
 
     def __call__(self, *args, **kwargs):
         if "lm_head" in kwargs:
-            if _plain_head(kwargs["lm_head"]):
-                kwargs = {**kwargs, "lm_head": _StandInHead(_Apply(self, kwargs["lm_head"]))}
-        elif len(args) > 2 and _plain_head(args[2]):
-            args = (*args[:2], _StandInHead(_Apply(self, args[2])), *args[3:])
-        return self.stock_forward(self.module, *args, **kwargs)
+            head = kwargs["lm_head"]
+            if Int8Head.serves(head):
+                kwargs = dict(kwargs, lm_head=Int8Head(self, head))
+        elif len(args) > 2 and Int8Head.serves(args[2]):
+            args = args[:2] + (Int8Head(self, args[2]),) + args[3:]
+        return self.stock_forward(self.processor, *args, **kwargs)
+
+
+class Int8Head:
+    """Stands in for the served head inside one processor call: no `weight`, and quant_method is the
+    object itself, whose apply() the processor calls with the hidden rows."""
+
+    def __init__(self, node: LogitsNode, served):
+        self.node, self.served = node, served
+        self.quant_method = self
+
+    @staticmethod
+    def serves(head) -> bool:
+        if head is None or (hasattr(head, "set_lora") and hasattr(head, "apply_lora")):
+            return False
+        return _servable_weight(getattr(head, "weight", None))
+
+    def apply(self, layer, hidden_states, embedding_bias=None):
+        w = self.served.weight
+        out = self.node.int8_logits(w, hidden_states, embedding_bias)
+        if out is None:  # the stock product of the served weight (what the processor does for a dense head)
+            out = torch.matmul(hidden_states.to(w.dtype), w.T)
+            if embedding_bias is not None:
+                out += embedding_bias  # in place: the logits keep the head's dtype
+        return out
 
 
 def prepare(module):
-    return _Node(module)
+    return LogitsNode(module)
 
 
 def forward(prepared, *args, **kwargs):

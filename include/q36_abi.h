@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define Q36_ABI_VERSION 1
+#define Q36_ABI_VERSION 2
 #define Q36_OK 0
 #define Q36_EINVAL 1
 #define Q36_ELAUNCH 2
@@ -372,7 +372,13 @@ int q36_attn_decode(const q36_decode_args* a, q36_stream_t stream);
  * NULL to skip; y = bf16((h * rstd) * (1 + w))) -> per-row int8 (s = amax/127, half away) ->
  * acc = xq . wq^T (int32, wq int8 [V, H], ws fp32 [V]) -> logit = bf16((acc * xs) * ws) ->
  * ids int32 [R] = first index of the row's largest logit.  logits bf16 [R, V] is optional (NULL
- * skips the store).  V % 16 == 0.  Workspace: q36_lmhead_workspace_bytes(R), 256-byte aligned. */
+ * skips the store).  V % 16 == 0.  Workspace: q36_lmhead_workspace_bytes(R), 256-byte aligned
+ * (enough for every mode).
+ * mode Q36_LMH_W8A8X2: two activation terms (H/w8a8.py:25-37 quantize_act two_term, the reference's
+ * arithmetic from 64 rows): q1, s1 as above, then q2, s2 the same rule on the residual
+ * fma(-q1, s1, y); logit = bf16(fma(acc1, s1, acc2 * s2) * ws) (H/w8a8.py:66-70). */
+#define Q36_LMH_W8A8 0
+#define Q36_LMH_W8A8X2 1
 typedef struct q36_lmhead_args {
   int32_t R, H, V;
   const void* h;
@@ -384,6 +390,7 @@ typedef struct q36_lmhead_args {
   void* logits;
   void* workspace;
   size_t workspace_bytes;
+  int32_t mode; /* Q36_LMH_W8A8 or Q36_LMH_W8A8X2 */
 } q36_lmhead_args;
 size_t q36_lmhead_workspace_bytes(int32_t R);
 int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream);

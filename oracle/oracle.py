@@ -77,7 +77,7 @@ class DecodeArgs(C.Structure):
 
 class LmheadArgs(C.Structure):
     _fields_ = [("R", I32), ("H", I32), ("V", I32), ("h", P), ("norm_w", P), ("eps", C.c_float), ("wq", P),
-                ("ws", P), ("ids", P), ("logits", P), ("n_threads", I32)]
+                ("ws", P), ("ids", P), ("logits", P), ("n_threads", I32), ("mode", I32)]
 
 
 def _declare(L):
@@ -374,7 +374,7 @@ def attn_oproj(attn, gate, wo, so, n_threads=0):
 
 
 # ---------------------------------------------------------------- lm_head
-def lmhead(h, norm_w, eps, wq, ws, want_logits=False, n_threads=0):
+def lmhead(h, norm_w, eps, wq, ws, want_logits=False, n_threads=0, two_term=False):
     h = np.ascontiguousarray(h, np.uint16)
     R, H = h.shape
     V = wq.shape[0]
@@ -383,7 +383,7 @@ def lmhead(h, norm_w, eps, wq, ws, want_logits=False, n_threads=0):
     nw = None if norm_w is None else np.ascontiguousarray(norm_w, np.uint16)
     wq = np.ascontiguousarray(wq, np.int8)
     ws = np.ascontiguousarray(ws, np.float32)
-    a = LmheadArgs(R, H, V, _p(h), _p(nw), eps, _p(wq), _p(ws), _p(ids), _p(logits), n_threads)
+    a = LmheadArgs(R, H, V, _p(h), _p(nw), eps, _p(wq), _p(ws), _p(ids), _p(logits), n_threads, int(two_term))
     if lib().q36o_lmhead(C.byref(a)):
         raise ValueError("q36o_lmhead failed")
     return ids, logits

@@ -1059,10 +1059,12 @@ int q36o_attn_decode(const q36o_decode_args* a) {
  * logit (torch.argmax order; the reference leaves argmax to the stock sampler, H/node.py:136-151). */
 int q36o_lmhead(const q36o_lmhead_args* a) {
   int R = a->R, H = a->H, V = a->V;
-  if (H % 512) return -1;
+  if (H % 512 || a->mode < 0 || a->mode > 1) return -1;
+  const int two = a->mode == 1;
   if (a->n_threads > 0) omp_set_num_threads(a->n_threads);
-  int8_t* xq = (int8_t*)malloc((size_t)R * H);
-  float* xs = (float*)malloc(sizeof(float) * R);
+  /* term u of row r at xq + (2 r + u) H (two terms) or r H (one term) */
+  int8_t* xq = (int8_t*)malloc((size_t)R * H * (two ? 2 : 1));
+  float* xs = (float*)malloc(sizeof(float) * R * (two ? 2 : 1));
 #pragma omp parallel for schedule(static)
   for (int r = 0; r < R; ++r) {
     float* y = (float*)malloc(sizeof(float) * H);
@@ -1072,16 +1074,34 @@ int q36o_lmhead(const q36o_lmhead_args* a) {
       float rstd = 1.f / sqrtf(ss / (float)H + a->eps);
       for (int i = 0; i < H; ++i) y[i] = bf((y[i] * rstd) * (1.f + q36o_bf16_to_f32(a->norm_w[i])));
     }
-    quant_row_i8(y, H, xq + (size_t)r * H, xs + r);
+    int8_t* q1 = xq + (size_t)r * H * (two ? 2 : 1);
+    float* s1 = xs + (size_t)r * (two ? 2 : 1);
+    quant_row_i8(y, H, q1, s1);
+    if (two) {
+      /* H/w8a8.py:33-36: the second term quantizes x - q1 * s1 (one fused multiply-add) by the
+       * same rule */
+      for (int i = 0; i < H; ++i) y[i] = fmaf(-(float)q1[i], s1[0], y[i]);
+      quant_row_i8(y, H, q1 + H, s1 + 1);
+    }
     free(y);
   }
 #pragma omp parallel for schedule(dynamic, 1)
   for (int r = 0; r < R; ++r) {
     float best = -INFINITY;
     int bi = 0;
+    const int8_t* q1 = xq + (size_t)r * H * (two ? 2 : 1);
+    const float* s1 = xs + (size_t)r * (two ? 2 : 1);
     for (int n = 0; n < V; ++n) {
-      int32_t acc = i8_row_dot(xq + (size_t)r * H, a->wq + (size_t)n * H, H);
-      float lg = bf(((float)acc * xs[r]) * a->ws[n]);
+      int32_t acc = i8_row_dot(q1, a->wq + (size_t)n * H, H);
+      float lg;
+      if (two) {
+        /* H/w8a8.py:66-70 (the contraction L/qk_proj_decode.cu:1103-1107 states):
+         * fma(acc1, s1, acc2 * s2) * ws, rounded to bf16 */
+        int32_t acc2 = i8_row_dot(q1 + H, a->wq + (size_t)n * H, H);
+        lg = bf(fmaf((float)acc, s1[0], (float)acc2 * s1[1]) * a->ws[n]);
+      } else {
+        lg = bf(((float)acc * s1[0]) * a->ws[n]);
+      }
       if (a->logits) a->logits[(size_t)r * V + n] = q36o_f32_to_bf16(lg);
       if (lg > best) { best = lg; bi = n; }
     }

@@ -197,6 +197,7 @@ typedef struct {
   int32_t* ids;             /* [R] */
   uint16_t* logits;         /* optional bf16 [R, V] */
   int n_threads;
+  int mode;                 /* 0: one int8 activation term; 1: two terms (H/w8a8.py:25-37) */
 } q36o_lmhead_args;
 int q36o_lmhead(const q36o_lmhead_args* a);
 

@@ -1,7 +1,7 @@
 """GPU parity of the int8 lm_head + argmax (libq36 through the C-ABI) against the CPU oracle.
 
-Bar: int8 activations, logits (exact: int32 accumulation and two IEEE products) and argmax ids
-bit-exact."""
+Bar: int8 activations, logits (exact: int32 accumulation and two IEEE products; two terms: the int32
+accumulators of both terms, one fma and one product) and argmax ids bit-exact."""
 import numpy as np
 import pytest
 import torch
@@ -37,6 +37,40 @@ def test_lmhead_logits_and_ids_exact(lmh, oracle_mod, dev, R, V, norm):
     ids, logits = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=nw, eps=1e-6, want_logits=True)
     torch.cuda.synchronize()
     rid, rlog = O.lmhead(bits16(d["h"]), bits16(nw) if norm else None, 1e-6, np_(q), np_(s), want_logits=True)
+    assert np.array_equal(bits16(logits), rlog), "logits differ"
+    assert np.array_equal(np_(ids), rid), "argmax ids differ"
+
+
+@pytest.mark.parametrize("R,V,norm", [(1, 2048, True), (64, 4096, True), (100, 4112, False), (256, 8192, True),
+                                      (300, 2320, True)])
+def test_lmhead_two_term_logits_and_ids_exact(lmh, oracle_mod, dev, R, V, norm):
+    O = oracle_mod
+    print(f"lmhead two-term R={R} V={V} norm={norm}", flush=True)
+    d, q, s = _setup(lmh, dev, R, V, seed=3 * R + V)
+    ws = lmh.Workspace(R, dev)
+    nw = d["norm_w"] if norm else None
+    ids, logits = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=nw, eps=1e-6, want_logits=True, two_term=True)
+    torch.cuda.synchronize()
+    rid, rlog = O.lmhead(bits16(d["h"]), bits16(nw) if norm else None, 1e-6, np_(q), np_(s), want_logits=True,
+                         two_term=True)
+    assert np.array_equal(bits16(logits), rlog), "two-term logits differ"
+    assert np.array_equal(np_(ids), rid), "two-term argmax ids differ"
+
+
+@pytest.mark.parametrize("R,two", [(64, False), (300, False), (100, True)])
+def test_lmhead_full_vocab_logits(lmh, oracle_mod, dev, R, two):
+    """The full 151936 vocabulary with the logits stored: each persistent workgroup walks several
+    tiles (the next tile's loads in flight across the epilogue, the alternating scale buffers), and
+    every logit and id is compared."""
+    O = oracle_mod
+    V = 151936
+    print(f"lmhead full vocab logits R={R} two_term={two}", flush=True)
+    d, q, s = _setup(lmh, dev, R, V, seed=R + 11)
+    ws = lmh.Workspace(R, dev)
+    ids, logits = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=d["norm_w"], eps=1e-6, want_logits=True,
+                                         two_term=two)
+    torch.cuda.synchronize()
+    rid, rlog = O.lmhead(bits16(d["h"]), bits16(d["norm_w"]), 1e-6, np_(q), np_(s), want_logits=True, two_term=two)
     assert np.array_equal(bits16(logits), rlog), "logits differ"
     assert np.array_equal(np_(ids), rid), "argmax ids differ"
 

@@ -272,21 +272,39 @@ class _Processor(torch.nn.Module):
         return torch.matmul(hidden_states, lm_head.weight.T)
 
 
-def test_lmhead_node_logits_and_ids(dev):
+@pytest.mark.parametrize("R", [8, 100, 300])
+def test_lmhead_node_logits_and_ids(dev, R):
+    """The node's logits and greedy ids are the int8 path's: the two-term form up to 256 rows, one
+    term above; the served head is not modified."""
     from bundles_amd.qwen36_lmhead8 import lmhead8, node
-    R, V = 8, 4096
-    g = torch.Generator(device=dev).manual_seed(3)
+    V = 4096
+    g = torch.Generator(device=dev).manual_seed(3 + R)
     h = torch.randn((R, 2048), generator=g, device=dev).to(torch.bfloat16)
     head = _Holder(weight=(torch.randn((V, 2048), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+    w_before = head.weight.detach().clone()
     proc = _Processor()
     prepared = node.prepare(proc)
     logits = node.forward(prepared, None, h, head)
     q, s = lmhead8.quantize_rows(head.weight.data)
     ws = lmhead8.Workspace(R, dev)
-    ids, ref = lmhead8.w8a8_lmhead_argmax(h, q, s, ws, want_logits=True)
+    ids, ref = lmhead8.w8a8_lmhead_argmax(h, q, s, ws, want_logits=True, two_term=R <= node.MAX_TWO_TERM)
     torch.cuda.synchronize()
     assert torch.equal(logits.view(torch.int16), ref.view(torch.int16))
     assert torch.equal(prepared.last_ids, ids)
-    # an embedding bias is not on the int8 path: stock matmul
-    out = prepared.logits(head, h, embedding_bias=torch.zeros(V, device=dev))
+    assert torch.equal(head.weight, w_before)
+    # the copy is reused while the weight is unchanged, rebuilt after an in-place update
+    c0 = prepared.copy
+    node.forward(prepared, None, h, head)
+    assert prepared.copy is c0
+    with torch.no_grad():
+        head.weight.mul_(2)
+    node.forward(prepared, None, h, head)
+    assert prepared.copy is not c0
+    # an embedding bias is not on the int8 path: the stock product of the served weight
+    out = node.Int8Head(prepared, head).apply(None, h, embedding_bias=torch.zeros(V, device=dev))
     assert out.dtype == torch.bfloat16 and prepared.last_ids is None
+    # a head the node does not serve (fp32 weight) reaches the processor unchanged
+    head32 = _Holder(weight=torch.randn((V, 2048), generator=g, device=dev))
+    assert not node.Int8Head.serves(head32)
+    out = node.forward(prepared, None, h.float(), head32)
+    assert out.dtype == torch.float32

@@ -42,6 +42,44 @@ def test_lmhead_exact_without_norm(oracle_mod):
     assert np.array_equal(ids, np.argmax(O.bf16_to_f32(ref), axis=1))
 
 
+def torch_quant_two_term(y):
+    """The reference's two-term activation rule (H/w8a8.py:25-37) restated: the int8 rule on y, then on
+    the residual y - q1 s1 formed in float64 (q1 s1 and the difference are exact there) and rounded once
+    to float32, which is what one fused multiply-add gives."""
+    q1, s1 = torch_quant_rows_i8(y)
+    res = (y.astype(np.float64) - q1.astype(np.float64) * s1[:, None].astype(np.float64)).astype(np.float32)
+    q2, s2 = torch_quant_rows_i8(res)
+    return q1, s1, q2, s2, res
+
+
+def test_lmhead_two_term_exact(oracle_mod):
+    """Two terms: the int32 accumulators of both terms exactly (numpy int64), the epilogue
+    fma(acc1, s1, acc2 * s2) * ws (float64 fma then one float32 rounding, the multiply by ws rounded
+    again), the bf16 logits and ids bit for bit; the two terms reconstruct y to within s2 / 2."""
+    O = oracle_mod
+    R, V = 5, 1280
+    h, wq, ws = _lmhead_inputs(O, R, V, 4)
+    ids, logits = O.lmhead(h, None, 1e-6, wq, ws, want_logits=True, two_term=True)
+    y = O.bf16_to_f32(h)
+    q1, s1, q2, s2, res = torch_quant_two_term(y)
+    recon = q1.astype(np.float64) * s1[:, None] + q2.astype(np.float64) * s2[:, None]
+    assert np.all(np.abs(recon - y) <= s2[:, None] * 0.5 * (1 + 1e-5) + 1e-12)  # ties land on s2 / 2
+    assert np.all(s2 <= s1 * 0.5 * (1 + 1e-6))  # the residual is at most half a step of term 1
+    a1 = q1.astype(np.int64) @ wq.astype(np.int64).T
+    a2 = q2.astype(np.int64) @ wq.astype(np.int64).T
+    inner = (a2.astype(np.float32) * s2[:, None]).astype(np.float64)
+    f = (a1.astype(np.float64) * s1[:, None].astype(np.float64) + inner).astype(np.float32)  # one rounding
+    ref = O.f32_to_bf16(f * ws[None, :])
+    assert np.array_equal(logits, ref)
+    assert np.array_equal(ids, np.argmax(O.bf16_to_f32(ref), axis=1))
+    # the second term brings the logits closer to the unquantized activations' than one term does
+    exact = y.astype(np.float64) @ (wq.astype(np.float64) * ws[:, None]).T
+    _, one = O.lmhead(h, None, 1e-6, wq, ws, want_logits=True)
+    e1 = np.abs(O.bf16_to_f32(one) - exact).mean()
+    e2 = np.abs(O.bf16_to_f32(logits) - exact).mean()
+    assert e2 < 0.5 * e1, (e1, e2)
+
+
 def test_lmhead_ties_take_the_first_index(oracle_mod):
     O = oracle_mod
     R, V = 2, 512
