@@ -117,21 +117,25 @@ def bench_moe(args, torch, dev, n_layers=1, zipf=1.1, seed0=0):
     torch.cuda.synchronize()
     ms_graph = (time.perf_counter() - t0) * 1e3 / (reps * n_layers)
 
-    # each phase alone with events on its stream (for the kernel roofline), cycling the layers
+    # each phase alone, timed with events on its launch stream over `reps` rounds of the layers: the
+    # launches of one phase run back to back, cycling the layers (each layer's workspace keeps the
+    # lists and rows its earlier phases wrote), so with several layers every launch reads its weights
+    # from HBM
     phases = [dict(moe.moe_phases(x, None, L["d"]["router_w"], L["d"]["gate_w"], L["ew"], K, L["ws"], L["out"],
                                   router_bias=L["d"]["router_bias"])) for L in layers]
     order = ("route", "up", "down", "combine")
-    ev = {n: [] for n in order}
-    for _ in range(reps):
-        for ph in phases:
-            for n in order:
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record()
+    phase_ms = {}
+    for n in order:
+        for ph in phases:  # once untimed, so every layer's inputs to this phase are current
+            ph[n]()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            for ph in phases:
                 ph[n]()
-                b.record()
-                ev[n].append((a, b))
-    torch.cuda.synchronize()
-    phase_ms = {n: sum(a.elapsed_time(b) for a, b in ev[n]) / len(ev[n]) for n in order}
+        b.record()
+        b.synchronize()
+        phase_ms[n] = a.elapsed_time(b) / (reps * n_layers)
 
     # algorithmic bytes (each weight byte once per unique use, plus activations in and out)
     S = M * K

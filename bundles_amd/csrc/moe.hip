@@ -113,24 +113,25 @@ __device__ __forceinline__ void rs_stage(float* v, int lane) {
   }
 }
 constexpr int kRouteTT = 8;   // tokens per router workgroup
+constexpr int kRouteEW = 4;   // experts per router workgroup, one per wave
 constexpr int kRouteH = 2048;
 template <int DT>
 __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_router_wg) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int bid = blockIdx.x;
   if (bid < n_router_wg) {
+    // Router workgroup = 8 tokens x 4 experts, one expert per wave: the router GEMV is VALU work
+    // in the canonical order, so it is spread over every SIMD of the chip with several waves each
     constexpr int NJ = kRouteH / 512;
     __shared__ v4i xt[kRouteTT][kRouteH / 8];
-    const int neg = d.E / 16;
+    const int neg = d.E / kRouteEW;
     const int eg = bid % neg, tg = bid / neg;
-    const int e0 = eg * 16 + wave * 4;
+    const int e0 = eg * kRouteEW + wave;
     const int t0 = tg * kRouteTT;
-    v4i w[4][NJ];
+    v4i w[NJ];
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        w[e][j] = ldg16(reinterpret_cast<const uint8_t*>(d.wr + (size_t)(e0 + e) * kRouteH + 8 * (lane + 64 * j)));
+    for (int j = 0; j < NJ; ++j)
+      w[j] = ldg16(reinterpret_cast<const uint8_t*>(d.wr + (size_t)e0 * kRouteH + 8 * (lane + 64 * j)));
 #pragma unroll
     for (int r = 0; r < kRouteTT * kRouteH / 8 / 256; ++r) {
       const int c = threadIdx.x + 256 * r;
@@ -139,39 +140,37 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
       xt[t][cc] = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)tok * kRouteH + 8 * cc));
     }
     __syncthreads();
-    float v[kRouteTT * 4];
+    float v[kRouteTT];
 #pragma unroll
-    for (int i = 0; i < kRouteTT * 4; ++i) v[i] = 0.f;
+    for (int i = 0; i < kRouteTT; ++i) v[i] = 0.f;
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int t = 0; t < kRouteTT; ++t) {
         const v4i xv = xt[t][lane + 64 * j];
+        float a = v[t];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float a = v[t * 4 + e];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            a = __builtin_fmaf(bf_lo((uint32_t)xv[q]), bf_lo((uint32_t)w[e][j][q]), a);
-            a = __builtin_fmaf(bf_hi((uint32_t)xv[q]), bf_hi((uint32_t)w[e][j][q]), a);
-          }
-          v[t * 4 + e] = a;
+        for (int q = 0; q < 4; ++q) {
+          a = __builtin_fmaf(bf_lo((uint32_t)xv[q]), bf_lo((uint32_t)w[j][q]), a);
+          a = __builtin_fmaf(bf_hi((uint32_t)xv[q]), bf_hi((uint32_t)w[j][q]), a);
         }
+        v[t] = a;
       }
-    // reduce-scatter: after the stage with offset o a lane keeps the half of its outputs whose
-    // index bit matches its lane bit; 32 outputs over xor 32 .. 2 leave output (lane >> 1).
-    static_assert(kRouteTT * 4 == 32, "the stage list below assumes 32 outputs per wave");
-    rs_stage<32, 32>(v, lane);
-    rs_stage<16, 16>(v, lane);
-    rs_stage<8, 8>(v, lane);
-    rs_stage<4, 4>(v, lane);
-    rs_stage<2, 2>(v, lane);
-    float tot = v[0] + __shfl_xor(v[0], 1);
-    const int idx = lane >> 1;                 // index bits 4..0 = lane bits 5..1
-    const int t = idx >> 2, e = idx & 3;
-    if ((lane & 1) == 0 && t0 + t < d.M) {
-      if (d.bias) tot = tot + d.bias[e0 + e];
-      d.logits[(size_t)(t0 + t) * d.E + e0 + e] = rbf(tot);
+    // reduce-scatter over xor 32, 16, 8 (a lane keeps the half of its outputs whose index bit
+    // matches its lane bit: token (lane >> 3) after three stages), then the butterfly's last three
+    // stages (xor 4, 2, 1) among the eight lanes that hold the token
+    static_assert(kRouteTT == 8, "the stage list below assumes 8 outputs per wave");
+    rs_stage<8, 32>(v, lane);
+    rs_stage<4, 16>(v, lane);
+    rs_stage<2, 8>(v, lane);
+    float tot = v[0];
+    tot = tot + __shfl_xor(tot, 4);
+    tot = tot + __shfl_xor(tot, 2);
+    tot = tot + __shfl_xor(tot, 1);
+    const int t = lane >> 3;
+    if ((lane & 7) == 0 && t0 + t < d.M) {
+      if (d.bias) tot = tot + d.bias[e0];
+      d.logits[(size_t)(t0 + t) * d.E + e0] = rbf(tot);
     }
     return;
   }
@@ -1193,7 +1192,7 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
 // Raise a kernel's dynamic-LDS limit (once per device and kernel) when a launch needs more than
 // the 64 KiB default; gfx950 has 160 KiB per CU.
 int launch_route(const MoeDev& d, int dtype, hipStream_t st) {
-  const int n_router = (d.E / 16) * ((d.M + kRouteTT - 1) / kRouteTT);
+  const int n_router = (d.E / kRouteEW) * ((d.M + kRouteTT - 1) / kRouteTT);
   if (dtype == Q36_MOE_FP8)
     route_logits_kernel<Q36_MOE_FP8><<<n_router + d.M, 256, 0, st>>>(d, n_router);
   else

@@ -48,7 +48,7 @@ def test_static_rejections(dev):
     ws = moe.Workspace(1024, 2048, 512, 10, 1, dev, max_tokens=8)
     out = torch.empty_like(d["x"])
     a = moe._args(d["x"], None, d["router_w"], d["gate_w"], None, 10, ws, out, None, None)
-    a.dtype, a.M = 1, 256  # E = 1024 at 256 rows needs more than the static scratch
+    a.dtype, a.M, a.topk = 1, 256, 16  # 256 rows x 17 slots need more than the static scratch
     a.workspace, a.workspace_bytes = None, 0
     assert _call(L.q36_moe_forward_static, a) == 1
     assert b"scratch" in L.q36_last_error()
