@@ -26,7 +26,8 @@ class MoeArgs(C.Structure):
                 ("x", P), ("router_w", P), ("router_bias", P), ("positions", P),
                 ("w13", P), ("s13", P), ("w2", P), ("s2", P), ("sw13", P), ("ss13", P), ("sw2", P), ("ss2", P),
                 ("gate_w", P), ("out", P), ("workspace", P), ("workspace_bytes", SZ),
-                ("dbg_acc13", P), ("dbg_acc2", P), ("dbg_h", P)]
+                ("dbg_acc13", P), ("dbg_acc2", P), ("dbg_h", P),
+                ("resid", P), ("norm_w", P), ("norm_eps", C.c_float), ("norm_out", P)]
 
 
 class MoeWsLayout(C.Structure):

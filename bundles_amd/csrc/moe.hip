@@ -72,6 +72,10 @@ struct MoeDev {
   int32_t* dbg_acc13;
   int32_t* dbg_acc2;
   uint16_t* dbg_h;
+  uint16_t* resid;        // the fused add-norm (norm_out != nullptr)
+  const uint16_t* norm_w;
+  float norm_eps;
+  uint16_t* norm_out;
 };
 
 __device__ __forceinline__ v4i ldg16(const uint8_t* p) { return *reinterpret_cast<const v4i*>(p); }
@@ -983,19 +987,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // One workgroup per token; every y row of the token (its k routed slots t*k + j and the shared
 // slot M*k + t) is loaded before any is added, then
 // out = bf16(fma(gate, y_shared, ((0 + y_0) + y_1) ... + y_{k-1})).
+// With the fused add-norm (L/qk_route.cu:630-820 combine_norm): z = out + resid in fp32,
+// resid <- bf16(z), and the Gemma RMSNorm of z; the sum of squares runs in q36_add_rmsnorm's order
+// (lane l owns the 8-element chunks l + 64 j, fma from zero in j order, then an xor butterfly): the
+// workgroup's chunk c sits with thread c, so the z values meet in LDS and wave 0 adds them up.
+constexpr int kCombH = 2048;
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
   const int t = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool valid = d.pos == nullptr || d.pos[t] != 0;
   const int S = d.M * d.k;
-  __shared__ float gate_s;
+  __shared__ float gate_s, rstd_s;
   __shared__ int prow[17];
+  __shared__ float zs[kCombH / 8][8];
   if (tid <= d.k) prow[tid] = tid < d.k ? t * d.k + tid : S + t;
   if (valid && wave == 0) {
     float acc = 0.f;
-    for (int j = 0; j < d.H / 512; ++j) {
+    for (int j = 0; j < kCombH / 512; ++j) {
       const int c = lane + 64 * j;
-      const v4i xv = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)t * d.H + 8 * c));
+      const v4i xv = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)t * kCombH + 8 * c));
       const v4i gv = ldg16(reinterpret_cast<const uint8_t*>(d.gate_w + 8 * c));
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -1007,46 +1017,82 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
     if (lane == 0) gate_s = sigmoid_q(acc);
   }
   __syncthreads();
-  for (int c = tid; 8 * c < d.H; c += 256) {
-    uint4 o = make_uint4(0u, 0u, 0u, 0u);
-    if (valid) {
-      v4i yv[17];
+  const int c = tid;  // the thread's 8-element chunk (H = 2048: one per thread)
+  uint4 o = make_uint4(0u, 0u, 0u, 0u);
+  if (valid) {
+    v4i yv[17];
 #pragma unroll
-      for (int j = 0; j < 17; ++j)
-        yv[j] = ldg16(reinterpret_cast<const uint8_t*>(d.y + (size_t)prow[j <= d.k ? j : d.k] * d.H + 8 * c));
-      float acc[8];
+    for (int j = 0; j < 17; ++j)
+      yv[j] = ldg16(reinterpret_cast<const uint8_t*>(d.y + (size_t)prow[j <= d.k ? j : d.k] * kCombH + 8 * c));
+    float acc[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) acc[q] = 0.f;
+    for (int q = 0; q < 8; ++q) acc[q] = 0.f;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        if (j < d.k) {
+    for (int j = 0; j < 16; ++j) {
+      if (j < d.k) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            acc[2 * q] = acc[2 * q] + bf_lo((uint32_t)yv[j][q]);
-            acc[2 * q + 1] = acc[2 * q + 1] + bf_hi((uint32_t)yv[j][q]);
-          }
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] = acc[2 * q] + bf_lo((uint32_t)yv[j][q]);
+          acc[2 * q + 1] = acc[2 * q + 1] + bf_hi((uint32_t)yv[j][q]);
         }
       }
-      v4i sv = yv[0];
-#pragma unroll
-      for (int j = 1; j < 17; ++j)
-        if (j == d.k) sv = yv[j];
-      const float g = gate_s;
-      uint32_t w[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        w[q] = pack_bf2(__builtin_fmaf(g, bf_lo((uint32_t)sv[q]), acc[2 * q]),
-                        __builtin_fmaf(g, bf_hi((uint32_t)sv[q]), acc[2 * q + 1]));
-      o = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    *reinterpret_cast<uint4*>(d.out + (size_t)t * d.H + 8 * c) = o;
+    v4i sv = yv[0];
+#pragma unroll
+    for (int j = 1; j < 17; ++j)
+      if (j == d.k) sv = yv[j];
+    const float g = gate_s;
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      w[q] = pack_bf2(__builtin_fmaf(g, bf_lo((uint32_t)sv[q]), acc[2 * q]),
+                      __builtin_fmaf(g, bf_hi((uint32_t)sv[q]), acc[2 * q + 1]));
+    o = make_uint4(w[0], w[1], w[2], w[3]);
   }
+  const size_t at = (size_t)t * kCombH + 8 * c;
+  *reinterpret_cast<uint4*>(d.out + at) = o;
+  if (d.norm_out == nullptr) return;
+  // the fused add-norm
+  const v4i rv = *reinterpret_cast<const v4i*>(d.resid + at);
+  const uint32_t ow[4] = {o.x, o.y, o.z, o.w};
+  float z[8];
+  v4i nv;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    z[2 * q] = bf_lo(ow[q]) + bf_lo((uint32_t)rv[q]);
+    z[2 * q + 1] = bf_hi(ow[q]) + bf_hi((uint32_t)rv[q]);
+    nv[q] = (int)pack_bf2(z[2 * q], z[2 * q + 1]);
+  }
+  *reinterpret_cast<v4i*>(d.resid + at) = nv;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) zs[c][i] = z[i];
+  __syncthreads();
+  if (wave == 0) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kCombH / 512; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float zv = zs[lane + 64 * j][i];
+        ss = __builtin_fmaf(zv, zv, ss);
+      }
+    ss = wave_sum_bfly(ss);
+    if (lane == 0) rstd_s = 1.f / sqrtf(ss / (float)kCombH + d.norm_eps);
+  }
+  __syncthreads();
+  const float rstd = rstd_s;
+  const v4i wv = *reinterpret_cast<const v4i*>(d.norm_w + 8 * c);
+  v4i ov;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    ov[q] = (int)pack_bf2((z[2 * q] * rstd) * (1.f + bf_lo((uint32_t)wv[q])),
+                          (z[2 * q + 1] * rstd) * (1.f + bf_hi((uint32_t)wv[q])));
+  *reinterpret_cast<v4i*>(d.norm_out + at) = ov;
 }
 
 // ------------------------------------------------------------------------------------------
 // prepare-time quantizers
 // ------------------------------------------------------------------------------------------
-// One workgroup per row; K % 8 == 0.
 __global__ __launch_bounds__(256) void quant_rows_i8_kernel(const uint16_t* w, int K, int8_t* q, float* s) {
   const size_t row = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1163,9 +1209,11 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
                                 a->gate_w && a->out),
               "q36_moe_forward: an expert weight, scale, gate_w or out pointer is null");
   const void* ptrs[] = {a->x, a->router_w, a->w13, a->w2, a->sw13, a->sw2, a->gate_w, a->out, a->workspace,
-                        a->dbg_acc13, a->dbg_acc2, a->dbg_h};
+                        a->dbg_acc13, a->dbg_acc2, a->dbg_h, a->resid, a->norm_w, a->norm_out};
   for (const void* p : ptrs) Q36_REQUIRE(aligned16(p), "q36_moe: pointer %p is not 16-byte aligned", p);
   Q36_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0, "q36_moe: workspace must be 256-byte aligned");
+  Q36_REQUIRE(a->norm_out == nullptr || (a->resid && a->norm_w),
+              "q36_moe: the fused add-norm (norm_out) needs resid and norm_w");
   q36_moe_ws_layout L;
   layout(a->M, a->E, a->H, a->I, a->topk, a->dtype, &L);
   Q36_REQUIRE(a->workspace_bytes >= L.total, "q36_moe: workspace of %zu bytes is smaller than the %zu required",
@@ -1185,7 +1233,8 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
               reinterpret_cast<uint8_t*>(ws + L.xq),
               reinterpret_cast<float*>(ws + L.xs), reinterpret_cast<uint16_t*>(ws + L.h),
               reinterpret_cast<uint16_t*>(ws + L.y), a->dbg_acc13, a->dbg_acc2,
-              static_cast<uint16_t*>(a->dbg_h)};
+              static_cast<uint16_t*>(a->dbg_h), static_cast<uint16_t*>(a->resid),
+              static_cast<const uint16_t*>(a->norm_w), a->norm_eps, static_cast<uint16_t*>(a->norm_out)};
   return Q36_OK;
 }
 

@@ -7,8 +7,9 @@ the stock decoder layer the node replicates (L/layer.py:486-531): input add-norm
 MoE; the projection + add-norm around the mixers (L/proj.py:60-112); the GDN mixer's in_proj split
 and verify (L/proj_fused.py:1-20, L/gdn_fused.py:37-57); the attention verify (L/attn_fused.py:110-124,
 232-273); the lm_head node with the greedy sampler (H/node.py:136-151).  Each layer's input norm is the
-add-norm fed by the previous layer's MoE output (the reference folds it into the combine,
-L/layer.py:66-145; here it is its own launch).  Every launch is a libq36 entry; nothing here computes.
+add-norm fed by the previous layer's MoE output, folded into that MoE's combine launch as the
+reference folds it (L/layer.py:66-145, L/qk_route.cu:630-820).  Every launch is a libq36 entry;
+nothing here computes.
 
 The projections are e4m3 with 128x128 block scales (the configuration's weight format), the KV
 cache e4m3 with one-token pages, the lm_head int8 per channel.
@@ -178,7 +179,7 @@ class HybridWorkspace:
             return torch.empty(shape, dtype=dtype, device=dev)
         n_gdn = KINDS.count("gdn")
         self.bufs = dict(
-            residual=e(M, HIDDEN), h=e(M, HIDDEN), o=e(M, HIDDEN), m=e(M, HIDDEN),
+            residual=e(M, HIDDEN), h=e(M, HIDDEN), h2=e(M, HIDDEN), o=e(M, HIDDEN), m=e(M, HIDDEN),
             mixed=e(M, GDN_QKV), z=e(M, GDN_Z), b=e(M, GDN_HV), a=e(M, GDN_HV), gout=e(M, GDN_Z),
             snaps=[e(self.B, self.T, GDN_HV, 128, 128, dtype=torch.float32) for _ in range(n_gdn)] if self.snapshots
             else None,
@@ -207,7 +208,7 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
         if trace is not None:
             trace[name] = t.clone() if isinstance(t, torch.Tensor) else t
 
-    res, h = b["residual"], b["h"]
+    res, h, h_next = b["residual"], b["h"], b["h2"]
     res.copy_(x)
     add_rmsnorm(None, res, w.layers[0].input_norm_w, w.eps, out=h, stream=stream)
     keep("x", x)
@@ -254,11 +255,12 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
         add_rmsnorm(b["o"], res, L.post_norm_w, w.eps, out=h, stream=stream)
         keep(f"L{i}.post", h)
         keep(f"L{i}.res_mid", res)
-        moe.moe_row_batch(h, None, L.router_w, L.gate_w, L.experts, TOPK, ws.moe, out=b["m"],
-                          router_bias=L.router_bias, stream=stream)
-        keep(f"L{i}.moe", b["m"])
+        # the next block's input add-norm runs inside the MoE's combine (same bits as add_rmsnorm)
         nxt = w.layers[i + 1].input_norm_w if i + 1 < len(w.layers) else w.final_norm_w
-        add_rmsnorm(b["m"], res, nxt, w.eps, out=h, stream=stream)
+        moe.moe_row_batch(h, None, L.router_w, L.gate_w, L.experts, TOPK, ws.moe, out=b["m"],
+                          router_bias=L.router_bias, stream=stream, norm=(res, nxt, w.eps, h_next))
+        h, h_next = h_next, h
+        keep(f"L{i}.moe", b["m"])
         keep(f"L{i}.res_out", res)
     keep("final", h)
     lmhead8.w8a8_lmhead_argmax(h, w.lm_q, w.lm_s, ws.lmhead, norm_w=None, eps=w.eps, ids=b["ids"], stream=stream)

@@ -179,7 +179,7 @@ class Workspace:
             y=v(L.y, (S + M) * self.H, torch.bfloat16).view(S + M, self.H))
 
 
-def _args(x, positions, router_w, gate_w, ew, topk, ws: Workspace, out, router_bias, debug):
+def _args(x, positions, router_w, gate_w, ew, topk, ws: Workspace, out, router_bias, debug, norm=None):
     M, H = x.shape
     if M > ws.max_tokens:
         raise ValueError(f"moe_row_batch: {M} rows exceed the workspace's {ws.max_tokens}")
@@ -192,9 +192,19 @@ def _args(x, positions, router_w, gate_w, ew, topk, ws: Workspace, out, router_b
         raise ValueError("moe_row_batch: router_bias must be contiguous float32")
     dbg = debug or {}
     w = [None] * 8 if ew is None else [ew.w13, ew.s13, ew.w2, ew.s2, ew.sw13, ew.ss13, ew.sw2, ew.ss2]
+    resid = norm_w = norm_out = None
+    eps = 0.0
+    if norm is not None:
+        resid, norm_w, eps, norm_out = norm
+        for name, t in (("resid", resid), ("norm_out", norm_out)):
+            if t.dtype != torch.bfloat16 or not t.is_contiguous() or tuple(t.shape) != tuple(x.shape):
+                raise ValueError(f"moe_row_batch: {name} must be contiguous bfloat16 {tuple(x.shape)}")
+        if norm_w.dtype != torch.bfloat16 or not norm_w.is_contiguous() or norm_w.numel() != H:
+            raise ValueError(f"moe_row_batch: norm_w must be contiguous bfloat16 [{H}]")
     return MoeArgs(M, router_w.shape[0], H, ws.I, topk, ws.dtype, ptr(x), ptr(router_w), ptr(router_bias),
                    ptr(positions), *(ptr(t) for t in w), ptr(gate_w), ptr(out), ptr(ws.buf), ws.buf.numel(),
-                   ptr(dbg.get("acc13")), ptr(dbg.get("acc2")), ptr(dbg.get("h")))
+                   ptr(dbg.get("acc13")), ptr(dbg.get("acc2")), ptr(dbg.get("h")), ptr(resid), ptr(norm_w),
+                   float(eps), ptr(norm_out))
 
 
 def route(x, positions, router_w, topk: int, ws: Workspace, router_bias=None, stream=None):
@@ -205,13 +215,17 @@ def route(x, positions, router_w, topk: int, ws: Workspace, router_bias=None, st
 
 
 def moe_row_batch(x, positions, router_w, gate_w, ew: ExpertWeights, topk: int, ws: Workspace, out=None,
-                  router_bias=None, debug=None, stream=None):
-    """out[M, H] = shared_gate * shared_expert(x) + sum_j w_j * expert_{id_j}(x)  (bf16)."""
+                  router_bias=None, debug=None, stream=None, norm=None):
+    """out[M, H] = shared_gate * shared_expert(x) + sum_j w_j * expert_{id_j}(x)  (bf16).
+
+    norm = (resid, norm_w, eps, norm_out) fuses the next block's input add-norm into the combine:
+    resid <- bf16(out + resid) in place and norm_out = its Gemma RMSNorm, the same bits as
+    glue.add_rmsnorm(out, resid, norm_w, eps) after the block (L/qk_route.cu:630-820 combine_norm)."""
     if ew.E != router_w.shape[0] or ew.I != ws.I or ew.dtype != ws.dtype or ew.E != ws.E:
         raise ValueError("moe_row_batch: expert weights, router and workspace disagree on E / I / dtype")
     if out is None:
         out = torch.empty_like(x)
-    a = _args(x, positions, router_w, gate_w, ew, topk, ws, out, router_bias, debug)
+    a = _args(x, positions, router_w, gate_w, ew, topk, ws, out, router_bias, debug, norm)
     check(_lib.lib().q36_moe_forward(C.byref(a), _lib.stream_handle(stream)), "q36_moe_forward")
     return out
 

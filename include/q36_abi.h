@@ -95,6 +95,15 @@ typedef struct q36_moe_args {
   int32_t* dbg_acc13;
   int32_t* dbg_acc2;
   void* dbg_h;
+  /* Optional: the next block's input add-norm fused into the combine (the reference's combine_norm,
+   * L/qk_route.cu:630-820), when norm_out is not NULL: z = out + resid (fp32, out the bf16 combine
+   * result), resid <- bf16(z) in place, norm_out = bf16((z * rstd) * (1 + norm_w)) with rstd over z
+   * in q36_add_rmsnorm's order: the same bits as q36_add_rmsnorm(out, resid, norm_w) after the block.
+   * resid, norm_out bf16 [M, H]; norm_w bf16 [H]. */
+  void* resid;
+  const void* norm_w;
+  float norm_eps;
+  void* norm_out;
 } q36_moe_args;
 
 typedef struct q36_moe_ws_layout {

@@ -210,6 +210,37 @@ def test_moe_config2_fp8_stages(q36, oracle_mod, dev, seed):
     assert up[1] <= 2e-2 and dn[1] <= 2e-2, (up, dn)
 
 
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_moe_fused_add_norm(q36, oracle_mod, dev, dtype):
+    """The next block's add-norm fused into the combine gives the same bits as the block followed by
+    q36_add_rmsnorm: the block output, the updated residual and the normalised rows (padding rows
+    included), and matches the oracle's add-norm on the block output."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import glue
+    O = oracle_mod
+    M, E = 40, 64
+    d = synth.moe_inputs(M, dev, seed=21 + dtype, E=E, zipf=1.1)
+    ew = q36.prepare_experts(d["w13"], d["w2"], d["sw13"], d["sw2"], dtype)
+    ws = q36.Workspace(E, 2048, 512, 10, dtype, dev)
+    pos = torch.arange(1, M + 1, dtype=torch.int32, device=dev)
+    pos[3::7] = 0
+    g = synth.gen(dev, 77)
+    resid0 = synth.randn((M, 2048), g, dev)
+    nw = synth.randn((2048,), g, dev, 0.1)
+    ref = q36.moe_row_batch(d["x"], pos, d["router_w"], d["gate_w"], ew, 10, ws, router_bias=d["router_bias"])
+    r_ref = resid0.clone()
+    y_ref = glue.add_rmsnorm(ref, r_ref, nw, 1e-6)
+    r_got = resid0.clone()
+    y_got = torch.empty_like(resid0)
+    got = q36.moe_row_batch(d["x"], pos, d["router_w"], d["gate_w"], ew, 10, ws, router_bias=d["router_bias"],
+                            norm=(r_got, nw, 1e-6, y_got))
+    torch.cuda.synchronize()
+    for a, b, what in ((got, ref, "out"), (r_got, r_ref, "residual"), (y_got, y_ref, "normed rows")):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), what
+    hn, res = O.add_rmsnorm(bits16(got), bits16(resid0), bits16(nw), 1e-6)
+    assert np.array_equal(bits16(y_got), hn) and np.array_equal(bits16(r_got), res)
+
+
 def test_moe_repeat_deterministic(q36, dev):
     """Two calls on one workspace give identical bits (the self-resetting ticket, no races)."""
     from bundles_amd import synth
