@@ -117,8 +117,15 @@ __global__ __launch_bounds__(256) void proj_gemm_kernel(GemmDev g) {
   __shared__ __align__(16) float xs_l[NKB * TG];  // [NKB][TG], token fastest
   __shared__ float ws_l[4][NKB];                  // each wave's weight block scales
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
-  const int t0 = blockIdx.y * TG;
-  const int n0 = __builtin_amdgcn_readfirstlane(blockIdx.x * 64 * TPW + wave * 16 * TPW);  // the wave's tiles
+  // XCD-aware order: workgroup b runs on XCD b % 8, which owns the row blocks rb = xcd (mod 8) with
+  // every token group of each, so a weight tile is fetched into one L2 and its re-reads by the other
+  // token groups hit there
+  const int nrb = g.N / (64 * TPW), ntg = (g.T + TG - 1) / TG;
+  const int xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
+  const int rb = xcd + 8 * (jj / ntg);
+  if (rb >= nrb) return;
+  const int t0 = (jj % ntg) * TG;
+  const int n0 = __builtin_amdgcn_readfirstlane(rb * 64 * TPW + wave * 16 * TPW);  // the wave's tiles
   const int K = NKB * 128;
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(g.W + ((size_t)(n0 >> 4) * NKB << 11)), (short)0, TPW * NKB << 11, 0x00020000);
@@ -368,11 +375,11 @@ LinWs lin_ws(int T, int K) {
   return w;
 }
 
-// grid: (N / (64 TPW) row blocks, token groups of 16 NTT)
+// grid: the row blocks (N / (64 TPW), rounded up to a multiple of the 8 XCDs) x token groups of 16 NTT
 template <int NTT, int NKB, int PD, int TPW = 2>
 void launch_gemm(const GemmDev& g, hipStream_t st) {
-  const dim3 grid(g.N / (64 * TPW), (g.T + 16 * NTT - 1) / (16 * NTT));
-  proj_gemm_kernel<NTT, NKB, PD, TPW><<<grid, 256, 0, st>>>(g);
+  const int nrb = g.N / (64 * TPW), ntg = (g.T + 16 * NTT - 1) / (16 * NTT);
+  proj_gemm_kernel<NTT, NKB, PD, TPW><<<8 * ((nrb + 7) / 8) * ntg, 256, 0, st>>>(g);
 }
 
 // 8-bit codes (e4m3 or int8) [N, K] row-major -> fragment order; thread = one 16-byte chunk of the output
