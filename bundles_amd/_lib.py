@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "libq36.so")
 
 Q36_OK, Q36_EINVAL, Q36_ELAUNCH = 0, 1, 2
 Q36_MOE_INT8, Q36_MOE_FP8 = 0, 1
-Q36_LMH_W8A8, Q36_LMH_W8A8X2 = 0, 1
+Q36_LMH_W8A8, Q36_LMH_W8A8X2, Q36_LMH_W8A16 = 0, 1, 2
 
 P = C.c_void_p
 I32 = C.c_int32
@@ -79,6 +79,11 @@ class Fp8LinearArgs(C.Structure):
                 ("seg", LinearSeg * 4), ("workspace", P), ("workspace_bytes", SZ)]
 
 
+class Dense8LinearArgs(C.Structure):
+    _fields_ = [("T", I32), ("N", I32), ("K", I32), ("n_out", I32), ("x", P), ("q", P), ("s", P),
+                ("s_ld", C.c_int64), ("nseg", I32), ("seg", LinearSeg * 4)]
+
+
 class AddNormArgs(C.Structure):
     _fields_ = [("T", I32), ("H", I32), ("delta", P), ("residual", P), ("norm_w", P), ("eps", C.c_float), ("out", P)]
 
@@ -113,6 +118,7 @@ SYMBOLS = [
     ("q36_fp8_linear_workspace_bytes", SZ, [I32, I32]),
     ("q36_fp8_linear", I32, [C.POINTER(Fp8LinearArgs), P]),
     ("q36_add_rmsnorm", I32, [C.POINTER(AddNormArgs), P]),
+    ("q36_dense8_linear", I32, [C.POINTER(Dense8LinearArgs), P]),
     ("q36_attn_decode_workspace_bytes", SZ, [I32, I32]),
     ("q36_attn_decode", I32, [C.POINTER(DecodeArgs), P]),
     ("q36_lmhead_workspace_bytes", SZ, [I32]),

@@ -27,6 +27,7 @@
 
 #include "q36_device.h"
 #include "q36_host.h"
+#include "q36_w8a16.h"
 
 namespace q36 {
 namespace {
@@ -38,6 +39,7 @@ struct LmhDev {
   int R, V;
   int Rs;   // activation rows in xq: R (one term) or 64 * ceil(R / 32) (two terms, see act_row)
   int x2;   // two activation terms (Q36_LMH_W8A8X2)
+  int w16;  // W8A16: the prep writes the (normed) bf16 rows to xq instead of quantizing them
   const uint16_t* h;
   const uint16_t* norm_w;
   float eps;
@@ -90,6 +92,17 @@ __global__ __launch_bounds__(256) void lmh_prep_kernel(LmhDev d) {
         y[j][2 * q + 1] = rbf((y[j][2 * q + 1] * rstd) * (1.f + bf_hi((uint32_t)wv[q])));
       }
     }
+  }
+  if (d.w16) {  // W8A16: the bf16 rows themselves
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      v4i ov;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ov[q] = (int)pack_bf2(y[j][2 * q], y[j][2 * q + 1]);
+      *reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(d.xq) + (size_t)r * kLH + 8 * (lane + 64 * j)) = ov;
+    }
+    if (lane == 0) d.keys[r] = 0ull;
+    return;
   }
   // one int8 term per row; with two terms the second quantizes the residual y - q1 s1 (formed as
   // one fma) by the same rule, so y = q1 s1 + q2 s2 to within s2 / 2
@@ -445,7 +458,10 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
   Q36_REQUIRE(a->H == kLH, "q36_lmhead_argmax: H=%d unsupported (this build is specialised to 2048)", a->H);
   Q36_REQUIRE(a->R >= 1 && a->R <= (1 << 20), "q36_lmhead_argmax: R=%d out of range", a->R);
   Q36_REQUIRE(a->V >= 16 && a->V % 16 == 0, "q36_lmhead_argmax: V=%d must be a positive multiple of 16", a->V);
-  Q36_REQUIRE(a->mode == Q36_LMH_W8A8 || a->mode == Q36_LMH_W8A8X2, "q36_lmhead_argmax: mode %d unknown", a->mode);
+  Q36_REQUIRE(a->mode == Q36_LMH_W8A8 || a->mode == Q36_LMH_W8A8X2 || a->mode == Q36_LMH_W8A16,
+              "q36_lmhead_argmax: mode %d unknown", a->mode);
+  Q36_REQUIRE(a->mode != Q36_LMH_W8A16 || (a->R <= 64 && a->V % 32 == 0),
+              "q36_lmhead_argmax: the W8A16 form serves R <= 64 rows and V a multiple of 32 (R=%d V=%d)", a->R, a->V);
   Q36_REQUIRE(a->h && a->wq && a->ws && a->ids && a->workspace, "q36_lmhead_argmax: a required pointer is null");
   Q36_REQUIRE(aligned16(a->h) && aligned16(a->wq) && aligned16(a->ws) && aligned16(a->norm_w) &&
                   (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0,
@@ -454,13 +470,27 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
   Q36_REQUIRE(a->workspace_bytes >= L.total, "q36_lmhead_argmax: workspace of %zu bytes < %zu required",
               a->workspace_bytes, L.total);
   char* ws = static_cast<char*>(a->workspace);
-  const int x2 = a->mode == Q36_LMH_W8A8X2;
-  LmhDev d{a->R, a->V, act_rows(a->R, x2), x2, static_cast<const uint16_t*>(a->h), static_cast<const uint16_t*>(a->norm_w), a->eps,
+  const int x2 = a->mode == Q36_LMH_W8A8X2, w16 = a->mode == Q36_LMH_W8A16;
+  LmhDev d{a->R, a->V, act_rows(a->R, x2), x2, w16, static_cast<const uint16_t*>(a->h), static_cast<const uint16_t*>(a->norm_w), a->eps,
            static_cast<const int8_t*>(a->wq), a->ws, a->ids, static_cast<uint16_t*>(a->logits),
            reinterpret_cast<int8_t*>(ws + L.xq), reinterpret_cast<float*>(ws + L.xs),
            reinterpret_cast<unsigned long long*>(ws + L.keys)};
   hipStream_t st = static_cast<hipStream_t>(stream);
   lmh_prep_kernel<<<(a->R + 3) / 4, 256, 0, st>>>(d);
+  if (w16) {
+    W16Dev g{};
+    g.T = a->R;
+    g.N = a->V;
+    g.K = kLH;
+    g.x = reinterpret_cast<const uint16_t*>(d.xq);  // the prep's bf16 rows (2 R * H bytes fit in xq)
+    g.q = d.wq;
+    g.ws = d.ws;
+    g.logits = d.logits;
+    g.keys = d.keys;
+    launch_w8a16(g, 0, st);
+    lmh_ids_kernel<<<(a->R + 255) / 256, 256, 0, st>>>(d);
+    return check_launch("q36_lmhead_argmax");
+  }
   const int nvt = (a->V + kBN - 1) / kBN, nrt = (d.Rs + kBM - 1) / kBM;
   // persistent: one workgroup per CU (a multiple of 8, one XCD in eight), never more than the
   // busiest XCD's tiles

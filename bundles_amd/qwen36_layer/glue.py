@@ -1,5 +1,6 @@
 """The hybrid layer's glue on libq36: the e4m3 block-scaled linear with column-segmented outputs
-(q36_fp8_linear) and the fused residual add + Gemma RMSNorm (q36_add_rmsnorm).
+(q36_fp8_linear), the W8A16 linear on DENSE8 int8 copies (q36_dense8_linear) and the fused residual
+add + Gemma RMSNorm (q36_add_rmsnorm).
 
 Mirrors the reference's decode projections and add-norm (R = qwen36_nodes_kb34, L = R/qwen36_layer):
 gdn_in_proj / qkv_proj with their outputs split by column (L/qk_proj_decode.cu:409,434; the DENSE8
@@ -15,7 +16,7 @@ from dataclasses import dataclass
 import torch
 
 from .. import _lib
-from .._lib import AddNormArgs, Fp8LinearArgs, check, ptr
+from .._lib import AddNormArgs, Dense8LinearArgs, Fp8LinearArgs, check, ptr
 from .moe import pack_frag8, quantize_blocks_e4m3
 
 
@@ -76,20 +77,47 @@ def fp8_linear(x: torch.Tensor, w: Fp8Weight, ws: LinearWorkspace, segments=None
         segments, ret = [(0, out)], out
     else:
         ret = None
+    segs = _segments("fp8_linear", T, w.n, segments)
+    a = Fp8LinearArgs(T, w.qp.shape[0], K, w.n, ptr(x), ptr(w.qp), ptr(w.s), len(segments), segs,
+                      ptr(ws.buf), ws.buf.numel())
+    check(_lib.lib().q36_fp8_linear(C.byref(a), _lib.stream_handle(stream)), "q36_fp8_linear")
+    return ret
+
+
+def _segments(fn: str, T: int, n: int, segments):
     if not 1 <= len(segments) <= 4:
-        raise ValueError("fp8_linear: 1 to 4 segments")
+        raise ValueError(f"{fn}: 1 to 4 segments")
     end = 0
     segs = (_lib.LinearSeg * 4)()
     for i, (c0, o) in enumerate(segments):
         if c0 != end or o.dtype != torch.bfloat16 or o.shape[0] != T or o.stride(1) != 1:
-            raise ValueError(f"fp8_linear: segment {i} (col0 {c0}) must continue at column {end} as bf16 [T, w]")
+            raise ValueError(f"{fn}: segment {i} (col0 {c0}) must continue at column {end} as bf16 [T, w]")
         segs[i] = _lib.LinearSeg(c0, o.stride(0), o.data_ptr())
         end = c0 + o.shape[1]
-    if end != w.n:
-        raise ValueError(f"fp8_linear: segments cover {end} of {w.n} columns")
-    a = Fp8LinearArgs(T, w.qp.shape[0], K, w.n, ptr(x), ptr(w.qp), ptr(w.s), len(segments), segs,
-                      ptr(ws.buf), ws.buf.numel())
-    check(_lib.lib().q36_fp8_linear(C.byref(a), _lib.stream_handle(stream)), "q36_fp8_linear")
+    if end != n:
+        raise ValueError(f"{fn}: segments cover {end} of {n} columns")
+    return segs
+
+
+def dense8_linear(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, segments=None, stream=None):
+    """y = x . dequant(q, s)^T (bf16) on a DENSE8 copy (formats.quant_dense8: q int8 [N, K], s fp16
+    [K/128, >= N] group-major, possibly a column block of a wider buffer), x bf16 [T, K], T <= 64.
+    segments as fp8_linear's.  The reference's decode W8A16 projections (L/dense8.py:229-265)."""
+    T, K = x.shape
+    N = q.shape[0]
+    if x.dtype != torch.bfloat16 or not x.is_contiguous():
+        raise ValueError("dense8_linear: x must be contiguous bf16 [T, K]")
+    if (q.dtype != torch.int8 or not q.is_contiguous() or q.shape[1] != K or s.dtype != torch.float16
+            or s.dim() != 2 or s.shape[0] != K // 128 or s.shape[1] < N or s.stride(1) != 1):
+        raise ValueError(f"dense8_linear: the copy must be q int8 [N, {K}] and s fp16 [{K // 128}, >= N]")
+    if segments is None:
+        out = torch.empty((T, N), dtype=torch.bfloat16, device=x.device)
+        segments, ret = [(0, out)], out
+    else:
+        ret = None
+    segs = _segments("dense8_linear", T, N, segments)
+    a = Dense8LinearArgs(T, N, K, N, ptr(x), ptr(q), ptr(s), s.stride(0), len(segments), segs)
+    check(_lib.lib().q36_dense8_linear(C.byref(a), _lib.stream_handle(stream)), "q36_dense8_linear")
     return ret
 
 

@@ -2,7 +2,8 @@
 
 Mirrors the reference's lm_head glue (R = qwen36_nodes_kb34, H = R/qwen36_lmhead8):
   quantize_rows       <- H/lmhead8.py:111 (per-row int8, fp32 scale amax/127, round half away)
-  w8a8_lmhead_argmax  <- H/w8a8.py:116-120 w8a8_linear, with the greedy argmax of the stock sampler
+  w8a8_lmhead_argmax  <- H/w8a8.py:116-120 w8a8_linear (one or two activation terms) and
+                         H/lmhead8.py:57-91 (W8A16), with the greedy argmax of the stock sampler
                          (H/node.py:136-151) fused in; logits are returned only when asked for.
 """
 from __future__ import annotations
@@ -28,9 +29,10 @@ class Workspace:
 
 
 def w8a8_lmhead_argmax(h, q, scale, ws: Workspace, norm_w=None, eps: float = 1e-6, want_logits: bool = False,
-                       ids=None, stream=None, two_term: bool = False, logits=None):
+                       ids=None, stream=None, two_term: bool = False, logits=None, w8a16: bool = False):
     """h bf16 [R, 2048] -> ids int32 [R] (and bf16 logits [R, V] when want_logits, into `logits` when
-    given).  two_term: the reference's two-term activation form (H/w8a8.py:25-37)."""
+    given).  two_term: the reference's two-term activation form (H/w8a8.py:25-37); w8a16: the bf16
+    rows times the int8 weights unquantized (H/lmhead8.py:57-91; R <= 64, V a multiple of 32)."""
     R, H = h.shape
     V = q.shape[0]
     if R > ws.R_max:
@@ -45,6 +47,7 @@ def w8a8_lmhead_argmax(h, q, scale, ws: Workspace, norm_w=None, eps: float = 1e-
                                not logits.is_contiguous()):
         raise ValueError(f"w8a8_lmhead_argmax: logits must be contiguous bf16 [{R}, {V}]")
     a = LmheadArgs(R, H, V, ptr(h), ptr(norm_w), eps, ptr(q), ptr(scale), ptr(ids), ptr(logits), ptr(ws.buf),
-                   ws.buf.numel(), _lib.Q36_LMH_W8A8X2 if two_term else _lib.Q36_LMH_W8A8)
+                   ws.buf.numel(),
+                   _lib.Q36_LMH_W8A16 if w8a16 else _lib.Q36_LMH_W8A8X2 if two_term else _lib.Q36_LMH_W8A8)
     check(_lib.lib().q36_lmhead_argmax(C.byref(a), _lib.stream_handle(stream)), "q36_lmhead_argmax")
     return (ids, logits) if (want_logits or logits is not None) else ids

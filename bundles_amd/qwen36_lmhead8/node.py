@@ -12,11 +12,11 @@ Design:
   HeadCopy     the int8 copy of one served weight (codes + per-row fp32 scales, H/lmhead8.py:95-143),
                built on the first eligible call outside graph capture and rebuilt only when the served
                weight's storage, shape or version changes.
-  row policy   the arithmetic follows the reference's choice by row count (H/node.py:9-11,144-151),
-               within what this build has: at most MAX_TWO_TERM rows run the two-term W8A8 form
-               (H/w8a8.py:25-37; the reference's rule from 64 rows, and its nearest form below 64,
-               where it runs W8A16); more rows, up to MAX_ROWS, run the one-term W8A8 form (config 5's
-               int8 lm_head over 2048 rows; the reference hands more than 256 rows to a bf16 matmul).
+  row policy   the arithmetic follows the reference's choice by row count (H/node.py:9-11,144-151):
+               fewer than W8A16_BELOW rows run W8A16 (bf16 rows, int8 weights; H/lmhead8.py:57-91),
+               up to MAX_TWO_TERM rows the two-term W8A8 form (H/w8a8.py:25-37); more rows, up to
+               MAX_ROWS, run the one-term W8A8 form (config 5's int8 lm_head over 2048 rows; the
+               reference hands more than 256 rows to a bf16 matmul).
   greedy ids   the same launch finds each row's first largest logit; Int8Head keeps them on the node
                (last_ids) for a sampler that reads them instead of taking the argmax again.
 Heads the int8 path does not serve (no dense 2-D bf16 CUDA weight of width 2048, LoRA-wrapped heads, an
@@ -34,10 +34,13 @@ from . import lmhead8
 HIDDEN = 2048
 MAX_ROWS = 4096       # rows a call may carry on the int8 path (the workspace is sized once for this)
 MAX_TWO_TERM = 256    # row batches up to this size take the two-term activation form
+W8A16_BELOW = 64      # row batches below this size keep the activations in bf16
 
 
-def row_mode(rows: int) -> str:
-    """The activation form for a row batch of `rows` rows: 'two_term' or 'one_term'."""
+def row_mode(rows: int, vocab: int = 151936) -> str:
+    """The arithmetic for a row batch of `rows` rows: 'w8a16', 'two_term' or 'one_term'."""
+    if rows < W8A16_BELOW and vocab % 32 == 0:
+        return "w8a16"
     return "two_term" if rows <= MAX_TWO_TERM else "one_term"
 
 
@@ -106,8 +109,9 @@ class LogitsNode:
         ws = self.workspace_for(h.device) if hc is not None else None
         if ws is None:
             return None
+        mode = row_mode(h.shape[0], hc.q.shape[0])
         ids, logits = lmhead8.w8a8_lmhead_argmax(h.contiguous(), hc.q, hc.scale, ws, want_logits=True,
-                                                 two_term=row_mode(h.shape[0]) == "two_term")
+                                                 two_term=mode == "two_term", w8a16=mode == "w8a16")
         self.last_ids = ids
         return logits
 

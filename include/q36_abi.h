@@ -328,6 +328,24 @@ typedef struct q36_fp8_linear_args {
 size_t q36_fp8_linear_workspace_bytes(int32_t T, int32_t K);
 int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream);
 
+/* ---- DENSE8 W8A16 linear: the reference's decode projections on its int8 copies (dense8 seg / part,
+ * L/qk_proj_decode.cu:483-1102; L/dense8.py:229-401), for the verify row batches ----
+ * x bf16 [T, K] (1 <= T <= 64), q int8 [N, K] row-major, s fp16 [K/128][s_ld] group-major (the layout
+ * q36_quant_dense8 writes; s_ld >= N).  y[t, n] = bf16(acc), acc = fma(sum over the group's 128 columns of
+ * x * q (bf16 products, fp32 accumulation), s[g][n], acc) over the groups in order from zero.  Column
+ * segments as q36_fp8_linear's (col0, ld multiples of 4, outputs 8-byte aligned).  N % 32 == 0,
+ * K % 256 == 0.  No workspace. */
+typedef struct q36_dense8_linear_args {
+  int32_t T, N, K, n_out;
+  const void* x;
+  const void* q;
+  const void* s;
+  int64_t s_ld;
+  int32_t nseg;
+  q36_linear_seg seg[4];
+} q36_dense8_linear_args;
+int q36_dense8_linear(const q36_dense8_linear_args* a, q36_stream_t stream);
+
 /* ---- Fused residual add + Gemma RMSNorm between the hybrid layer's blocks: replaces the add-norm
  * of L/proj.py:60-81 (_add_norm_kernel) and the stock fused add-RMSNorm it reproduces ----
  * z = bf16 delta + residual in fp32 (delta NULL: z = residual); residual <- bf16(z) when delta is
@@ -385,9 +403,13 @@ int q36_attn_decode(const q36_decode_args* a, q36_stream_t stream);
  * (enough for every mode).
  * mode Q36_LMH_W8A8X2: two activation terms (H/w8a8.py:25-37 quantize_act two_term, the reference's
  * arithmetic from 64 rows): q1, s1 as above, then q2, s2 the same rule on the residual
- * fma(-q1, s1, y); logit = bf16(fma(acc1, s1, acc2 * s2) * ws) (H/w8a8.py:66-70). */
+ * fma(-q1, s1, y); logit = bf16(fma(acc1, s1, acc2 * s2) * ws) (H/w8a8.py:66-70).
+ * mode Q36_LMH_W8A16 (R <= 64, V % 32 == 0): the reference's arithmetic below 64 rows (H/lmhead8.py:57-91):
+ * the bf16 rows (normed when norm_w is given) times the int8 weights widened exactly to bf16, fp32
+ * accumulation, logit = bf16(acc * ws). */
 #define Q36_LMH_W8A8 0
 #define Q36_LMH_W8A8X2 1
+#define Q36_LMH_W8A16 2
 typedef struct q36_lmhead_args {
   int32_t R, H, V;
   const void* h;
@@ -399,7 +421,7 @@ typedef struct q36_lmhead_args {
   void* logits;
   void* workspace;
   size_t workspace_bytes;
-  int32_t mode; /* Q36_LMH_W8A8 or Q36_LMH_W8A8X2 */
+  int32_t mode; /* Q36_LMH_W8A8, Q36_LMH_W8A8X2 or Q36_LMH_W8A16 */
 } q36_lmhead_args;
 size_t q36_lmhead_workspace_bytes(int32_t R);
 int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream);

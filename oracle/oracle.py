@@ -108,6 +108,8 @@ def _declare(L):
     L.q36o_quant_blocks_e4m3.argtypes = [P, I32, I32, P, P]
     L.q36o_fp8_linear.restype = I32
     L.q36o_fp8_linear.argtypes = [I32, I32, I32, P, P, P, P, I32]
+    L.q36o_dense8_linear.restype = I32
+    L.q36o_dense8_linear.argtypes = [I32, I32, I32, P, P, P, C.c_int64, P, I32]
     L.q36o_add_rmsnorm.restype = I32
     L.q36o_add_rmsnorm.argtypes = [I32, I32, P, P, P, C.c_float, P]
     L.q36o_route.restype = I32
@@ -374,7 +376,21 @@ def attn_oproj(attn, gate, wo, so, n_threads=0):
 
 
 # ---------------------------------------------------------------- lm_head
-def lmhead(h, norm_w, eps, wq, ws, want_logits=False, n_threads=0, two_term=False):
+def dense8_linear(x, q, s, n_threads=0):
+    """x bf16 bits [T, K]; q int8 [N, K]; s fp16 bits (uint16) or float16 [K/128, >= N], group-major
+    (the layout quant_dense8 writes) -> bf16 bits [T, N]."""
+    x = np.ascontiguousarray(x, np.uint16)
+    q = np.ascontiguousarray(q, np.int8)
+    s = np.ascontiguousarray(s).view(np.uint16) if s.dtype == np.float16 else np.ascontiguousarray(s, np.uint16)
+    T, K = x.shape
+    N = q.shape[0]
+    out = np.empty((T, N), np.uint16)
+    if lib().q36o_dense8_linear(T, N, K, _p(x), _p(q), _p(s), C.c_int64(s.shape[1]), _p(out), n_threads):
+        raise ValueError("q36o_dense8_linear failed")
+    return out
+
+
+def lmhead(h, norm_w, eps, wq, ws, want_logits=False, n_threads=0, two_term=False, w8a16=False):
     h = np.ascontiguousarray(h, np.uint16)
     R, H = h.shape
     V = wq.shape[0]
@@ -383,7 +399,8 @@ def lmhead(h, norm_w, eps, wq, ws, want_logits=False, n_threads=0, two_term=Fals
     nw = None if norm_w is None else np.ascontiguousarray(norm_w, np.uint16)
     wq = np.ascontiguousarray(wq, np.int8)
     ws = np.ascontiguousarray(ws, np.float32)
-    a = LmheadArgs(R, H, V, _p(h), _p(nw), eps, _p(wq), _p(ws), _p(ids), _p(logits), n_threads, int(two_term))
+    a = LmheadArgs(R, H, V, _p(h), _p(nw), eps, _p(wq), _p(ws), _p(ids), _p(logits), n_threads,
+                   2 if w8a16 else int(two_term))
     if lib().q36o_lmhead(C.byref(a)):
         raise ValueError("q36o_lmhead failed")
     return ids, logits

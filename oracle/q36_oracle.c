@@ -955,6 +955,30 @@ int q36o_fp8_linear(int T, int N, int K, const uint16_t* x, const uint8_t* wq, c
   return 0;
 }
 
+int q36o_dense8_linear(int T, int N, int K, const uint16_t* x, const int8_t* q, const uint16_t* s, int64_t s_ld,
+                       uint16_t* out, int n_threads) {
+  if (K % 128 || T < 1 || N < 1 || s_ld < N) return -1;
+  if (n_threads > 0) omp_set_num_threads(n_threads);
+  float* xf = (float*)malloc(sizeof(float) * (size_t)T * K);
+  for (size_t i = 0; i < (size_t)T * K; ++i) xf[i] = q36o_bf16_to_f32(x[i]);
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; ++n) {
+    const int8_t* w = q + (size_t)n * K;
+    for (int t = 0; t < T; ++t) {
+      const float* xr = xf + (size_t)t * K;
+      float acc = 0.f;
+      for (int g = 0; g < K / 128; ++g) {
+        double dot = 0.0;
+        for (int i = 128 * g; i < 128 * g + 128; ++i) dot += (double)xr[i] * (double)w[i];
+        acc = fmaf((float)dot, q36o_f16_to_f32(s[(size_t)g * s_ld + n]), acc);
+      }
+      out[(size_t)t * N + n] = q36o_f32_to_bf16(acc);
+    }
+  }
+  free(xf);
+  return 0;
+}
+
 /* The add-norm between blocks (L/proj.py:60-81): z = bf16 delta + residual in fp32 (no delta:
  * z = residual); residual <- bf16(z) when delta is given; out = bf16((z * rstd) * (1 + w)),
  * rstd = 1 / sqrt(ss / H + eps), ss = q36o_dot_canon(z, z) (the kernel's fixed order). */
@@ -1057,9 +1081,45 @@ int q36o_attn_decode(const q36o_decode_args* a) {
  * (H/w8a8.py:16-23), acc = sum xq * wq (int32), logit = (acc * xs) * ws (H/w8a8.py:66-71), rounded
  * to bf16 (the node's output dtype), and the greedy id = the first index of the largest bf16
  * logit (torch.argmax order; the reference leaves argmax to the stock sampler, H/node.py:136-151). */
+/* W8A16 lm_head (H/lmhead8.py:57-91 _w8a16_kernel): logit = bf16(acc * ws[n]) with acc the sum of the
+ * bf16 row times the int8 weights (every product exact in fp32), taken exactly (double) and rounded
+ * once to fp32: the kernel sums in fp32 in its own order, so this form is the tolerance reference. */
+static int lmhead_w8a16(const q36o_lmhead_args* a) {
+  int R = a->R, H = a->H, V = a->V;
+  float* y = (float*)malloc(sizeof(float) * (size_t)R * H);
+  for (int r = 0; r < R; ++r) {
+    float* yr = y + (size_t)r * H;
+    for (int i = 0; i < H; ++i) yr[i] = q36o_bf16_to_f32(a->h[(size_t)r * H + i]);
+    if (a->norm_w) {
+      float ss = q36o_dot_canon(yr, yr, H);
+      float rstd = 1.f / sqrtf(ss / (float)H + a->eps);
+      for (int i = 0; i < H; ++i) yr[i] = bf((yr[i] * rstd) * (1.f + q36o_bf16_to_f32(a->norm_w[i])));
+    }
+  }
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int r = 0; r < R; ++r) {
+    const float* yr = y + (size_t)r * H;
+    float best = -INFINITY;
+    int bi = 0;
+    for (int n = 0; n < V; ++n) {
+      const int8_t* w = a->wq + (size_t)n * H;
+      double acc = 0.0;
+      for (int i = 0; i < H; ++i) acc += (double)yr[i] * (double)w[i];
+      float lg = bf((float)acc * a->ws[n]);
+      if (a->logits) a->logits[(size_t)r * V + n] = q36o_f32_to_bf16(lg);
+      if (lg > best) { best = lg; bi = n; }
+    }
+    a->ids[r] = bi;
+  }
+  free(y);
+  return 0;
+}
+
 int q36o_lmhead(const q36o_lmhead_args* a) {
   int R = a->R, H = a->H, V = a->V;
-  if (H % 512 || a->mode < 0 || a->mode > 1) return -1;
+  if (H % 512 || a->mode < 0 || a->mode > 2) return -1;
+  if (a->n_threads > 0) omp_set_num_threads(a->n_threads);
+  if (a->mode == 2) return lmhead_w8a16(a);
   const int two = a->mode == 1;
   if (a->n_threads > 0) omp_set_num_threads(a->n_threads);
   /* term u of row r at xq + (2 r + u) H (two terms) or r H (one term) */

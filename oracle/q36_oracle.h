@@ -197,9 +197,17 @@ typedef struct {
   int32_t* ids;             /* [R] */
   uint16_t* logits;         /* optional bf16 [R, V] */
   int n_threads;
-  int mode;                 /* 0: one int8 activation term; 1: two terms (H/w8a8.py:25-37) */
+  int mode;                 /* 0: one int8 activation term; 1: two terms (H/w8a8.py:25-37);
+                               2: W8A16, bf16 rows x int8 weights (H/lmhead8.py:57-91) */
 } q36o_lmhead_args;
 int q36o_lmhead(const q36o_lmhead_args* a);
+
+/* ---- DENSE8 W8A16 linear (L/dense8.py:1-28,229-401) ----
+ * x bf16 [T, K], q int8 [N, K], s fp16 bits [K/128][s_ld]: y[t, n] = bf16(acc), acc = fmaf(dot_g, s[g][n], acc)
+ * over the 128-column groups in order from zero, dot_g the exact sum of the group's products rounded once
+ * to fp32. */
+int q36o_dense8_linear(int T, int N, int K, const uint16_t* x, const int8_t* q, const uint16_t* s, int64_t s_ld,
+                       uint16_t* out, int n_threads);
 
 /* ---- decode / verify attention over an e4m3 KV cache ---- */
 typedef struct {

@@ -44,7 +44,8 @@ def test_struct_layouts_match_header(tmp_path):
                "q36_gdn_ring_args": _lib.GdnRingArgs,
                "q36_attn_args": _lib.AttnArgs, "q36_oproj_args": _lib.OprojArgs, "q36_lmhead_args": _lib.LmheadArgs,
                "q36_decode_args": _lib.DecodeArgs, "q36_linear_seg": _lib.LinearSeg,
-               "q36_fp8_linear_args": _lib.Fp8LinearArgs, "q36_add_norm_args": _lib.AddNormArgs}
+               "q36_fp8_linear_args": _lib.Fp8LinearArgs, "q36_add_norm_args": _lib.AddNormArgs,
+               "q36_dense8_linear_args": _lib.Dense8LinearArgs}
     hdr = open(HEADER).read()
     structs = {k: v for k, v in structs.items() if f"typedef struct {k}" in hdr}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]

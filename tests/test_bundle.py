@@ -97,3 +97,12 @@ def test_row_batch_rule():
         assert layer.row_batch(fb) is want
         assert layer.verify_batch(fb) is (name == "verify")
     assert not layer.row_batch(types.SimpleNamespace(positions=None)) and not layer.row_batch(None)
+
+
+def test_lmhead_row_policy():
+    """The lm_head arithmetic by row count (H/node.py:9-11,144-151): W8A16 below 64 rows (when the
+    vocabulary is a multiple of the W8A16 tile), two terms up to 256, one term above."""
+    from bundles_amd.qwen36_lmhead8 import node
+    assert [node.row_mode(r) for r in (1, 63, 64, 256, 257, 4096)] == \
+        ["w8a16", "w8a16", "two_term", "two_term", "one_term", "one_term"]
+    assert node.row_mode(8, vocab=4112) == "two_term"

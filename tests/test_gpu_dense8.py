@@ -1,0 +1,102 @@
+"""GPU parity of the W8A16 GEMM (libq36 through the C-ABI) against the CPU oracle: the DENSE8 linear
+(q36_dense8_linear) and the lm_head's W8A16 form (q36_lmhead_argmax, Q36_LMH_W8A16).
+
+Bar: the GPU sums the bf16 x int8 products (each exact in fp32) in fp32 in its MFMA order, the oracle
+sums each 128-column group exactly and rounds once, so outputs agree within the bf16 bar (worst row
+relative L2 error 4e-3, most elements bit-equal); the lm_head ids are each row's first largest GPU
+logit, and the logit they pick is within one bf16 step of the oracle's row maximum.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_bf16_close, bf16_f32, bits16, np_
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def mods():
+    from bundles_amd import _lib
+    _lib.lib()
+    from bundles_amd.qwen36_layer import formats, glue
+    from bundles_amd.qwen36_lmhead8 import lmhead8
+    return formats, glue, lmhead8
+
+
+def _copy(formats, N, K, dev, seed, s_pad=0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w = (torch.randn((N, K), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    wide = torch.zeros((K // 128, N + s_pad), dtype=torch.float16, device=dev)
+    q, s = formats.quant_dense8(w, s=wide[:, :N] if s_pad else None)
+    return q, (wide if s_pad else s)
+
+
+@pytest.mark.parametrize("T,N,K", [(1, 2048, 2048), (4, 12352, 2048), (16, 2048, 4096), (37, 4096, 2048),
+                                   (64, 12352, 2048), (64, 2048, 4096)])
+def test_dense8_linear_vs_oracle(mods, oracle_mod, dev, T, N, K):
+    formats, glue, _ = mods
+    print(f"dense8 linear T={T} N={N} K={K}", flush=True)
+    q, s = _copy(formats, N, K, dev, seed=T + N + K, s_pad=32 if T == 16 else 0)
+    x = torch.randn((T, K), generator=torch.Generator(device=dev).manual_seed(T), device=dev).to(torch.bfloat16)
+    y = glue.dense8_linear(x, q, s)
+    torch.cuda.synchronize()
+    ref = oracle_mod.dense8_linear(bits16(x), np_(q), np_(s).view(np.uint16))
+    worst, _, exact = assert_bf16_close(bits16(y), ref, 4e-3, "dense8 linear")
+    assert exact > 0.9, f"only {exact:.3f} of the outputs bit-equal"
+
+
+def test_dense8_linear_segments_gdn_in_proj(mods, oracle_mod, dev):
+    """The GDN in_proj split (8192 | 4096 | 32 | 32 columns) into strided views of one buffer."""
+    formats, glue, _ = mods
+    T, N, K = 24, 12352, 2048
+    q, s = _copy(formats, N, K, dev, seed=7)
+    x = torch.randn((T, K), generator=torch.Generator(device=dev).manual_seed(8), device=dev).to(torch.bfloat16)
+    big = torch.full((T, N + 64), -7.0, dtype=torch.bfloat16, device=dev)
+    cols = [0, 8192, 12288, 12320]
+    widths = [8192, 4096, 32, 32]
+    outs = [big[:, c + 16 * i:c + 16 * i + w_] for i, (c, w_) in enumerate(zip(cols, widths))]
+    glue.dense8_linear(x, q, s, segments=list(zip(cols, outs)))
+    whole = glue.dense8_linear(x, q, s)
+    torch.cuda.synchronize()
+    got = torch.cat(outs, dim=1)
+    assert torch.equal(got, whole), "segmented and whole outputs differ"
+    gaps = [big[:, c + 16 * i - 16:c + 16 * i] for i, c in enumerate(cols) if i]
+    assert all(torch.all(gp == -7.0) for gp in gaps), "a store landed outside its segment"
+    ref = oracle_mod.dense8_linear(bits16(x), np_(q), np_(s).view(np.uint16))
+    assert_bf16_close(bits16(whole), ref, 4e-3, "dense8 segments")
+
+
+def test_dense8_linear_rejects_bad_shapes(mods, dev):
+    formats, glue, _ = mods
+    q, s = _copy(formats, 64, 2048, dev, seed=1)
+    with pytest.raises(RuntimeError, match="T=65"):
+        glue.dense8_linear(torch.zeros((65, 2048), dtype=torch.bfloat16, device=dev), q, s)
+    with pytest.raises(ValueError):
+        glue.dense8_linear(torch.zeros((4, 1024), dtype=torch.bfloat16, device=dev), q, s)
+
+
+@pytest.mark.parametrize("R,V,norm", [(1, 4096, True), (16, 151936, True), (37, 8192, False), (64, 4096, True)])
+def test_lmhead_w8a16_vs_oracle(mods, oracle_mod, dev, R, V, norm):
+    from bundles_amd import synth
+    _, _, lmh = mods
+    print(f"lmhead W8A16 R={R} V={V} norm={norm}", flush=True)
+    d = synth.lmhead_inputs(R, V, dev, seed=R + V + 1)
+    q, s = lmh.quantize_rows(d["w"])
+    ws = lmh.Workspace(R, dev)
+    nw = d["norm_w"] if norm else None
+    ids, logits = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=nw, eps=1e-6, want_logits=True, w8a16=True)
+    torch.cuda.synchronize()
+    rid, rlog = oracle_mod.lmhead(bits16(d["h"]), bits16(nw) if norm else None, 1e-6, np_(q), np_(s),
+                                  want_logits=True, w8a16=True)
+    got = bits16(logits)
+    _, _, exact = assert_bf16_close(got, rlog, 4e-3, "W8A16 logits")
+    assert exact > 0.9, f"only {exact:.3f} of the logits bit-equal"
+    g = bf16_f32(got)
+    r = bf16_f32(rlog)
+    assert np.array_equal(np_(ids), np.argmax(g, axis=1)), "ids are not the first largest GPU logit"
+    rmax = r.max(axis=1)
+    picked = r[np.arange(R), np_(ids)]
+    assert np.all(rmax - picked <= np.abs(rmax) * 2 ** -7 + 1e-6), "an id's logit is below the oracle maximum"
+    agree = np.mean(np_(ids) == rid)
+    assert agree >= 0.9, f"ids agree on {agree:.2f} of the rows"

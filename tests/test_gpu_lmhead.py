@@ -1,7 +1,8 @@
 """GPU parity of the int8 lm_head + argmax (libq36 through the C-ABI) against the CPU oracle.
 
 Bar: int8 activations, logits (exact: int32 accumulation and two IEEE products; two terms: the int32
-accumulators of both terms, one fma and one product) and argmax ids bit-exact."""
+accumulators of both terms, one fma and one product) and argmax ids bit-exact.  The W8A16 form (fp32
+accumulation of exact products in the MFMA's order) is judged in test_gpu_dense8.py."""
 import numpy as np
 import pytest
 import torch

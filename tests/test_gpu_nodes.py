@@ -272,10 +272,10 @@ class _Processor(torch.nn.Module):
         return torch.matmul(hidden_states, lm_head.weight.T)
 
 
-@pytest.mark.parametrize("R", [8, 100, 300])
+@pytest.mark.parametrize("R", [8, 64, 100, 300])
 def test_lmhead_node_logits_and_ids(dev, R):
-    """The node's logits and greedy ids are the int8 path's: the two-term form up to 256 rows, one
-    term above; the served head is not modified."""
+    """The node's logits and greedy ids are the int8 path's: W8A16 below 64 rows, the two-term form up
+    to 256 rows, one term above; the served head is not modified."""
     from bundles_amd.qwen36_lmhead8 import lmhead8, node
     V = 4096
     g = torch.Generator(device=dev).manual_seed(3 + R)
@@ -287,7 +287,10 @@ def test_lmhead_node_logits_and_ids(dev, R):
     logits = node.forward(prepared, None, h, head)
     q, s = lmhead8.quantize_rows(head.weight.data)
     ws = lmhead8.Workspace(R, dev)
-    ids, ref = lmhead8.w8a8_lmhead_argmax(h, q, s, ws, want_logits=True, two_term=R <= node.MAX_TWO_TERM)
+    mode = node.row_mode(R, V)
+    assert mode == ("w8a16" if R < 64 else "two_term" if R <= 256 else "one_term")
+    ids, ref = lmhead8.w8a8_lmhead_argmax(h, q, s, ws, want_logits=True, two_term=mode == "two_term",
+                                          w8a16=mode == "w8a16")
     torch.cuda.synchronize()
     assert torch.equal(logits.view(torch.int16), ref.view(torch.int16))
     assert torch.equal(prepared.last_ids, ids)
