@@ -22,7 +22,7 @@ struct W16Dev {
   uint16_t* ys[4];
 };
 
-// T <= 64, N % 32 == 0, K % 256 == 0 (checked by the callers)
+// T <= 64, N % 32 == 0, K 2048 (mode 0) or 2048 / 4096 (mode 1), checked by the callers
 int launch_w8a16(const W16Dev& d, int mode, hipStream_t st);
 
 }  // namespace q36

@@ -4,17 +4,18 @@
 //     171-197; H/node.py:144-151): logit = bf16(acc * ws[row]) with one fp32 scale per vocab row, fused
 //     with the greedy argmax (q36_lmhead_argmax, mode Q36_LMH_W8A16);
 //   - the DENSE8 decode projections (L/dense8.py:1-28,229-401; the copy q36_quant_dense8 writes):
-//     one fp16 scale per (row, 128-column group), acc = fma(group dot, scale, acc) in group order,
-//     outputs bf16 split into column segments (q36_dense8_linear).
+//     one fp16 scale per (row, 128-column group), acc = fma(group dot, scale, acc) in group order
+//     within a K chunk, the chunks' sums added in order, outputs bf16 split into column segments
+//     (q36_dense8_linear).
 //
-// Layout of the work: a workgroup owns 128 weight rows, each of its four waves 32 (two 16-row MFMA
-// tiles), against every token (up to 64: NTT tiles of 16).  K advances 64 columns a step: lane l loads
+// Layout of the work: a wave owns 16 RT weight rows (RT 16-row MFMA tiles) over a chunk of K, against
+// every token (up to 64: NTT tiles of 16).  K advances 64 columns a step: lane l loads
 // 16 int8 of row l % 16 at column 64 s + 16 (l / 16) (four lanes cover 64 contiguous bytes of a row),
 // and the 16 bf16 of its token at the same columns; the low and high 8 of each feed two
 // v_mfma_f32_16x16x32_bf16 (the same column split on both operands, so every product is formed once).
 // int8 -> bf16 is exact: v_cvt_f32_i32 with a sign-extended byte select, then the high half of the f32.
-// The weights stream from HBM kDepth steps ahead in registers; the activations (a few hundred KB at
-// most) come from L2.  With the weights as the first operand a lane ends with token l % 16 and four
+// The weights stream from HBM kDepth steps ahead in registers, the activations (a few hundred KB at
+// most, read from L2) with them.  With the weights as the first operand a lane ends with token l % 16 and four
 // consecutive rows 4 (l / 16) .. + 3 of each tile.
 #include <hip/hip_fp16.h>
 
@@ -29,7 +30,6 @@ namespace {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
-constexpr int kRowsWG = 128;   // weight rows per workgroup
 constexpr int kDepth = 4;      // weight steps in flight per wave
 
 // 16 int8 (one v4i) -> two fragments of 8 bf16 (low 8 bytes, high 8 bytes)
@@ -59,77 +59,117 @@ __device__ __forceinline__ float round_bf16_w(float x) {
   return __builtin_bit_cast(float, __builtin_convertvector((v2f){0.f, x}, v2bf));
 }
 
-template <int NTT, int MODE>
-__global__ __launch_bounds__(256) void w8a16_kernel(W16Dev d) {
-  __shared__ uint32_t rkey[4][64];  // MODE 0: each wave's best key per token
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
-  const int r0 = blockIdx.x * kRowsWG + wave * 32;  // the wave's rows (N % 32 == 0: all in or all out)
+// One workgroup: WAVES waves in RG = WAVES / KS row groups of 16 RT rows; the KS waves of a row group
+// split K into KS contiguous chunks (a multiple of 128 columns each) and their fp32 partial sums meet in
+// LDS, added in chunk order by the first wave of the group, which runs the epilogue.
+template <int NTT, int RT, int KS, int WAVES, int MODE, int K>
+__global__ __launch_bounds__(64 * WAVES) void w8a16_kernel(W16Dev d) {
+  constexpr int RG = WAVES / KS;
+  constexpr int RW = 16 * RT;      // rows per wave
+  // steps in flight: weights, activations (and mode 1's group scales); four token tiles hold half as many
+  constexpr int D = NTT >= 4 ? kDepth / 2 : kDepth;
+  constexpr int NACC = RT * NTT * 4;
+  __shared__ float red[KS > 1 ? WAVES - RG : 1][KS > 1 ? NACC : 1][KS > 1 ? 64 : 1];
+  __shared__ uint32_t rkey[MODE == 0 ? RG : 1][64];
+  // the wave index through readfirstlane: uniform to the compiler, so the buffer descriptors built from
+  // it live in SGPRs (a descriptor in VGPRs turns every buffer load into a readfirstlane loop)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lr = lane & 15,
+            lg = lane >> 4;
+  const int ks = wave % KS, rg = wave / KS;
+  const int r0 = blockIdx.x * (RG * RW) + rg * RW;  // N % RW == 0: a wave's rows are all in or all out
   const bool active = r0 < d.N;
-  const int K = d.K, nsteps = K / 64;
-  // weights: row r0 + 16 rt + lr, bytes 64 s + 16 lg of it
+  // K is a template argument so the step loop unrolls completely: with a loop edge the compiler waits for
+  // every outstanding load at the top of each pass, which caps the loads in flight at one pass
+  constexpr int kc = K / KS, nsteps = kc / 64;
+  const int k0 = ks * kc;
+  // weights: row r0 + 16 rt + lr, bytes k0 + 64 s + 16 lg .. + 15 of it
   const int8_t* wrow = d.q + (size_t)(active ? r0 : 0) * K;
   const __amdgpu_buffer_rsrc_t wrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)wrow, (short)0, active ? 32 * K : 0, 0x00020000);
-  const int wv0 = lr * K + 16 * lg, wv1 = (16 + lr) * K + 16 * lg;
-  // activations: token 16 tt + lr (rows past T read as zero), elements 64 s + 16 lg .. + 15
+      __builtin_amdgcn_make_buffer_rsrc((void*)wrow, (short)0, active ? RW * K : 0, 0x00020000);
+  int wv[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) wv[rt] = (16 * rt + lr) * K + k0 + 16 * lg;
+  // activations: token 16 tt + lr (tokens past T read as zero), elements k0 + 64 s + 16 lg .. + 15
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)d.x, (short)0, d.T * K * 2, 0x00020000);
   int xv[NTT];
 #pragma unroll
   for (int tt = 0; tt < NTT; ++tt) {
     const int t = 16 * tt + lr;
-    xv[tt] = t < d.T ? (t * K + 16 * lg) * 2 : d.T * K * 2;
+    xv[tt] = t < d.T ? (t * K + k0 + 16 * lg) * 2 : d.T * K * 2;
   }
-  v4f acc[2][NTT], part[2][NTT];
+  v4f acc[RT][NTT], part[RT][NTT];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt) acc[rt][tt] = part[rt][tt] = v4f{0.f, 0.f, 0.f, 0.f};
-  v4i wq[kDepth][2];
   if (active) {
+    v4i wq[D][RT], xa[D][NTT], xb[D][NTT];
+    uint2 scl[D / 2][RT];  // mode 1: the fp16 scales of the group starting at an even step
+    // Loads are issued without a branch (a conditional load makes the compiler wait for every
+    // outstanding load at the join): a step past the chunk gets an offset past both descriptors' ranges,
+    // which returns zeros and moves no data.
+    auto issue = [&](int u, int s) {
+      const bool in = s < nsteps;
+      const int wo = in ? 64 * s : (1 << 30), xo = in ? 128 * s : (1 << 30);
 #pragma unroll
-    for (int s = 0; s < kDepth; ++s) {
-      wq[s][0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wv0, 64 * s, 2);
-      wq[s][1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wv1, 64 * s, 2);
-    }
-    for (int s0 = 0; s0 < nsteps; s0 += kDepth) {
+      for (int rt = 0; rt < RT; ++rt) wq[u][rt] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wv[rt], wo, 2);
 #pragma unroll
-      for (int u = 0; u < kDepth; ++u) {
+      for (int tt = 0; tt < NTT; ++tt) {
+        xa[u][tt] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv[tt], xo, 0);
+        xb[u][tt] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv[tt], xo + 16, 0);
+      }
+      if constexpr (MODE == 1) {
+        if (!(u & 1)) {
+          const int g = (k0 >> 7) + (min(s, nsteps - 2) >> 1);  // past the chunk: its last group again
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+            scl[u >> 1][rt] = *reinterpret_cast<const uint2*>(d.s16 + (size_t)g * d.s_ld + r0 + 16 * rt + 4 * lg);
+        }
+      }
+    };
+#pragma unroll
+    for (int u = 0; u < D; ++u) issue(u, u);
+    uint2 sc_cur[RT];  // mode 1: the current group's scales, taken at its first step before the refill
+#pragma unroll
+    for (int s0 = 0; s0 < nsteps; s0 += D) {
+#pragma unroll
+      for (int u = 0; u < D; ++u) {
         const int s = s0 + u;
-        v4i xa[NTT], xb[NTT];
+        v8bf alo[RT], ahi[RT], blo[NTT], bhi[NTT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) widen16(wq[u][rt], alo[rt], ahi[rt]);
 #pragma unroll
         for (int tt = 0; tt < NTT; ++tt) {
-          xa[tt] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv[tt], 128 * s, 0);
-          xb[tt] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv[tt], 128 * s + 16, 0);
-        }
-        v8bf alo[2], ahi[2];
-        widen16(wq[u][0], alo[0], ahi[0]);
-        widen16(wq[u][1], alo[1], ahi[1]);
-        if (s + kDepth < nsteps) {
-          wq[u][0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wv0, 64 * (s + kDepth), 2);
-          wq[u][1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wv1, 64 * (s + kDepth), 2);
-        }
-#pragma unroll
-        for (int tt = 0; tt < NTT; ++tt) {
-          const v8bf blo = __builtin_bit_cast(v8bf, xa[tt]), bhi = __builtin_bit_cast(v8bf, xb[tt]);
-#pragma unroll
-          for (int rt = 0; rt < 2; ++rt) {
-            v4f& p = MODE == 0 ? acc[rt][tt] : part[rt][tt];
-            p = mfma_bf16(alo[rt], blo, p);
-            p = mfma_bf16(ahi[rt], bhi, p);
-          }
+          blo[tt] = __builtin_bit_cast(v8bf, xa[u][tt]);
+          bhi[tt] = __builtin_bit_cast(v8bf, xb[u][tt]);
         }
         if constexpr (MODE == 1) {
-          // the end of a 128-column group: acc = fma(group dot, s16[group][row], acc), group dot reset
-          if (s & 1) {
-            const int g = s >> 1;
+          if (!(u & 1)) {
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-              const uint2 sv = *reinterpret_cast<const uint2*>(d.s16 + (size_t)g * d.s_ld + r0 + 16 * rt + 4 * lg);
-              const float sc[4] = {__half2float(__ushort_as_half((unsigned short)(sv.x & 0xffffu))),
-                                   __half2float(__ushort_as_half((unsigned short)(sv.x >> 16))),
-                                   __half2float(__ushort_as_half((unsigned short)(sv.y & 0xffffu))),
-                                   __half2float(__ushort_as_half((unsigned short)(sv.y >> 16)))};
+            for (int rt = 0; rt < RT; ++rt) sc_cur[rt] = scl[u >> 1][rt];
+          }
+        }
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            v4f& p = MODE == 0 ? acc[rt][tt] : part[rt][tt];
+            p = mfma_bf16(alo[rt], blo[tt], p);
+            p = mfma_bf16(ahi[rt], bhi[tt], p);
+          }
+        // the refill after the last read of the slot's registers, so the loads land in the same
+        // registers every iteration (no copies at the loop edge, which would wait for them)
+        issue(u, s + D);
+        if constexpr (MODE == 1) {
+          // the end of a 128-column group: acc = fma(group dot, s16[group][row], acc), group dot reset
+          if (u & 1) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+              const float sc[4] = {__half2float(__ushort_as_half((unsigned short)(sc_cur[rt].x & 0xffffu))),
+                                   __half2float(__ushort_as_half((unsigned short)(sc_cur[rt].x >> 16))),
+                                   __half2float(__ushort_as_half((unsigned short)(sc_cur[rt].y & 0xffffu))),
+                                   __half2float(__ushort_as_half((unsigned short)(sc_cur[rt].y >> 16)))};
 #pragma unroll
               for (int tt = 0; tt < NTT; ++tt) {
 #pragma unroll
@@ -143,6 +183,29 @@ __global__ __launch_bounds__(256) void w8a16_kernel(W16Dev d) {
       }
     }
   }
+  if constexpr (KS > 1) {
+    // partial sums of the later K chunks through LDS, added in chunk order
+    if (ks > 0) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) red[rg * (KS - 1) + ks - 1][(rt * NTT + tt) * 4 + i][lane] = acc[rt][tt][i];
+    }
+    __syncthreads();
+    if (ks == 0) {
+#pragma unroll
+      for (int j = 0; j < KS - 1; ++j)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+          for (int tt = 0; tt < NTT; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[rt][tt][i] += red[rg * (KS - 1) + j][(rt * NTT + tt) * 4 + i][lane];
+    }
+  }
+  const bool owner = active && ks == 0;  // the wave that finishes its row group
   if constexpr (MODE == 0) {
     // logit = bf16(acc * ws[row]); the first row of each token's largest logit in this workgroup
 #pragma unroll
@@ -150,9 +213,9 @@ __global__ __launch_bounds__(256) void w8a16_kernel(W16Dev d) {
       const int t = 16 * tt + lr;
       float bv = -__builtin_inff();
       int bi = 0;
-      if (active) {
+      if (owner) {
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
+        for (int rt = 0; rt < RT; ++rt) {
           const int rb = r0 + 16 * rt + 4 * lg;
           const float4 w4 = *reinterpret_cast<const float4*>(d.ws + rb);
           const float wsv[4] = {w4.x, w4.y, w4.z, w4.w};
@@ -160,7 +223,7 @@ __global__ __launch_bounds__(256) void w8a16_kernel(W16Dev d) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             lg4[i] = round_bf16_w(acc[rt][tt][i] * wsv[i]);
-            if (lg4[i] > bv) bv = lg4[i], bi = rb + i - blockIdx.x * kRowsWG;
+            if (lg4[i] > bv) bv = lg4[i], bi = rb + i - blockIdx.x * (RG * RW);
           }
           if (d.logits && t < d.T)
             *reinterpret_cast<uint2*>(d.logits + (size_t)t * d.N + rb) =
@@ -171,28 +234,30 @@ __global__ __launch_bounds__(256) void w8a16_kernel(W16Dev d) {
       // order-preserving bf16 key, first row on ties (the larger 0xffff - row)
       uint32_t b16 = __float_as_uint(bv + 0.f) >> 16;
       b16 = (b16 & 0x8000u) ? (~b16 & 0xffffu) : (b16 | 0x8000u);
-      uint32_t key = active ? ((b16 << 16) | (0xffffu - (uint32_t)bi)) : 0u;
+      uint32_t key = owner ? ((b16 << 16) | (0xffffu - (uint32_t)bi)) : 0u;
       key = max(key, (uint32_t)__shfl_xor((int)key, 16));
       key = max(key, (uint32_t)__shfl_xor((int)key, 32));
-      if (lg == 0) rkey[wave][16 * tt + lr] = key;
+      if (ks == 0 && lg == 0) rkey[rg][16 * tt + lr] = key;
     }
     __syncthreads();
     if (tid < 16 * NTT && tid < d.T) {
-      const uint32_t k = max(max(rkey[0][tid], rkey[1][tid]), max(rkey[2][tid], rkey[3][tid]));
+      uint32_t k = rkey[0][tid];
+#pragma unroll
+      for (int j = 1; j < RG; ++j) k = max(k, rkey[j][tid]);
       if (k != 0u) {
-        const uint32_t row = (uint32_t)(blockIdx.x * kRowsWG) + (0xffffu - (k & 0xffffu));
+        const uint32_t row = (uint32_t)(blockIdx.x * (RG * RW)) + (0xffffu - (k & 0xffffu));
         atomicMax(&d.keys[tid], ((unsigned long long)(k >> 16) << 32) | (unsigned long long)(0xffffffffu - row));
       }
     }
   } else {
-    if (!active) return;
+    if (!owner) return;
     // column segments (four columns never straddle a boundary: the boundaries are multiples of 4)
 #pragma unroll
     for (int tt = 0; tt < NTT; ++tt) {
       const int t = 16 * tt + lr;
       if (t >= d.T) continue;
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         const int col = r0 + 16 * rt + 4 * lg;
         if (col >= d.nout) continue;
         const int sg = (d.nseg > 1 && col >= d.c0[1]) + (d.nseg > 2 && col >= d.c0[2]) + (d.nseg > 3 && col >= d.c0[3]);
@@ -203,22 +268,60 @@ __global__ __launch_bounds__(256) void w8a16_kernel(W16Dev d) {
   }
 }
 
+// The launch shape: token tiles NTT (T <= 16 NTT), row tiles per wave RT, K split KS, waves per
+// workgroup WAVES.  Every shape the policy can pick is instantiated here.
+#define Q36_W16_SHAPES_0(X) X(1, 2, 1, 4) X(2, 2, 1, 4) X(4, 2, 1, 4)
+#define Q36_W16_SHAPES_1(X) \
+  X(1, 2, 4, 8) X(2, 2, 4, 8) X(4, 2, 4, 8) \
+  X(1, 1, 8, 8) X(2, 1, 8, 8) X(4, 1, 8, 8)
+
+struct W16Shape {
+  int ntt, rt, ks, waves;
+};
+
+// Measured on MI355X over T = 4..64: the lm_head (N in the 100 000s) streams whole rows, 32 a wave;
+// the projections split K so that every CU has waves: in quarters for the 9216- and 12352-row
+// in_proj / qkv, in eighths for the 2048-row o_proj / out_proj.
+W16Shape w16_shape(const W16Dev& d, int mode) {
+  const int ntt = d.T <= 16 ? 1 : d.T <= 32 ? 2 : 4;
+  if (mode == 0) return {ntt, 2, 1, 4};
+  return d.N >= 8192 ? W16Shape{ntt, 2, 4, 8} : W16Shape{ntt, 1, 8, 8};
+}
+
+template <int NTT, int RT, int KS, int WAVES, int MODE>
+void launch_shape(const W16Dev& d, hipStream_t st) {
+  constexpr int rows_wg = (WAVES / KS) * 16 * RT;
+  const int grid = (d.N + rows_wg - 1) / rows_wg;
+  if constexpr (MODE == 1) {
+    if (d.K == 4096) {
+      w8a16_kernel<NTT, RT, KS, WAVES, MODE, 4096><<<grid, 64 * WAVES, 0, st>>>(d);
+      return;
+    }
+  }
+  w8a16_kernel<NTT, RT, KS, WAVES, MODE, 2048><<<grid, 64 * WAVES, 0, st>>>(d);
+}
+
 template <int MODE>
-int launch_ntt(const W16Dev& d, hipStream_t st) {
-  const int grid = (d.N + kRowsWG - 1) / kRowsWG;
-  if (d.T <= 16)
-    w8a16_kernel<1, MODE><<<grid, 256, 0, st>>>(d);
-  else if (d.T <= 32)
-    w8a16_kernel<2, MODE><<<grid, 256, 0, st>>>(d);
-  else
-    w8a16_kernel<4, MODE><<<grid, 256, 0, st>>>(d);
-  return Q36_OK;
+int launch_mode(const W16Dev& d, hipStream_t st) {
+  const W16Shape s = w16_shape(d, MODE);
+#define Q36_W16_CASE(NTT, RT, KS, W)                                              \
+  if (s.ntt == NTT && s.rt == RT && s.ks == KS && s.waves == W) {                 \
+    launch_shape<NTT, RT, KS, W, MODE>(d, st);                                    \
+    return Q36_OK;                                                                \
+  }
+  if constexpr (MODE == 0) {
+    Q36_W16_SHAPES_0(Q36_W16_CASE)
+  } else {
+    Q36_W16_SHAPES_1(Q36_W16_CASE)
+  }
+#undef Q36_W16_CASE
+  return Q36_EINVAL;
 }
 
 }  // namespace
 
 int launch_w8a16(const W16Dev& d, int mode, hipStream_t st) {
-  return mode == 0 ? launch_ntt<0>(d, st) : launch_ntt<1>(d, st);
+  return mode == 0 ? launch_mode<0>(d, st) : launch_mode<1>(d, st);
 }
 
 }  // namespace q36
@@ -228,7 +331,7 @@ using namespace q36;
 extern "C" int q36_dense8_linear(const q36_dense8_linear_args* a, q36_stream_t stream) {
   Q36_REQUIRE(a != nullptr, "q36_dense8_linear: null args");
   Q36_REQUIRE(a->T >= 1 && a->T <= 64, "q36_dense8_linear: T=%d must be in [1, 64]", a->T);
-  Q36_REQUIRE(a->K >= 256 && a->K % 256 == 0 && a->K <= 8192, "q36_dense8_linear: K=%d must be a multiple of 256",
+  Q36_REQUIRE(a->K == 2048 || a->K == 4096, "q36_dense8_linear: K=%d must be 2048 or 4096 (the model's widths)",
               a->K);
   Q36_REQUIRE(a->N >= 32 && a->N % 32 == 0 && a->N <= (1 << 20), "q36_dense8_linear: N=%d must be a multiple of 32",
               a->N);

@@ -331,10 +331,11 @@ int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream);
 /* ---- DENSE8 W8A16 linear: the reference's decode projections on its int8 copies (dense8 seg / part,
  * L/qk_proj_decode.cu:483-1102; L/dense8.py:229-401), for the verify row batches ----
  * x bf16 [T, K] (1 <= T <= 64), q int8 [N, K] row-major, s fp16 [K/128][s_ld] group-major (the layout
- * q36_quant_dense8 writes; s_ld >= N).  y[t, n] = bf16(acc), acc = fma(sum over the group's 128 columns of
- * x * q (bf16 products, fp32 accumulation), s[g][n], acc) over the groups in order from zero.  Column
+ * q36_quant_dense8 writes; s_ld >= N).  y[t, n] = bf16(acc): within each of up to 8 K chunks,
+ * acc_c = fma(sum over the group's 128 columns of x * q (exact products, fp32 accumulation), s[g][n], acc_c)
+ * over the chunk's groups in order; acc = the chunk sums added in chunk order.  Column
  * segments as q36_fp8_linear's (col0, ld multiples of 4, outputs 8-byte aligned).  N % 32 == 0,
- * K % 256 == 0.  No workspace. */
+ * K is 2048 or 4096 (the model's projection widths).  No workspace. */
 typedef struct q36_dense8_linear_args {
   int32_t T, N, K, n_out;
   const void* x;
