@@ -252,17 +252,21 @@ def bench_attn(args, torch, dev):
         proj()
         oproj()
     torch.cuda.synchronize()
-    # as in the engine's captured verify step: one graph per projection, replayed
     ms_p = events_time(proj, args.steps, torch)
     ms_o = events_time(oproj, args.steps, torch)
+    # as in the engine's captured verify step: the calls inside one graph (no per-call graph launch),
+    # `inner` calls back to back, replayed
+    inner = 10
     gp, go = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.graph(gp):
-        proj()
+        for _ in range(inner):
+            proj()
     with torch.cuda.graph(go):
-        oproj()
+        for _ in range(inner):
+            oproj()
     torch.cuda.synchronize()
-    ms_pg = events_time(gp.replay, args.steps, torch)
-    ms_og = events_time(go.replay, args.steps, torch)
+    ms_pg = events_time(gp.replay, max(1, args.steps // inner), torch) / inner
+    ms_og = events_time(go.replay, max(1, args.steps // inner), torch) / inner
     wbytes = 9216 * 2048 + 72 * 16 * 4 + 2048 * 4096 + 16 * 32 * 4
     abytes = T * 2048 * 2 + T * (8192 + 1024) * 2 + T * 1024 + 2 * T * 4096 * 2 + T * 2048 * 2
     tot = wbytes + abytes
@@ -517,7 +521,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="moe,moe_high_u,gdn,gdn_ring,lmhead,attn,decode,hybrid",
-                    help="comma list of the nodes to run (the headline needs moe)")
+                    help="comma list of the nodes to run (the headline needs moe; without it the line "
+                         "carries the listed legs only)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 256 MiB device copy (the reference kernel for HBM counters)")
     args = ap.parse_args()
@@ -531,16 +536,17 @@ def main():
     _lib.lib()  # fails loudly when libq36.so is not built
     dev = torch.device("cuda:0")
     only = set(args.only.split(","))
-    print(f"bench: MoE fp8 batch 64, {COLD_LAYERS} layers cycled (cold), steps={args.steps} warmup={args.warmup}",
-          file=sys.stderr, flush=True)
-    moe_res = bench_moe(args, torch, dev, n_layers=COLD_LAYERS)
-    print(f"bench: MoE cold done ({moe_res['ms_graph'] * 1e3:.1f} us/layer)", file=sys.stderr, flush=True)
-    torch.cuda.empty_cache()
-    moe_warm = bench_moe(args, torch, dev, n_layers=1)
-    moe_warm.pop("_host")
-    print(f"bench: MoE warm done ({moe_warm['ms_graph'] * 1e3:.1f} us/layer)", file=sys.stderr, flush=True)
-    torch.cuda.empty_cache()
-    moe_hiu = None
+    moe_res = moe_warm = moe_hiu = None
+    if "moe" in only:
+        print(f"bench: MoE fp8 batch 64, {COLD_LAYERS} layers cycled (cold), steps={args.steps} "
+              f"warmup={args.warmup}", file=sys.stderr, flush=True)
+        moe_res = bench_moe(args, torch, dev, n_layers=COLD_LAYERS)
+        print(f"bench: MoE cold done ({moe_res['ms_graph'] * 1e3:.1f} us/layer)", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        moe_warm = bench_moe(args, torch, dev, n_layers=1)
+        moe_warm.pop("_host")
+        print(f"bench: MoE warm done ({moe_warm['ms_graph'] * 1e3:.1f} us/layer)", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
     if "moe_high_u" in only:
         moe_hiu = bench_moe(args, torch, dev, n_layers=2, zipf=None, seed0=100)
         moe_hiu.pop("_host")
@@ -580,6 +586,18 @@ def main():
         del src, dst
 
     cpu = cpu_legs = None
+    if moe_res is None:
+        # a run of single legs (--only without moe, e.g. under a profiler): no headline
+        line = {"metric": "per-leg run (no headline: --only without moe)", "value": None, "n_gpus": 1,
+                "legs": sorted(only)}
+        legs = {"lmhead": lmh_res, "attn": attn_res, "decode": dec_res, "hybrid": hyb_res, "gdn": gdn_res,
+                "gdn_ring": ring_res}
+        for k, v in legs.items():
+            if v is not None:
+                line[k] = {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()
+                           if isinstance(vv, (int, float, str))}
+        print(json.dumps(line), flush=True)
+        return
     if not args.no_cpu:
         print("bench: CPU oracle baselines", file=sys.stderr, flush=True)
         cpu, cpu_legs = cpu_baselines(moe_res, args.cpu_seconds)
@@ -635,7 +653,7 @@ def main():
             "bytes": attn_res["bytes"], "achieved_gbs": round(attn_res["gbs"], 1),
             "frac_hbm": round(attn_res["gbs"] / HBM_PEAK_GBS, 4),
             "workload": "128 tokens, e4m3 128x128-block qkv [9216,2048] + o_proj [2048,4096] (eager back-to-back "
-                        "launches; *_graph: one captured graph per call, replayed)"}
+                        "launches; *_graph: 10 calls captured in one graph, replayed, per call)"}
     if dec_res:
         line["attn_decode"] = {
             k: {"us_per_step": round(v["us_per_step"], 2), "bytes": v["bytes"], "achieved_gbs": round(v["gbs"], 1),

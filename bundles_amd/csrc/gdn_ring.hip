@@ -114,20 +114,31 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   reinterpret_cast<v4f*>(&xf[0][0][0])[tid] = v4f{0.f, 0.f, 0.f, 0.f};
   for (int i = tid; i < 16 * KW_STRIDE; i += 512) (&kw[16][0])[i] = 0.f;
 
-  // ---- requests, in two rounds.  Round one: every small operand (conv inputs, gate inputs, ring
-  // cursors, z, the norm weight), then a wait for all of it.  Round two: the committed ring entries
-  // and the checkpoint rows, consumed as they arrive.  Issuing the rows at once instead would put
-  // every workgroup's small loads behind the chip's 64 MB of rows in the memory queues: the conv
-  // would wait most of the stream.  Every load is unconditional (indices clamped into range, unused
-  // values selected away): a load under a branch makes the compiler wait for it at the join.
+  // ---- requests.  First every small operand (conv inputs, gate inputs, ring cursors, z, the norm
+  // weight, the committed ring entries by physical slot, so no address waits on the cursors), then
+  // the first checkpoint rows, then a wait for the small operands only.  Vector loads complete in
+  // issue order, so nothing the phases below need may be requested after a checkpoint row: a wait
+  // for it would wait for the rows too.  Every load is unconditional (indices clamped into range,
+  // unused values selected away): a load under a branch makes the compiler wait for it at the join.
   const int cur_wp = d.write_pos[rp], cur_cb = d.cache_base[rp];
-  // conv inputs, one channel per thread: q, k of key head hk, v of both value heads
+  // conv inputs, one channel per thread: q, k of key head hk, v of both value heads.  The unit's
+  // channels are three runs of the channel axis (q: 128, k: 128, v: 256); its conv state (3 bf16 a
+  // channel) is read as 192 16-byte pieces of those runs and handed out through LDS, and its window
+  // record and rolled state are written back the same way: a 2-byte access per lane and channel
+  // costs the CU's address unit a cycle per lane.
   const int ch = tid < 256 ? (tid >> 7) * (RHK * RK) + hk * RK + (tid & 127) : 2 * RHK * RK + hk * 2 * RV + (tid - 256);
-  uint16_t* cs = d.conv_state + slot * d.cs_slot + (int64_t)ch * 3;
+  // the 16-byte piece j of a per-channel array of `per` bf16: the run it falls in and its element offset
+  auto run_piece = [&](int j, int per, int64_t& elem) {
+    const int q8 = 128 * per / 8;  // pieces in the q run (and the k run); the v run has twice as many
+    const int run = j < q8 ? 0 : j < 2 * q8 ? 1 : 2;
+    const int base = run == 0 ? hk * RK : run == 1 ? RHK * RK + hk * RK : 2 * RHK * RK + hk * 2 * RV;
+    elem = (int64_t)base * per + 8 * (j - run * q8);
+  };
+  uint16_t* const cs_base = d.conv_state + slot * d.cs_slot;
+  int64_t cs_elem;
+  run_piece(min(tid, 191), 3, cs_elem);
+  const v4i csv = *reinterpret_cast<const v4i*>(cs_base + cs_elem);
   float w[TM + 3];
-  w[0] = bf2f(cs[0]);
-  w[1] = bf2f(cs[1]);
-  w[2] = bf2f(cs[2]);
 #pragma unroll
   for (int t = 0; t < TM; ++t) w[3 + t] = bf2f(d.mixed[(bos + min(t, T - 1)) * RQKV + ch]);
   const v2i cwr = *reinterpret_cast<const v2i*>(d.conv_w + (int64_t)ch * 4);
@@ -140,6 +151,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   // z: position tid >> 6 (rows past T read row T - 1), columns 4 (tid & 63) .. + 3 of the unit's 256
   const v2i zraw = *reinterpret_cast<const v2i*>(d.z + (bos + min(tid >> 6, T - 1)) * RZ + hk * 2 * RV + (tid & 63) * 4);
   const uint32_t nwraw = d.norm_w[tid & (RV - 1)];
+  // the committed ring entries by physical slot (placed in logical order, zero past the history, when
+  // they go to LDS) and gates
+  const int kc = tid >> 5, kcol = (tid & 31) * 4;  // keys: 16 slots x 32 x 4 columns
+  const v2i kraw = *reinterpret_cast<const v2i*>(d.k_ring + rp * d.k_slot + ((int64_t)hk * RL + kc) * RK + kcol);
+  const int dhd = tid >> 8, dc = (tid >> 4) & 15, dv = (tid & 15) * 8;  // d: 2 heads x 16 x 16 x 8
+  const v4i draw = *reinterpret_cast<const v4i*>(d.d_ring + rp * d.d_slot + ((int64_t)(2 * hk + dhd) * RL + dc) * RV + dv);
+  const float graw = d.g_ring[rp * d.g_slot + (2 * hk + ((tid >> 4) & 1)) * RL + (tid & 15)];
   // the checkpoint: wave w holds head w >> 2, rows 32 (w & 3) .. + 31 as two 16-row tiles; lane l
   // reads row l & 15 of a tile, columns 16 s + 4 (l >> 4) .. + 3 at step s.  Its 8 steps are
   // requested two at a time through the phases below (about 64 KB in flight a CU: enough to keep
@@ -158,20 +176,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     asm volatile("" ::: "memory");
   };
   request(0);
-  asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // the small operands (the 4 row requests may fly)
+  // The small operands have arrived (the 4 row requests may fly).  The wait comes from the compiler,
+  // through a use of each value: a hand-written wait is invisible to its accounting, which would then
+  // place its own wait for these values later, counted past the rows, and so wait for the rows.
+#pragma unroll
+  for (int i = 3; i < TM + 3; ++i) asm volatile("" ::"v"(w[i]));
+  asm volatile("" ::"v"(cwr), "v"(av), "v"(bv), "v"(dtw), "v"(alog), "v"(zraw), "v"(nwraw));
+  asm volatile("" ::"v"(kraw), "v"(draw), "v"(graw), "v"(csv));
+  // the unit's conv state through LDS (hx is free until the checkpoint dots): channel L = tid at
+  // elements 3 L .. 3 L + 2 of the staging run, in the order of the three runs
+  uint16_t* const stage = reinterpret_cast<uint16_t*>(&hx[0][0][0]);
+  if (tid < 192) *reinterpret_cast<v4i*>(stage + 8 * tid) = csv;
+  __syncthreads();
+  w[0] = bf2f(stage[3 * tid]);
+  w[1] = bf2f(stage[3 * tid + 1]);
+  w[2] = bf2f(stage[3 * tid + 2]);
   if ((tid >> 6) < T) *reinterpret_cast<v2i*>(&zs[tid >> 6][(tid & 63) * 4]) = zraw;
   if (tid < RV) nws[tid] = bf2f(nwraw);
   const int nv = min(max(__builtin_amdgcn_readfirstlane(cur_wp), 0), RL);
   const int cb = __builtin_amdgcn_readfirstlane(cur_cb);
-  // the committed ring entries (logical entry c of the key / d rows; entries past the history read
-  // entry 0's slot and are zeroed later) and gates
-  const int kc = tid >> 5, kcol = (tid & 31) * 4;  // keys: 16 entries x 32 x 4 columns
-  const v2i kraw = *reinterpret_cast<const v2i*>(d.k_ring + rp * d.k_slot +
-                                                 ((int64_t)hk * RL + ((cb + (kc < nv ? kc : 0)) & 15)) * RK + kcol);
-  const int dhd = tid >> 8, dc = (tid >> 4) & 15, dv = (tid & 15) * 8;  // d: 2 heads x 16 x 16 x 8
-  const v4i draw = *reinterpret_cast<const v4i*>(d.d_ring + rp * d.d_slot +
-                                                 ((int64_t)(2 * hk + dhd) * RL + ((cb + (dc < nv ? dc : 0)) & 15)) * RV + dv);
-  const float graw = d.g_ring[rp * d.g_slot + (2 * hk + ((tid >> 4) & 1)) * RL + ((cb + tid) & 15)];
 
   // ---- conv + SiLU (bf16 tap products, oldest first), the rolled state and the window record
   {
@@ -189,17 +212,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
         else vs[(tid - 256) >> 7][t][(tid - 256) & 127] = o;
       }
     }
-    uint16_t* rec = d.window + ws * d.win_slot + (int64_t)ch * (T + 2);
+    // the window record (T + 2 values a channel) into LDS after the conv state's 1536 elements;
+    // the rolled state over this channel's own three staged values (read above, by this thread only)
+    uint16_t* const rec = stage + 1536 + tid * (T + 2);
 #pragma unroll
     for (int i = 0; i < TM + 2; ++i)
       if (i < T + 2) rec[i] = (uint16_t)f2bf(w[1 + i]);
-    // this thread read its channel's state above and is its only reader: roll it in place
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
       float v = 0.f;
 #pragma unroll
       for (int t = 0; t < TM + 3; ++t) v = t == T + i ? w[t] : v;
-      cs[i] = (uint16_t)f2bf(v);
+      stage[3 * tid + i] = (uint16_t)f2bf(v);
     }
   }
   if (tid < 2 * T) {
@@ -218,18 +242,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
   }
   request(2);
   __syncthreads();
+  // the rolled conv state and the window record, 16 bytes a lane, from the staging runs
+  if (tid < 192) *reinterpret_cast<v4i*>(cs_base + cs_elem) = *reinterpret_cast<const v4i*>(stage + 8 * tid);
+  for (int j = tid; j < 64 * (T + 2); j += 512) {
+    int64_t we;
+    run_piece(j, T + 2, we);
+    *reinterpret_cast<v4i*>(d.window + ws * d.win_slot + we) = *reinterpret_cast<const v4i*>(stage + 1536 + 8 * j);
+  }
 
-  // ---- the committed entries into LDS: keys into key rows 0-15 (logical order, zero past the
-  // history), d entries (zero past the history), gates
+  // ---- the committed entries into LDS: physical slot p holds logical entry (p - cb) mod 16; keys
+  // into key rows 0-15 (logical order, zero past the history), d entries (zero past the history), gates
   {
-    const bool kon = kc < nv;
-    kw[kc][kcol] = kon ? bf_lo((uint32_t)kraw[0]) : 0.f;
-    kw[kc][kcol + 1] = kon ? bf_hi((uint32_t)kraw[0]) : 0.f;
-    kw[kc][kcol + 2] = kon ? bf_lo((uint32_t)kraw[1]) : 0.f;
-    kw[kc][kcol + 3] = kon ? bf_hi((uint32_t)kraw[1]) : 0.f;
+    const int lk = (kc - cb) & 15, ldc = (dc - cb) & 15;
+    const bool kon = lk < nv;
+    kw[lk][kcol] = kon ? bf_lo((uint32_t)kraw[0]) : 0.f;
+    kw[lk][kcol + 1] = kon ? bf_hi((uint32_t)kraw[0]) : 0.f;
+    kw[lk][kcol + 2] = kon ? bf_lo((uint32_t)kraw[1]) : 0.f;
+    kw[lk][kcol + 3] = kon ? bf_hi((uint32_t)kraw[1]) : 0.f;
     const v4i dz = {0, 0, 0, 0};
-    *reinterpret_cast<v4i*>(&dh[dhd][dc][dv]) = dc < nv ? draw : dz;
-    if (tid < 32) rg[tid >> 4][tid & 15] = graw;  // logical entry tid & 15
+    *reinterpret_cast<v4i*>(&dh[dhd][ldc][dv]) = ldc < nv ? draw : dz;
+    if (tid < 32) rg[tid >> 4][((tid & 15) - cb) & 15] = graw;
   }
   // ---- q/k unit vectors into the X fragments (q_t = vector t, k_t = vector 8 + t), the window keys
   // into key rows 16 + t; the window's key and gate appends (logical entries nv + t that fit)
@@ -402,7 +434,8 @@ extern "C" int q36_gdn_verify_ring(const q36_gdn_ring_args* a, q36_stream_t stre
               "q36_gdn_verify_ring: rows=%d slots=%d rslots=%d wslots=%d", a->rows, a->slots, a->rslots, a->wslots);
   Q36_REQUIRE(a->cs_slot >= RQKV * 3 && a->cs_slot % 8 == 0, "q36_gdn_verify_ring: conv_state slot stride %lld",
               (long long)a->cs_slot);
-  Q36_REQUIRE(a->win_slot >= (int64_t)RQKV * (a->T + 2), "q36_gdn_verify_ring: window slot stride %lld < 8192 x %d",
+  Q36_REQUIRE(a->win_slot >= (int64_t)RQKV * (a->T + 2) && a->win_slot % 8 == 0,
+              "q36_gdn_verify_ring: window slot stride %lld must be >= 8192 x %d and a multiple of 8",
               (long long)a->win_slot, a->T + 2);
   Q36_REQUIRE(a->d_slot >= RHV * RL * RV && a->dlo_slot >= RHV * RL * RV && a->d_slot % 8 == 0 && a->dlo_slot % 8 == 0,
               "q36_gdn_verify_ring: d ring slot strides must be >= 32 x 16 x 128 and multiples of 8");
@@ -410,10 +443,11 @@ extern "C" int q36_gdn_verify_ring(const q36_gdn_ring_args* a, q36_stream_t stre
               "q36_gdn_verify_ring: k ring slot strides must be >= 16 x 16 x 128 and multiples of 8");
   Q36_REQUIRE(a->g_slot >= RHV * RL && a->g_slot % 4 == 0, "q36_gdn_verify_ring: g ring slot stride %lld",
               (long long)a->g_slot);
-  Q36_REQUIRE(aligned16(a->h0) && aligned16(a->z) && aligned16(a->conv_state) && aligned16(a->conv_w) && aligned16(a->d_ring) &&
+  Q36_REQUIRE(aligned16(a->h0) && aligned16(a->z) && aligned16(a->conv_state) && aligned16(a->window) &&
+                  aligned16(a->conv_w) && aligned16(a->d_ring) &&
                   aligned16(a->dlo_ring) && aligned16(a->k_ring) && aligned16(a->klo_ring) && aligned16(a->g_ring) &&
                   aligned16(a->out),
-              "q36_gdn_verify_ring: h0, z, conv_state, conv_w, the rings and out must be 16-byte aligned");
+              "q36_gdn_verify_ring: h0, z, conv_state, window, conv_w, the rings and out must be 16-byte aligned");
   Q36_REQUIRE((reinterpret_cast<uintptr_t>(a->dt_bias) & 3) == 0, "q36_gdn_verify_ring: dt_bias must be 4-byte aligned");
   GdnRingDev d{a->B, a->T, a->rows, a->slots, a->rslots, a->wslots,
                static_cast<const uint16_t*>(a->mixed), static_cast<const uint16_t*>(a->z),

@@ -211,8 +211,8 @@ int q36_gdn_verify(const q36_gdn_args* a, q36_stream_t stream);
  *                 n + t < 16, each bf16 value split into high and low parts.
  *   dt_bias fp32 (dt_f32 = 1) or bf16 [32]; A_log fp32 [32]; norm_w bf16 [128]; scale: the q
  *                 scale (128^-1/2 for this model)
- * 1 <= T <= 8; h0, z, conv_state, conv_w, the rings and out 16-byte aligned, the slot strides
- * multiples of 16 bytes.  Requests must name distinct slots (they write them).  B = 0 launches
+ * 1 <= T <= 8; h0, z, conv_state, window, conv_w, the rings and out 16-byte aligned, the slot
+ * strides multiples of 16 bytes.  Requests must name distinct slots (they write them).  B = 0 launches
  * nothing. */
 typedef struct q36_gdn_ring_args {
   int32_t B, T, rows;
