@@ -261,7 +261,31 @@ __device__ __forceinline__ float key_logit(uint32_t key) {
   return __uint_as_float(b << 16);
 }
 
-// softmax / top-k / renormalise (L/i8x_decode.py:98-117)
+// Sorts the NM keys of a lane into descending order (bitonic network, NM a power of two).
+template <int NM>
+__device__ __forceinline__ void sort_desc(uint32_t* key) {
+#pragma unroll
+  for (int k2 = 2; k2 <= NM; k2 <<= 1)
+#pragma unroll
+    for (int j = k2 >> 1; j > 0; j >>= 1)
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint32_t hi = max(key[i], key[l]), lo = min(key[i], key[l]);
+          const bool desc = (i & k2) == 0;
+          key[i] = desc ? hi : lo;
+          key[l] = desc ? lo : hi;
+        }
+      }
+}
+
+// softmax / top-k / renormalise (L/i8x_decode.py:98-117).  One wave per token; lane l holds the
+// experts l + 64 m (NM = E / 64 keys, padded with zero keys to a power of two), sorted descending
+// in the lane, so each of the k picks is one wave max over the lanes' heads and a shift in the
+// winning lane.  The weights keep the oracle's arithmetic: p_j = exp(v_j - v_0) / sum in lane j,
+// their total added in pick order.
+template <int NM>
 __global__ __launch_bounds__(256) void route_topk_kernel(MoeDev d) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + wave;
@@ -275,49 +299,35 @@ __global__ __launch_bounds__(256) void route_topk_kernel(MoeDev d) {
     }
     return;
   }
-  float lg[16];
-  uint32_t key[16];
+  float lg[NM];
+  uint32_t key[NM];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) lg[m] = d.logits[(size_t)t * E + lane + 64 * (m < nm ? m : nm - 1)];
+  for (int m = 0; m < NM; ++m) lg[m] = d.logits[(size_t)t * E + lane + 64 * (m < nm ? m : nm - 1)];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) key[m] = m < nm ? logit_key(lg[m], lane + 64 * m) : 0u;
-  float mx = 0.f, vj[16];
-  int idj[16];
+  for (int m = 0; m < NM; ++m) key[m] = m < nm ? logit_key(lg[m], lane + 64 * m) : 0u;
+  sort_desc<NM>(key);
+  float mx = 0.f, my_v = 0.f;
+  int my_id = -1;
+  for (int j = 0; j < k; ++j) {  // k is uniform
+    const uint32_t win = wave_max_u32(key[0]);
+    const float v = key_logit(win);
+    if (j == 0) mx = v;
+    my_v = lane == j ? v : my_v;
+    my_id = lane == j ? (int)(0xffffu - (win & 0xffffu)) : my_id;
+    // keys are distinct: one lane pops its head (a bit select per key, no index arithmetic)
+    const uint32_t pop = key[0] == win ? 0xffffffffu : 0u;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    if (j < k) {
-      uint32_t lb = 0u;
-#pragma unroll
-      for (int m = 0; m < 16; ++m) lb = max(lb, key[m]);
-      const uint32_t win = wave_max_u32(lb);
-      const int id = (int)(0xffffu - (win & 0xffffu));
-      const float v = key_logit(win);
-      if (j == 0) mx = v;
-      vj[j] = v;
-      idj[j] = id;
-#pragma unroll
-      for (int m = 0; m < 16; ++m)
-        if (lane + 64 * m == id) key[m] = 0u;
-    }
+    for (int i = 0; i + 1 < NM; ++i) key[i] = (key[i + 1] & pop) | (key[i] & ~pop);
+    key[NM - 1] &= ~pop;
   }
   float part = 0.f;
 #pragma unroll
-  for (int m = 0; m < 16; ++m)
+  for (int m = 0; m < NM; ++m)
     if (m < nm) part = part + expf_q(lg[m] - mx);
   const float sum = wave_sum_bfly(part);
-  float wsum = 0.f, my_p = 0.f;
-  int my_id = -1;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    if (j < k) {
-      const float p = expf_q(vj[j] - mx) / sum;
-      wsum = wsum + p;
-      if (lane == j) {
-        my_p = p;
-        my_id = idj[j];
-      }
-    }
-  }
+  const float my_p = lane < k ? expf_q(my_v - mx) / sum : 0.f;
+  float wsum = 0.f;
+  for (int j = 0; j < k; ++j) wsum = wsum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_p), j));
   const float div = wsum > 0.f ? wsum : 1.f;
   if (lane < k) {
     d.ids[t * k + lane] = my_id;
@@ -1246,7 +1256,10 @@ int launch_route(const MoeDev& d, int dtype, hipStream_t st) {
     route_logits_kernel<Q36_MOE_FP8><<<n_router + d.M, 256, 0, st>>>(d, n_router);
   else
     route_logits_kernel<Q36_MOE_INT8><<<n_router + d.M, 256, 0, st>>>(d, n_router);
-  route_topk_kernel<<<(d.M + 3) / 4, 256, 0, st>>>(d);
+  if (d.E <= 512)
+    route_topk_kernel<8><<<(d.M + 3) / 4, 256, 0, st>>>(d);
+  else
+    route_topk_kernel<16><<<(d.M + 3) / 4, 256, 0, st>>>(d);
   return check_launch("q36_moe_route");
 }
 int launch_lists(const MoeDev& d, hipStream_t st) {
