@@ -34,6 +34,7 @@ namespace {
 
 constexpr int kLH = 2048;       // hidden (K)
 constexpr int kBM = 256, kBN = 256, kBK = 64, kNK = kLH / kBK;  // 32 K steps
+constexpr int kLmhWaves = 8;  // waves of the GEMM workgroup: two a SIMD
 
 struct LmhDev {
   int R, V;
@@ -175,8 +176,15 @@ __device__ __forceinline__ void wait_vm() {
 // row groups of XCDs (see lmh_gemm_body): two when there are at least 4 row tiles, evenly split
 __host__ __device__ __forceinline__ int lmh_groups(int nrt) { return nrt >= 4 && nrt % 2 == 0 ? 2 : 1; }
 
-template <bool STORE, bool X2>
+template <bool STORE, bool X2, int NW>
 __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
+  // NW waves: two vocab halves (wn) x NW / 2 token groups (wm); a wave owns 128 vocab columns (VB = 4
+  // blocks of 32) x TW tokens (TB blocks of 32)
+  constexpr int WM = NW / 2, TW = kBM / WM, TB = TW / 32, VB = 4;
+  constexpr int CPW = 16 / NW;            // 1 KB chunk pairs (A and B) a wave loads per step
+  constexpr int LPS = 2 * CPW;            // its loads per step
+  constexpr int NRD = 2 * TB + 2 * VB;    // its fragment reads per step
+  constexpr int NMF = 2 * TB * VB;        // its MFMAs per step
   // one object per LDS stage: the compiler tracks the buffer-to-LDS loads of each object apart
   __shared__ __align__(1024) int8_t a_s0[kBM * kBK], a_s1[kBM * kBK], a_s2[kBM * kBK], a_s3[kBM * kBK];
   __shared__ __align__(1024) int8_t b_s0[kBN * kBK], b_s1[kBN * kBK], b_s2[kBN * kBK], b_s3[kBN * kBK];
@@ -202,9 +210,9 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   int j = loc;
   if (vt_of(j) >= nvt) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2 waves of 128 x 128
+  const int wm = wave >> 1, wn = wave & 1;  // token group, vocab half
   const int wv = __builtin_amdgcn_readfirstlane(wave);
-  // Load i of wave w fills 1 KB chunk q = 4 w + i of a stage (tile rows 16 q .. 16 q + 15); lane l
+  // Load i of wave w fills 1 KB chunk q = CPW w + i of a stage (tile rows 16 q .. 16 q + 15); lane l
   // writes bytes 16 l .. 16 l + 15 of the chunk, which bswz assigns to row 16 q + l / 4, logical
   // 16-byte chunk (l % 4) ^ ((l / 8) % 4) ^ (l / 32).  Rows past R or V read as zero (buffer bounds).
   const int voff = (lane >> 2) * kLH + (((lane & 3) ^ ((lane >> 3) & 3) ^ (lane >> 5)) << 4);
@@ -224,18 +232,20 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   };
   // The row offset rides in the VGPR offset, the K offset in the SGPR offset: the buffer range
   // check covers only the former, so rows past the tile's last valid row read zero.
-  const int vrow[4] = {voff + (4 * wv) * 16 * kLH, voff + (4 * wv + 1) * 16 * kLH,
-                       voff + (4 * wv + 2) * 16 * kLH, voff + (4 * wv + 3) * 16 * kLH};
+  int vrow[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) vrow[i] = voff + (CPW * wv + i) * 16 * kLH;
   // Both operands with the default cache policy: the four workgroups of a row group read each weight
   // line in turn, and a streaming hint on the weights (measured) lets lines go before the last reader.
   auto issue_to = [&](const Tile& t, int ks, int8_t* as, int8_t* bs, int i) {
-    const int q = wv * 4 + i;
+    const int q = wv * CPW + i;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(t.a, as + q * 1024, 16, vrow[i], ks * kBK, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(t.b, bs + q * 1024, 16, vrow[i], ks * kBK, 0, 0);
   };
   auto issue_step = [&](const Tile& t, int ks, auto st, int i) { issue_to(t, ks, a_st(st), b_st(st), i); };
-  // the tile's weight and row scales (wave w: entries 64 w .. 64 w + 63 of each; past V or R: zero)
+  // the tile's weight and row scales (wave w < 4: entries 64 w .. 64 w + 63 of each; past V or R: zero)
   auto issue_scales = [&](const Tile& t, int par) {
+    if (wv >= 4) return;
     const __amdgpu_buffer_rsrc_t ws = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(d.ws + t.v0), (short)0, min(d.V - t.v0, kBN) * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(
@@ -247,21 +257,25 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   // (LDS chunk 2 h + l / 32); the MFMA gives lane l token l % 32 and vocab rows
   // 8 (j / 4) + 4 (l / 32) + j % 4 of register j.
   const int l32 = lane & 31, lh = lane >> 5;
-  const int fx0 = bswz(wm * 128 + l32, lh), fx1 = bswz(wm * 128 + l32, 2 + lh);  // + 32 kBK per t
+  const int fx0 = bswz(wm * TW + l32, lh), fx1 = bswz(wm * TW + l32, 2 + lh);  // + 32 kBK per t
   const int fw0 = bswz(wn * 128 + l32, lh), fw1 = bswz(wn * 128 + l32, 2 + lh);
-  v16i acc[4][4];     // [vocab block][token block]
-  v4i fx[2][2][4], fw[2][2][4];  // [register set][half step][block]
-  auto read_one = [&](auto st, auto fb, int k) {  // fragment k (0..15) of a step
+  v16i acc[VB][TB];     // [vocab block][token block]
+  v4i fx[2][2][TB], fw[2][2][VB];  // [register set][half step][block]
+  auto read_one = [&](auto st, auto fb, int k) {  // fragment k (0..NRD-1) of a step
     const int8_t* as = a_st(st);
     const int8_t* bs = b_st(st);
     constexpr int f = decltype(fb)::value;
-    const int h = (k >> 2) & 1, t = k & 3;
-    if (k < 8) fx[f][h][t] = *reinterpret_cast<const v4i*>(as + (h ? fx1 : fx0) + t * 32 * kBK);
-    else fw[f][h][t] = *reinterpret_cast<const v4i*>(bs + (h ? fw1 : fw0) + t * 32 * kBK);
+    if (k < 2 * TB) {
+      const int h = k / TB, t = k % TB;
+      fx[f][h][t] = *reinterpret_cast<const v4i*>(as + (h ? fx1 : fx0) + t * 32 * kBK);
+    } else {
+      const int h = (k - 2 * TB) / VB, t = (k - 2 * TB) % VB;
+      fw[f][h][t] = *reinterpret_cast<const v4i*>(bs + (h ? fw1 : fw0) + t * 32 * kBK);
+    }
   };
-  auto mfma_one = [&](auto fb, auto first, int k) {  // MFMA k (0..31) of a step
+  auto mfma_one = [&](auto fb, auto first, int k) {  // MFMA k (0..NMF-1) of a step
     constexpr int f = decltype(fb)::value;
-    const int h = k >> 4, vi = (k >> 2) & 3, ti = k & 3;
+    const int h = k / (VB * TB), vi = (k / TB) % VB, ti = k % TB;
     acc[vi][ti] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
         fw[f][h][vi], fx[f][h][ti], (decltype(first)::value && h == 0) ? v16i{} : acc[vi][ti], 0, 0, 0);
   };
@@ -276,44 +290,49 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     using nb = ic<1 - decltype(fb)::value>;
     using nst = ic<(decltype(cur)::value + 1) & 3>;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
+    for (int k = 0; k < NMF; ++k) {
       mfma_one(fb, first, k);
       if constexpr (decltype(next)::value)
-        if (k < 16) read_one(nst{}, nb{}, k);
+        if (k < NRD) read_one(nst{}, nb{}, k);
       if constexpr (decltype(loads)::value)
-        if (k >= 16 && k < 20) issue_step(t, ks + 4, cur, k - 16);
+        if (k >= NMF / 2 && k < NMF / 2 + CPW) issue_step(t, ks + 4, cur, k - NMF / 2);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
   int par = 0;
   Tile t = tile(j);
   issue_scales(t, 0);
-  issue_step(t, 0, ic<0>{}, 0), issue_step(t, 0, ic<0>{}, 1), issue_step(t, 0, ic<0>{}, 2), issue_step(t, 0, ic<0>{}, 3);
-  issue_step(t, 1, ic<1>{}, 0), issue_step(t, 1, ic<1>{}, 1), issue_step(t, 1, ic<1>{}, 2), issue_step(t, 1, ic<1>{}, 3);
-  issue_step(t, 2, ic<2>{}, 0), issue_step(t, 2, ic<2>{}, 1), issue_step(t, 2, ic<2>{}, 2), issue_step(t, 2, ic<2>{}, 3);
-  issue_step(t, 3, ic<3>{}, 0), issue_step(t, 3, ic<3>{}, 1), issue_step(t, 3, ic<3>{}, 2), issue_step(t, 3, ic<3>{}, 3);
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) issue_step(t, 0, ic<0>{}, i);
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) issue_step(t, 1, ic<1>{}, i);
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) issue_step(t, 2, ic<2>{}, i);
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) issue_step(t, 3, ic<3>{}, i);
   using T_ = std::true_type;
   using F_ = std::false_type;
   for (;;) {
     // the scales and step 0 of this tile: the oldest loads in flight (the epilogue's row atomics,
-    // issued after them, may finish first, hence 23 rather than 24)
-    if constexpr (STORE) wait_vm<0>(); else wait_vm<23>();
+    // issued after them, may finish first, hence one fewer than the three later steps' loads)
+    if constexpr (STORE) wait_vm<0>(); else wait_vm<3 * LPS - 1>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int k = 0; k < 16; ++k) read_one(ic<0>{}, ic<0>{}, k);
-    step(t, 0, ic<0>{}, ic<0>{}, T_{}, ic<16>{}, T_{}, T_{});
-    step(t, 1, ic<1>{}, ic<1>{}, F_{}, ic<16>{}, T_{}, T_{});
-    step(t, 2, ic<2>{}, ic<0>{}, F_{}, ic<16>{}, T_{}, T_{});
-    step(t, 3, ic<3>{}, ic<1>{}, F_{}, ic<16>{}, T_{}, T_{});
+    for (int k = 0; k < NRD; ++k) read_one(ic<0>{}, ic<0>{}, k);
+    using W2 = ic<2 * LPS>;
+    step(t, 0, ic<0>{}, ic<0>{}, T_{}, W2{}, T_{}, T_{});
+    step(t, 1, ic<1>{}, ic<1>{}, F_{}, W2{}, T_{}, T_{});
+    step(t, 2, ic<2>{}, ic<0>{}, F_{}, W2{}, T_{}, T_{});
+    step(t, 3, ic<3>{}, ic<1>{}, F_{}, W2{}, T_{}, T_{});
     for (int ks = 4; ks < kNK - 4; ks += 4) {
-      step(t, ks, ic<0>{}, ic<0>{}, F_{}, ic<16>{}, T_{}, T_{});
-      step(t, ks + 1, ic<1>{}, ic<1>{}, F_{}, ic<16>{}, T_{}, T_{});
-      step(t, ks + 2, ic<2>{}, ic<0>{}, F_{}, ic<16>{}, T_{}, T_{});
-      step(t, ks + 3, ic<3>{}, ic<1>{}, F_{}, ic<16>{}, T_{}, T_{});
+      step(t, ks, ic<0>{}, ic<0>{}, F_{}, W2{}, T_{}, T_{});
+      step(t, ks + 1, ic<1>{}, ic<1>{}, F_{}, W2{}, T_{}, T_{});
+      step(t, ks + 2, ic<2>{}, ic<0>{}, F_{}, W2{}, T_{}, T_{});
+      step(t, ks + 3, ic<3>{}, ic<1>{}, F_{}, W2{}, T_{}, T_{});
     }
-    step(t, kNK - 4, ic<0>{}, ic<0>{}, F_{}, ic<16>{}, F_{}, T_{});
-    step(t, kNK - 3, ic<1>{}, ic<1>{}, F_{}, ic<8>{}, F_{}, T_{});
+    step(t, kNK - 4, ic<0>{}, ic<0>{}, F_{}, W2{}, F_{}, T_{});
+    step(t, kNK - 3, ic<1>{}, ic<1>{}, F_{}, ic<LPS>{}, F_{}, T_{});
     step(t, kNK - 2, ic<2>{}, ic<0>{}, F_{}, ic<0>{}, F_{}, T_{});
     // last step: once every wave has read the ring, the next tile's loads go out first
     j += nloc;
@@ -325,13 +344,18 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     if (more) {
       issue_scales(tn, par ^ 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) issue_step(tn, 0, ic<0>{}, i), issue_step(tn, 1, ic<1>{}, i),
-                                  issue_step(tn, 2, ic<2>{}, i), issue_step(tn, 3, ic<3>{}, i);
+      for (int i = 0; i < CPW; ++i) issue_step(tn, 0, ic<0>{}, i);
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) issue_step(tn, 1, ic<1>{}, i);
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) issue_step(tn, 2, ic<2>{}, i);
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) issue_step(tn, 3, ic<3>{}, i);
     }
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int k = 0; k < 32; ++k) mfma_one(ic<1>{}, F_{}, k);
-    // Epilogue: lane l holds tokens r0 + wm*128 + 32 ti + l % 32 and, per token, vocab columns
+    for (int k = 0; k < NMF; ++k) mfma_one(ic<1>{}, F_{}, k);
+    // Epilogue: lane l holds tokens r0 + wm*TW + 32 ti + l % 32 and, per token, vocab columns
     // cb + 32 vi + 8 (j / 4) + 4 (l / 32) + j % 4, visited in increasing order.  Each logit
     // (acc * xs) * ws is rounded to bf16 once (hardware round-to-nearest-even); the lane keeps the
     // first column of its largest value (-0 and +0 compare equal, as in the bf16 argmax), folds it
@@ -342,22 +366,22 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     const float* wsl = sc_l[par][0];
     const float* xsl = sc_l[par][1];
     const int nin = d.V - t.v0 - (wn * 128 + 4 * lh);
-    // One term: token block ti is rows wm*128 + 32 ti of the tile.  Two terms: blocks 2b and 2b + 1
-    // hold the two terms of the same 32 tokens (act_row), token wm*64 + 32 b + l32 of the tile.
-    constexpr int NTB = X2 ? 2 : 4;
+    // One term: token block ti is rows wm*TW + 32 ti of the tile.  Two terms: blocks 2b and 2b + 1
+    // hold the two terms of the same 32 tokens (act_row), token wm*TW/2 + 32 b + l32 of the tile.
+    constexpr int NTB = X2 ? TB / 2 : TB;
     const int tok0 = X2 ? t.r0 / 2 : t.r0;
     {
 #pragma unroll
       for (int tb = 0; tb < NTB; ++tb) {
         const int ti = X2 ? 2 * tb : tb;
-        const int rl = X2 ? wm * 64 + tb * 32 + l32 : wm * 128 + ti * 32 + l32;  // token of the tile
+        const int rl = X2 ? wm * (TW / 2) + tb * 32 + l32 : wm * TW + ti * 32 + l32;  // token of the tile
         const int row = tok0 + rl;
-        const float xsr = xsl[wm * 128 + ti * 32 + l32];
-        const float xs2 = X2 ? xsl[wm * 128 + (ti + 1) * 32 + l32] : 0.f;
+        const float xsr = xsl[wm * TW + ti * 32 + l32];
+        const float xs2 = X2 ? xsl[wm * TW + (ti + 1) * 32 + l32] : 0.f;
         float bv = -__builtin_inff();
         int bi = 0;  // column offset from cbase
 #pragma unroll
-        for (int vi = 0; vi < 4; ++vi)
+        for (int vi = 0; vi < VB; ++vi)
 #pragma unroll
           for (int jg = 0; jg < 4; ++jg) {
             const int co = vi * 32 + 8 * jg;
@@ -401,13 +425,15 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
 }
 
 template <bool X2>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lmh_gemm_kernel(LmhDev d) {
-  lmh_gemm_body<false, X2>(d);
+__global__ __launch_bounds__(64 * kLmhWaves) __attribute__((amdgpu_waves_per_eu(kLmhWaves / 4, kLmhWaves / 4))) void
+lmh_gemm_kernel(LmhDev d) {
+  lmh_gemm_body<false, X2, kLmhWaves>(d);
 }
 // the same with the bf16 logits written out
 template <bool X2>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lmh_gemm_logits_kernel(LmhDev d) {
-  lmh_gemm_body<true, X2>(d);
+__global__ __launch_bounds__(64 * kLmhWaves) __attribute__((amdgpu_waves_per_eu(kLmhWaves / 4, kLmhWaves / 4))) void
+lmh_gemm_logits_kernel(LmhDev d) {
+  lmh_gemm_body<true, X2, kLmhWaves>(d);
 }
 
 __global__ __launch_bounds__(256) void lmh_ids_kernel(LmhDev d) {
@@ -497,13 +523,13 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
   const int ngrp = lmh_groups(nrt), vstep = 8 / ngrp;
   const int blocks = 8 * std::max(1, std::min(lmh_cus() / 8, ((nvt + vstep - 1) / vstep) * (nrt / ngrp)));
   if (d.logits && x2)
-    lmh_gemm_logits_kernel<true><<<blocks, 256, 0, st>>>(d);
+    lmh_gemm_logits_kernel<true><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
   else if (d.logits)
-    lmh_gemm_logits_kernel<false><<<blocks, 256, 0, st>>>(d);
+    lmh_gemm_logits_kernel<false><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
   else if (x2)
-    lmh_gemm_kernel<true><<<blocks, 256, 0, st>>>(d);
+    lmh_gemm_kernel<true><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
   else
-    lmh_gemm_kernel<false><<<blocks, 256, 0, st>>>(d);
+    lmh_gemm_kernel<false><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
   lmh_ids_kernel<<<(a->R + 255) / 256, 256, 0, st>>>(d);
   return check_launch("q36_lmhead_argmax");
 }
