@@ -99,12 +99,12 @@ __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
 // ------------------------------------------------------------------------------------------
 // 1. router logits + activation quantization
 // ------------------------------------------------------------------------------------------
-// Router workgroup = 8 tokens x 16 experts; wave w owns experts e0 .. e0 + 3.  The x tile is staged
-// in LDS; lane l keeps the 8-element chunks c = l + 64 j (j < H/512) of its 4 expert rows in
-// registers and accumulates every (token, expert) dot with fma in (j, i) order.  The 32 lane
-// partials of each output then meet in a recursive-halving reduce-scatter (xor 32 .. 2, then a
-// final xor-1 add): every sum pairs the same two operands as the xor butterfly (offsets 32 .. 1)
-// of q36o_dot_canon, so the logits are bit-identical to the oracle's.
+// Router workgroup = 8 tokens x 8 experts; wave w owns experts e0, e0 + 1.  The x tile is staged in
+// LDS; lane l keeps the 8-element chunks c = l + 64 j (j < H/512) of its 2 expert rows in registers
+// and accumulates every (token, expert) dot with fma in (j, i) order.  The 64 lane partials of each
+// output then meet in a recursive-halving reduce-scatter (xor 32 .. 4, then xor-2 and xor-1 adds):
+// every sum pairs the same two operands as the xor butterfly (offsets 32 .. 1) of q36o_dot_canon,
+// so the logits are bit-identical to the oracle's.
 // One reduce-scatter stage over N values: lanes whose bit O is set keep the upper half.
 template <int N, int O>
 __device__ __forceinline__ void rs_stage(float* v, int lane) {
@@ -117,25 +117,30 @@ __device__ __forceinline__ void rs_stage(float* v, int lane) {
   }
 }
 constexpr int kRouteTT = 8;   // tokens per router workgroup
-constexpr int kRouteEW = 4;   // experts per router workgroup, one per wave
+constexpr int kRouteEPW = 2;  // experts per wave: each unpacked activation serves both
+constexpr int kRouteEW = 4 * kRouteEPW;  // experts per router workgroup
 constexpr int kRouteH = 2048;
 template <int DT>
 __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_router_wg) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int bid = blockIdx.x;
   if (bid < n_router_wg) {
-    // Router workgroup = 8 tokens x 4 experts, one expert per wave: the router GEMV is VALU work
-    // in the canonical order, so it is spread over every SIMD of the chip with several waves each
+    // Router workgroup = 8 tokens x 8 experts, two per wave: the router GEMV is VALU work in the
+    // canonical order (the bf16 unpacking of the activations its largest part), so each unpacked
+    // element feeds two experts, and the work is still spread over every SIMD of the chip
     constexpr int NJ = kRouteH / 512;
+    constexpr int NO = kRouteTT * kRouteEPW;  // outputs per wave: (expert, token) pairs
     __shared__ v4i xt[kRouteTT][kRouteH / 8];
     const int neg = d.E / kRouteEW;
     const int eg = bid % neg, tg = bid / neg;
-    const int e0 = eg * kRouteEW + wave;
+    const int e0 = eg * kRouteEW + wave * kRouteEPW;
     const int t0 = tg * kRouteTT;
-    v4i w[NJ];
+    v4i w[kRouteEPW][NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      w[j] = ldg16(reinterpret_cast<const uint8_t*>(d.wr + (size_t)e0 * kRouteH + 8 * (lane + 64 * j)));
+    for (int x = 0; x < kRouteEPW; ++x)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        w[x][j] = ldg16(reinterpret_cast<const uint8_t*>(d.wr + (size_t)(e0 + x) * kRouteH + 8 * (lane + 64 * j)));
 #pragma unroll
     for (int r = 0; r < kRouteTT * kRouteH / 8 / 256; ++r) {
       const int c = threadIdx.x + 256 * r;
@@ -144,37 +149,46 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
       xt[t][cc] = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)tok * kRouteH + 8 * cc));
     }
     __syncthreads();
-    float v[kRouteTT];
+    float v[NO];  // output o = x * kRouteTT + t
 #pragma unroll
-    for (int i = 0; i < kRouteTT; ++i) v[i] = 0.f;
+    for (int i = 0; i < NO; ++i) v[i] = 0.f;
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int t = 0; t < kRouteTT; ++t) {
         const v4i xv = xt[t][lane + 64 * j];
-        float a = v[t];
+        float xf[8];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          a = __builtin_fmaf(bf_lo((uint32_t)xv[q]), bf_lo((uint32_t)w[j][q]), a);
-          a = __builtin_fmaf(bf_hi((uint32_t)xv[q]), bf_hi((uint32_t)w[j][q]), a);
+          xf[2 * q] = bf_lo((uint32_t)xv[q]);
+          xf[2 * q + 1] = bf_hi((uint32_t)xv[q]);
         }
-        v[t] = a;
+#pragma unroll
+        for (int x = 0; x < kRouteEPW; ++x) {
+          float a = v[x * kRouteTT + t];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            a = __builtin_fmaf(xf[2 * q], bf_lo((uint32_t)w[x][j][q]), a);
+            a = __builtin_fmaf(xf[2 * q + 1], bf_hi((uint32_t)w[x][j][q]), a);
+          }
+          v[x * kRouteTT + t] = a;
+        }
       }
-    // reduce-scatter over xor 32, 16, 8 (a lane keeps the half of its outputs whose index bit
-    // matches its lane bit: token (lane >> 3) after three stages), then the butterfly's last three
-    // stages (xor 4, 2, 1) among the eight lanes that hold the token
-    static_assert(kRouteTT == 8, "the stage list below assumes 8 outputs per wave");
-    rs_stage<8, 32>(v, lane);
-    rs_stage<4, 16>(v, lane);
-    rs_stage<2, 8>(v, lane);
+    // reduce-scatter over xor 32, 16, 8, 4 (a lane keeps the half of its outputs whose index bit
+    // matches its lane bit: output (lane >> 2) & 15 after four stages), then the butterfly's last
+    // two stages (xor 2, 1) among the four lanes that hold the output
+    static_assert(NO == 16, "the stage list below assumes 16 outputs per wave");
+    rs_stage<16, 32>(v, lane);
+    rs_stage<8, 16>(v, lane);
+    rs_stage<4, 8>(v, lane);
+    rs_stage<2, 4>(v, lane);
     float tot = v[0];
-    tot = tot + __shfl_xor(tot, 4);
     tot = tot + __shfl_xor(tot, 2);
     tot = tot + __shfl_xor(tot, 1);
-    const int t = lane >> 3;
-    if ((lane & 7) == 0 && t0 + t < d.M) {
-      if (d.bias) tot = tot + d.bias[e0];
-      d.logits[(size_t)(t0 + t) * d.E + e0] = rbf(tot);
+    const int o = (lane >> 2) & 15, t = o % kRouteTT, e = e0 + o / kRouteTT;
+    if ((lane & 3) == 0 && t0 + t < d.M) {
+      if (d.bias) tot = tot + d.bias[e];
+      d.logits[(size_t)(t0 + t) * d.E + e] = rbf(tot);
     }
     return;
   }

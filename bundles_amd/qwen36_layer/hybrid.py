@@ -12,7 +12,9 @@ reference folds it (L/layer.py:66-145, L/qk_route.cu:630-820).  Every launch is 
 nothing here computes.
 
 The projections are e4m3 with 128x128 block scales (the configuration's weight format), the KV
-cache e4m3 with one-token pages, the lm_head int8 per channel.
+cache e4m3 with one-token pages, the lm_head int8 per channel with the lm_head node's arithmetic by
+row count (lm_mode: W8A16 below 64 rows, two-term W8A8 up to 256, one-term above; H/node.py:9-11,
+144-151).
 """
 from __future__ import annotations
 
@@ -21,7 +23,7 @@ from dataclasses import dataclass, field
 import torch
 
 from .. import synth
-from ..qwen36_lmhead8 import lmhead8
+from ..qwen36_lmhead8 import lmhead8, node as lm_node
 from . import attn_fused, gdn_fused, moe
 from .glue import Fp8Weight, LinearWorkspace, add_rmsnorm, fp8_linear, prepare_fp8_weight
 
@@ -195,6 +197,11 @@ class HybridWorkspace:
         self.lmhead = lmhead8.Workspace(M, dev)
 
 
+def lm_mode(rows: int, vocab: int) -> str:
+    """The lm_head arithmetic the node uses for a row batch: 'w8a16', 'two_term' or 'one_term'."""
+    return lm_node.row_mode(rows, vocab)
+
+
 def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorkspace, trace: dict | None = None,
             stream=None) -> torch.Tensor:
     """x bf16 [B*T, 2048] (the embedded tokens) -> greedy ids int32 [B*T].  With trace (a dict), the
@@ -263,6 +270,8 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
         keep(f"L{i}.moe", b["m"])
         keep(f"L{i}.res_out", res)
     keep("final", h)
-    lmhead8.w8a8_lmhead_argmax(h, w.lm_q, w.lm_s, ws.lmhead, norm_w=None, eps=w.eps, ids=b["ids"], stream=stream)
+    mode = lm_mode(M, w.lm_q.shape[0])
+    lmhead8.w8a8_lmhead_argmax(h, w.lm_q, w.lm_s, ws.lmhead, norm_w=None, eps=w.eps, ids=b["ids"], stream=stream,
+                               two_term=mode == "two_term", w8a16=mode == "w8a16")
     keep("ids", b["ids"])
     return b["ids"]

@@ -127,6 +127,10 @@ def test_moe_blocks(run, oracle_mod):
 
 
 def test_lmhead_ids_bit_exact(run, oracle_mod):
+    """The node's arithmetic for the step's 256 rows is the two-term W8A8 form: ids bit-exact."""
+    from bundles_amd.qwen36_layer import hybrid
     O, tr, w = oracle_mod, run["trace"], run["w"]
-    ids, _ = O.lmhead(_sub(tr["final"]), None, w.eps, np_(w.lm_q), np_(w.lm_s))
+    mode = hybrid.lm_mode(run["ids"].shape[0], w.lm_q.shape[0])
+    assert mode == "two_term"
+    ids, _ = O.lmhead(_sub(tr["final"]), None, w.eps, np_(w.lm_q), np_(w.lm_s), two_term=True)
     assert np.array_equal(ids, np_(run["ids"])[:ROWS])
