@@ -595,7 +595,7 @@ def main():
         for k, v in legs.items():
             if v is not None:
                 line[k] = {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()
-                           if isinstance(vv, (int, float, str))}
+                           if isinstance(vv, (int, float, str, dict))}
         print(json.dumps(line), flush=True)
         return
     if not args.no_cpu:
