@@ -9,7 +9,9 @@ served module and its submodule dict untouched.  This node does the same with li
                     batches and deferred finalize run the stock block.
   GDN mixer      <- _replace_gdn_prefill's target-verify branch (L/layer.py:289-309) with
                     gdn_verify_fused (L/gdn_fused.py:37-57): in_proj, the verify over the ReplaySSM ring
-                    with its gated norm, and out_proj, on a verify batch; stock otherwise.
+                    with its gated norm, and out_proj, on a verify batch; stock otherwise.  A batch of at
+                    most DENSE8_ROWS rows projects through DENSE8 int8 copies of the served weights
+                    (W8A16, L/layer.py:13-17, L/dense8_store.py:8-13), wider ones through the e4m3 copies.
   attention      <- attn_fused.install (L/attn_fused.py:213-273): the q/gate/k/v projection with the q/k
                     norm, partial RoPE and the e4m3 KV write, the verify attention over the KV cache, and
                     the gated o_proj, on a verify batch; stock otherwise.
@@ -30,12 +32,14 @@ import torch
 
 from . import attn_fused, gdn_fused, moe
 from .engine import EngineView, SglangView
-from .glue import LinearWorkspace, fp8_linear, prepare_fp8_weight
+from .formats import quant_dense8
+from .glue import LinearWorkspace, dense8_linear, fp8_linear, prepare_fp8_weight
 
 HIDDEN, EXPERTS, INTERMEDIATE, TOPK = 2048, 512, 512, 10
 MAX_TOKENS = moe.MAX_TOKENS
 GDN_QKV, GDN_Z, GDN_HV = gdn_fused.QKV_DIM, gdn_fused.N_V_HEADS * gdn_fused.HEAD_V, gdn_fused.N_V_HEADS
 PROJ_IN = 4096
+DENSE8_ROWS = 32  # the reference's DENSE8 row limit for the recurrent block's projections
 
 
 def _mode_is(forward_batch, *names) -> bool:
@@ -162,7 +166,7 @@ class _GdnMixer:
     """The recurrent mixer's target-verify step: in_proj (e4m3 blocks, columns split q|k|v, z, b, a),
     q36_gdn_verify_ring over the engine's pools (conv, delta rule, ring appends, gated norm), out_proj."""
 
-    def __init__(self, lin, replica_lin, engine: EngineView, max_tokens: int):
+    def __init__(self, lin, replica_lin, engine: EngineView, max_tokens: int, dense8_rows: int = DENSE8_ROWS):
         w_qkvz, w_ba, w_out = lin.in_proj_qkvz.weight, lin.in_proj_ba.weight, lin.out_proj.weight
         core, norm = lin.attn, lin.norm
         _check("linear_attn.in_proj_qkvz.weight", w_qkvz, (GDN_QKV + GDN_Z, HIDDEN))
@@ -181,9 +185,14 @@ class _GdnMixer:
         self.conv_w, self.A_log, self.dt_bias = core.conv_weights, core.A_log, core.dt_bias.contiguous()
         self.norm_w, self.eps = norm.weight, float(getattr(norm, "eps", getattr(norm, "variance_epsilon", 1e-6)))
         self.scale = float(getattr(core, "head_k_dim", gdn_fused.HEAD_K)) ** -0.5
+        self.dense8_rows = min(int(dense8_rows), 64)
         with torch.no_grad():
-            self.in_proj = prepare_fp8_weight(torch.cat([w_qkvz, w_ba], dim=0))
+            w_in = torch.cat([w_qkvz, w_ba], dim=0)
+            self.in_proj = prepare_fp8_weight(w_in)
             self.out_proj = prepare_fp8_weight(w_out)
+            # the DENSE8 copies (int8 rows, fp16 scales per 128 columns) for the narrow batches
+            self.in8 = quant_dense8(w_in) if self.dense8_rows > 0 else None
+            self.out8 = quant_dense8(w_out.contiguous()) if self.dense8_rows > 0 else None
 
     def __call__(self, hidden_states, forward_batch):
         x = hidden_states
@@ -198,23 +207,30 @@ class _GdnMixer:
         e = dict(dtype=torch.bfloat16, device=x.device)
         mixed, z = torch.empty((rows, GDN_QKV), **e), torch.empty((rows, GDN_Z), **e)
         b, a = torch.empty((rows, GDN_HV), **e), torch.empty((rows, GDN_HV), **e)
-        fp8_linear(x, self.in_proj, sc.lin2048, segments=[(0, mixed), (GDN_QKV, z), (GDN_QKV + GDN_Z, b),
-                                                          (GDN_QKV + GDN_Z + GDN_HV, a)])
+        segs = [(0, mixed), (GDN_QKV, z), (GDN_QKV + GDN_Z, b), (GDN_QKV + GDN_Z + GDN_HV, a)]
+        dense8 = rows <= self.dense8_rows
+        if dense8:
+            dense8_linear(x, *self.in8, segments=segs)
+        else:
+            fp8_linear(x, self.in_proj, sc.lin2048, segments=segs)
         p = pools
         core = gdn_fused.gdn_verify_ring(mixed, z, a, b, p.conv_state, self.conv_w, p.window, self.A_log,
                                          self.dt_bias, p.h0, p.d, p.dlo, p.k, p.klo, p.g, p.qsl, p.state_idx,
                                          p.replay_idx, p.win_idx, p.write_pos, p.cache_base, self.norm_w, self.eps,
                                          self.scale, T=p.draft)
         out = torch.empty((rows, HIDDEN), **e)
-        fp8_linear(core, self.out_proj, sc.lin4096, segments=[(0, out)])
+        if dense8:
+            dense8_linear(core, *self.out8, segments=[(0, out)])
+        else:
+            fp8_linear(core, self.out_proj, sc.lin4096, segments=[(0, out)])
         return out
 
 
-def _install_gdn(module, replica, engine, max_tokens):
+def _install_gdn(module, replica, engine, max_tokens, dense8_rows):
     lin = module.linear_attn
     private = copy.copy(lin)
     private._modules = dict(lin._modules)
-    mixer = _GdnMixer(lin, private, engine, max_tokens)
+    mixer = _GdnMixer(lin, private, engine, max_tokens, dense8_rows)
     private.forward = mixer
     replica._modules["linear_attn"] = private
     return mixer
@@ -278,10 +294,12 @@ def _install_attention(module, replica, engine, max_tokens):
 
 # ---- entry --------------------------------------------------------------------------------------------
 def prepare(module, dtype: int = moe.Q36_MOE_FP8, topk: int = TOPK, max_tokens: int = MAX_TOKENS,
-            engine: EngineView | None = None, mixers: bool = True):
+            engine: EngineView | None = None, mixers: bool = True, dense8_rows: int = DENSE8_ROWS):
     """Replica of the served decoder layer with the libq36 paths installed; the served module and its
     submodule dict are left untouched.  engine: where the mixers find the verify batch's pools
-    (default: SGLang's attention backend, absent here); mixers=False installs the MoE only."""
+    (default: SGLang's attention backend, absent here); mixers=False installs the MoE only;
+    dense8_rows: verify batches up to this many rows run the recurrent block's projections on DENSE8
+    copies (0: never)."""
     _moe_block(module, topk)
     replica = copy.copy(module)
     replica._modules = dict(module._modules)
@@ -290,7 +308,7 @@ def prepare(module, dtype: int = moe.Q36_MOE_FP8, topk: int = TOPK, max_tokens: 
     mixer = None
     if mixers:
         if hasattr(module, "linear_attn"):
-            mixer = _install_gdn(module, replica, engine, max_tokens)
+            mixer = _install_gdn(module, replica, engine, max_tokens, dense8_rows)
         elif hasattr(module, "qkv_proj") and hasattr(module, "o_proj"):
             mixer = _install_attention(module, replica, engine, max_tokens)
     stock_forward = type(module).forward

@@ -156,11 +156,14 @@ class _View:
         return self.kv
 
 
-def test_layer_node_gdn_verify(dev):
+@pytest.mark.parametrize("B", [6, 10])
+def test_layer_node_gdn_verify(dev, B):
+    """24 rows project through the DENSE8 copies (at most 32 rows, the reference's rule), 40 rows through
+    the e4m3 blocks; either way the node's step equals the same entries composed by hand."""
     from bundles_amd import synth
-    from bundles_amd.qwen36_layer import engine, gdn_fused, glue, layer
-    B, T = 6, 4
-    print("layer node GDN mixer", flush=True)
+    from bundles_amd.qwen36_layer import engine, formats, gdn_fused, glue, layer
+    T = 4
+    print(f"layer node GDN mixer B={B}", flush=True)
     f = synth.gdn_ring_inputs(B, T, dev, seed=21)
     g = synth.gen(dev, 22)
     x = synth.randn((B * T, 2048), g, dev)
@@ -179,16 +182,22 @@ def test_layer_node_gdn_verify(dev):
     pos = torch.arange(100, 100 + B * T, dtype=torch.int32, device=dev)
     out, _ = layer.forward(node, pos, x, None, _batch("target_verify", pos))
     # the same step composed from the entries by hand
-    inw, outw = glue.prepare_fp8_weight(torch.cat([w_qkvz, w_ba])), glue.prepare_fp8_weight(w_out)
+    dense8 = B * T <= layer.DENSE8_ROWS
     e = dict(dtype=torch.bfloat16, device=dev)
     mixed, z = torch.empty((B * T, 8192), **e), torch.empty((B * T, 4096), **e)
     b, a = torch.empty((B * T, 32), **e), torch.empty((B * T, 32), **e)
-    glue.fp8_linear(x, inw, glue.LinearWorkspace(B * T, 2048, dev), [(0, mixed), (8192, z), (12288, b), (12320, a)])
+    segs = [(0, mixed), (8192, z), (12288, b), (12320, a)]
+    if dense8:
+        in8, out8 = formats.quant_dense8(torch.cat([w_qkvz, w_ba])), formats.quant_dense8(w_out)
+        glue.dense8_linear(x, *in8, segments=segs)
+    else:
+        inw, outw = glue.prepare_fp8_weight(torch.cat([w_qkvz, w_ba])), glue.prepare_fp8_weight(w_out)
+        glue.fp8_linear(x, inw, glue.LinearWorkspace(B * T, 2048, dev), segs)
     core = gdn_fused.gdn_verify_ring(mixed, z, a, b, f["conv_state"], f["conv_w"], f["window"], f["A_log"],
                                      f["dt_bias"], f["h0"], f["d_ring"], f["dlo_ring"], f["k_ring"], f["klo_ring"],
                                      f["g_ring"], f["qsl"], f["state_idx"], f["replay_idx"], f["win_idx"],
                                      f["write_pos"], f["cache_base"], f["norm_w"], 1e-6, 128 ** -0.5, T=T)
-    ref = glue.fp8_linear(core, outw, glue.LinearWorkspace(B * T, 4096, dev))
+    ref = glue.dense8_linear(core, *out8) if dense8 else glue.fp8_linear(core, outw, glue.LinearWorkspace(B * T, 4096, dev))
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
     for k in ("conv_state", "window", "d_ring", "dlo_ring", "k_ring", "klo_ring", "g_ring"):
