@@ -31,12 +31,27 @@ __device__ __forceinline__ v4f mfma_e4m3(v8i a, v8i b) {
 
 // ------------------------------------------------------------------------------------------
 // activation quantization: one workgroup per token; thread tid owns 8-element chunks tid + 256 r.
-// Row-major e4m3 codes q[T][K] and per 128-group scales s[T][K/128].
+// e4m3 codes q and per 128-group scales s[T][K/128]; the codes row-major [T][K], or (frag) in MFMA
+// fragment order: token tile t / 16 and 128-block kb at ((t / 16) * K / 128 + kb) * 2048, byte j of
+// the block at (j % 32) / 16 * 1024 + 16 * (t % 16 + 16 * (j / 32)) + j % 16 -- the 32 bytes lane
+// t % 16 + 16 (j / 32) feeds the MFMA, as two 16-byte halves 1 KB apart.  In fragment order the grid
+// also covers the tokens up to the next multiple of 16, whose codes and scales are zero.
 // gate != nullptr: the value quantized is bf16(x * sigmoid(gate)) (the o_proj input).
 // ------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* x, const uint16_t* gate, int K, uint8_t* q,
-                                                        float* s) {
+__device__ __forceinline__ size_t frag_offset(int t, int k, int K) {
+  const int kb = k >> 7, j = k & 127;
+  return ((size_t)(t >> 4) * (K >> 7) + kb) * 2048 + ((j & 31) >> 4) * 1024 + 16 * ((t & 15) + 16 * (j >> 5)) + (j & 15);
+}
+__global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* x, const uint16_t* gate, int T, int K, bool frag,
+                                                        uint8_t* q, float* s) {
   const int t = blockIdx.x, tid = threadIdx.x;
+  if (t >= T) {  // fragment-order padding token
+    for (int c = tid; 8 * c < K; c += 256) {
+      *reinterpret_cast<uint2*>(q + frag_offset(t, 8 * c, K)) = make_uint2(0u, 0u);
+      if ((c & 15) == 0) s[(size_t)t * (K >> 7) + c / 16] = 0.f;
+    }
+    return;
+  }
   for (int c = tid; 8 * c < K; c += 256) {
     const v4i xv = ldg16a(reinterpret_cast<const uint8_t*>(x + (size_t)t * K + 8 * c));
     float f[8];
@@ -62,7 +77,7 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* x, const
     uint32_t wd[2] = {0u, 0u};
 #pragma unroll
     for (int i = 0; i < 8; i += 2) wd[i >> 2] |= f2e4m3x2_hw(f[i] * inv, f[i + 1] * inv) << (8 * (i & 3));
-    *reinterpret_cast<uint2*>(q + (size_t)t * K + 8 * c) = make_uint2(wd[0], wd[1]);
+    *reinterpret_cast<uint2*>(q + (frag ? frag_offset(t, 8 * c, K) : (size_t)t * K + 8 * c)) = make_uint2(wd[0], wd[1]);
     if ((c & 15) == 0) s[(size_t)t * (K >> 7) + c / 16] = m / 448.f;
   }
 }
@@ -244,12 +259,145 @@ __global__ __launch_bounds__(256) void proj_gemm_kernel(GemmDev g) {
 }
 
 // ------------------------------------------------------------------------------------------
-// per-(token, head) epilogue of the QKV projection: one wave per item, 20 items per token (16 q
-// heads with their gates, 2 k, 2 v); lane holds dims lane + 64 i.  q and k: Gemma RMSNorm over 256
-// dims (sum
-// of squares by an xor butterfly over the wave, rstd = 1/sqrt(ss/256 + eps)), x = bf16((x * rstd) *
-// (1 + w)), then neox RoPE on dims 0..63 (pairs i, i + 32) with the fp32 cos|sin row of the
-// position; k and v also go to the e4m3 cache (satfinite, no scale).
+// K-sliced e4m3 projection GEMM: the same Y = bf16(sum_kb blocksum_kb(t, n) * xs[t, kb] * ws[n / 128, kb])
+// with the activations in fragment order (act_quant frag).  Workgroup = RG x KS waves over a tile of
+// 16 RT RG weight rows x 16 TT tokens; wave (rg, ks) owns RT 16-row tiles and the KB 128-blocks
+// ks KB .. +KB-1 of K, and keeps DEPTH blocks of its weight fragments in flight from the start, so
+// no wave waits on more than KB / DEPTH round trips.  Its running sums acc = fma(blocksum, xs * ws,
+// acc) go over its own blocks in increasing order from zero; the KS slices then meet in LDS and are
+// added in slice order (the K order of the slices).  The token group's activation fragments
+// (TT x K/128 x 2 KB) are copied into LDS once by buffer DMA and read by the RG row groups there.
+// The token groups of a row block are 8 workgroups apart in the grid, so they run on one XCD and
+// share its L2 for the weights.
+// ------------------------------------------------------------------------------------------
+template <int RT, int TT, int KB, int RG, int KS, int DEPTH>
+__global__ __launch_bounds__(64 * RG * KS) __attribute__((amdgpu_waves_per_eu(RG * KS / 4, RG * KS / 4))) void
+ks_gemm_kernel(GemmDev g) {
+  constexpr int NW = RG * KS, NKB = KB * KS, TG = 16 * TT, RB = 16 * RT * RG;
+  constexpr int QW = RT * TT;                   // output fragments (16 x 16) per wave
+  constexpr int PART = KS * RG * QW * 64 * 16;  // partial sums, bytes
+  constexpr int ABYTES = TT * NKB * 2048;
+  static_assert(KB % DEPTH == 0 && DEPTH <= KB, "whole rounds of blocks in flight");
+  __shared__ __align__(16) uint8_t lds[PART > ABYTES ? PART : ABYTES];
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wave / KS, ks = wave % KS;
+  const int nrb = g.N / RB, ntg = (g.T + TG - 1) / TG;
+  const int xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
+  const int rb = xcd + 8 * (jj / ntg);
+  if (rb >= nrb) return;
+  const int t0 = (jj % ntg) * TG;
+  const int tile0 = __builtin_amdgcn_readfirstlane((rb * RB) / 16 + rg * RT);  // the wave's first row tile
+  const int kb0 = ks * KB;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g.W + ((size_t)tile0 * NKB << 11)), (short)0, RT * NKB << 11, 0x00020000);
+  // activation fragments of the token group: tiles t0 / 16 .. (tiles past the padded T read zero)
+  const int ntile_a = (g.T + 15) / 16 - t0 / 16;
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g.A + ((size_t)(t0 / 16) * NKB << 11)), (short)0, (ntile_a < TT ? ntile_a : TT) * NKB << 11, 0x00020000);
+  const int xsbytes = g.T * NKB * 4;
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc((void*)g.As, (short)0, xsbytes, 0x00020000);
+  // scales: the lane's token for every (token tile, block), the wave's weight block of every (tile, block)
+  float xs[TT][KB], wsc[RT][KB];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int t = t0 + 16 * tt + lr;
+      xs[tt][kb] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(srs, t < g.T ? (t * NKB + kb0 + kb) * 4 : xsbytes, 0, 0));
+    }
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) wsc[rt][kb] = g.Ws[(size_t)((tile0 + rt) >> 3) * NKB + kb0 + kb];
+  // 1 KB per DMA instruction, the group's fragments copied in global order
+  for (int i = wave; i < TT * NKB * 2; i += NW) pdma16(ars, lds + i * 1024, lane * 16 + i * 1024);
+  asm volatile("" ::: "memory");  // the copies stay ahead of the weight loads (the wait below counts on it)
+  v4i Wf[DEPTH][RT][2];
+  auto issue = [&](int kb, int sl) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        Wf[sl][rt][h] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, ((rt * NKB + kb0 + kb) << 11) + h * 1024, 2);
+  };
+  __builtin_amdgcn_sched_barrier(0);  // the scales first: they are needed by the first accumulate
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) issue(d, d);
+  __builtin_amdgcn_sched_barrier(0);  // every round in flight before the first MFMA
+  // the copies are older than the DEPTH rounds of weight loads just issued
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DEPTH * RT * 2) : "memory");
+  __syncthreads();
+  asm volatile("" ::: "memory");
+  v4f acc[RT][TT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[rt][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const int sl = kb % DEPTH;
+    v8i a[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const uint8_t* ap = lds + ((tt * NKB + kb0 + kb) << 11) + lane * 16;
+      a[tt] = cat8a(*reinterpret_cast<const v4i*>(ap), *reinterpret_cast<const v4i*>(ap + 1024));
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const v8i w = cat8a(Wf[sl][rt][0], Wf[sl][rt][1]);
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const v4f r = mfma_e4m3(w, a[tt]);
+        const float xw = xs[tt][kb] * wsc[rt][kb];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[rt][tt][i] = __builtin_fmaf(r[i], xw, acc[rt][tt][i]);
+      }
+    }
+    if (kb + DEPTH < KB) issue(kb + DEPTH, sl);
+  }
+  // the slices meet in LDS: [ks][rg][rt][tt][lane] float4
+  __syncthreads();  // every wave is done reading the activation fragments
+  float4* part = reinterpret_cast<float4*>(lds);
+  constexpr int Q = RG * QW * 64;  // output quads of the workgroup
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+      part[(size_t)ks * Q + ((rg * RT + rt) * TT + tt) * 64 + lane] =
+          make_float4(acc[rt][tt][0], acc[rt][tt][1], acc[rt][tt][2], acc[rt][tt][3]);
+  __syncthreads();
+  for (int qd = tid; qd < Q; qd += 64 * NW) {
+    float4 v = part[qd];
+#pragma unroll
+    for (int k = 1; k < KS; ++k) {
+      const float4 u = part[(size_t)k * Q + qd];
+      v.x += u.x;
+      v.y += u.y;
+      v.z += u.z;
+      v.w += u.w;
+    }
+    // quad qd = ((rg' RT + rt) TT + tt) 64 + l: token t0 + 16 tt + l % 16, rows 4 (l / 16) .. +3 of tile rg' RT + rt
+    const int l = qd & 63, f = qd >> 6, tt = f % TT, tr = f / TT;
+    const int t = t0 + 16 * tt + (l & 15);
+    const int col = rb * RB + tr * 16 + 4 * (l >> 4);
+    if (t < g.T && col < g.nout) {
+      const int sg = (g.nseg > 1 && col >= g.c0[1]) + (g.nseg > 2 && col >= g.c0[2]) + (g.nseg > 3 && col >= g.c0[3]);
+      *reinterpret_cast<uint2*>(g.ys[sg] + (size_t)t * g.ld[sg] + (col - g.c0[sg])) =
+          make_uint2(pack_bf2(v.x, v.y), pack_bf2(v.z, v.w));
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// per-(token, head) epilogue of the QKV projection: one wave per item, 18 items per token (16 q heads
+// with their gates, 2 kv heads).  Lanes 0-31 hold the normed head (q, or k), 8 consecutive dims a
+// lane, lanes 32-63 its companion (the gate, or v); every access is 16 bytes a lane.  q and k: Gemma
+// RMSNorm over 256 dims (sum of squares by an xor butterfly over the 32 lanes (ds_swizzle), rstd =
+// 1/sqrt(ss/256 + eps)), x = bf16((x * rstd) * (1 + w)), then neox RoPE on dims 0..63 (pairs i,
+// i + 32: lanes j and j ^ 4 of the first 8) with the fp32 cos|sin row of the position; k and v also
+// go to the e4m3 cache (satfinite, no scale).
 // ------------------------------------------------------------------------------------------
 struct RopeDev {
   int T, max_pos;
@@ -266,61 +414,74 @@ struct RopeDev {
   uint8_t* k8;
   uint8_t* v8;
 };
+constexpr int kRopeItems = 18;  // waves per token
 __global__ __launch_bounds__(256) void norm_rope_kernel(RopeDev d) {
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (item >= d.T * 20) return;
-  const int t = item / 20, h = item % 20;
-  // the head's values (and, for q heads, its gate) are loaded before the position's cos|sin row,
-  // whose address depends on another load
-  const uint16_t* row = d.qkv + (size_t)t * 9216;
-  int col;
-  const uint16_t* nw = nullptr;
-  if (h < 16) {
-    col = h * 512;  // q half of the head's [q(256) gate(256)]
-    nw = d.q_norm_w;
-  } else if (h < 18) {
-    col = 8192 + (h - 16) * 256;
-    nw = d.k_norm_w;
-  } else {
-    col = 8704 + (h - 18) * 256;
-  }
-  float x[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = bf2f(row[col + lane + 64 * i]);
-  if (h < 16) {
-    uint16_t gv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) gv[i] = row[col + 256 + lane + 64 * i];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) d.gate[((size_t)t * 16 + h) * 256 + lane + 64 * i] = gv[i];
-  }
+  if (item >= d.T * kRopeItems) return;
+  const int t = item / kRopeItems, h = item % kRopeItems;
+  const int half = lane >> 5, j = lane & 31;
+  const bool qhead = h < 16;
+  const int hh = h - 16;
+  const int col = qhead ? h * 512 + half * 256 + 8 * j : (half ? 8704 : 8192) + hh * 256 + 8 * j;
+  // the head's values and norm weights are requested before the position's cos|sin row, whose
+  // address depends on another load
+  const v4i raw = ldg16a(reinterpret_cast<const uint8_t*>(d.qkv + (size_t)t * 9216 + col));
+  const v4i wraw = ldg16a(reinterpret_cast<const uint8_t*>((qhead ? d.q_norm_w : d.k_norm_w) + 8 * j));
   int pos = d.positions[t];
   pos = pos < 0 ? 0 : (pos >= d.max_pos ? d.max_pos - 1 : pos);
-  const float* cs = d.cos_sin + (size_t)pos * 64;
-  if (nw) {
-    const float ss = wave_sum_bfly((x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]));
-    const float inv = 1.f / sqrtf(ss / 256.f + d.eps);
+  // lanes j < 8 rotate dims 8 j .. 8 j + 7 with cos|sin entries i = 8 (j & 3) + e
+  const float* cs = d.cos_sin + (size_t)pos * 64 + 8 * (j & 3);
+  const float4 c0 = *reinterpret_cast<const float4*>(cs), c1 = *reinterpret_cast<const float4*>(cs + 4);
+  const float4 s0 = *reinterpret_cast<const float4*>(cs + 32), s1 = *reinterpret_cast<const float4*>(cs + 36);
+  float x[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = rbf((x[i] * inv) * (bf2f(nw[lane + 64 * i]) + 1.f));
-    // RoPE on dims 0..63 = x[0] of every lane: pair (i, i + 32) = lanes (l, l ^ 32)
-    const float other = __shfl_xor(x[0], 32);
-    const int i = lane & 31;
-    const float c = cs[i], s = cs[32 + i];
-    x[0] = lane < 32 ? rbf(x[0] * c - other * s) : rbf(x[0] * c + other * s);
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = bf_lo((uint32_t)raw[i]);
+    x[2 * i + 1] = bf_hi((uint32_t)raw[i]);
   }
-  if (h < 16) {
+  // the sum of squares: every lane takes part (the companion half's sums are not used)
+  float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) d.q[((size_t)t * 16 + h) * 256 + lane + 64 * i] = (uint16_t)f2bf(x[i]);
+  for (int i = 0; i < 8; ++i) ss = __builtin_fmaf(x[i], x[i], ss);
+  ss += xor_swz<16>(ss);
+  ss += xor_swz<8>(ss);
+  ss += xor_swz<4>(ss);
+  ss += xor_swz<2>(ss);
+  ss += xor_swz<1>(ss);
+  const bool normed = half == 0;
+  // branch-free: every lane computes the normed and rotated values, the selects keep what applies
+  const float inv = 1.f / sqrtf(ss / 256.f + d.eps);
+  float y[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    y[2 * i] = rbf_hw((x[2 * i] * inv) * (bf_lo((uint32_t)wraw[i]) + 1.f));
+    y[2 * i + 1] = rbf_hw((x[2 * i + 1] * inv) * (bf_hi((uint32_t)wraw[i]) + 1.f));
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = normed ? y[e] : x[e];
+  // RoPE: lanes j < 4 take x c - x' s, lanes 4 <= j < 8 take x c + x' s (a sign flip is exact)
+  const float sg = j < 4 ? -1.f : 1.f;
+  const bool rot = normed && j < 8;
+  const float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float other = xor_swz<4>(y[e]);
+    const float r = rbf_hw(y[e] * c[e] + (sg * other) * sn[e]);
+    x[e] = rot ? r : y[e];
+  }
+  const uint4 packed =
+      make_uint4(pack_bf2_hw(x[0], x[1]), pack_bf2_hw(x[2], x[3]), pack_bf2_hw(x[4], x[5]), pack_bf2_hw(x[6], x[7]));
+  if (qhead) {
+    uint16_t* dst = normed ? d.q : d.gate;  // the gate half stores its own values (x = y = the loaded row)
+    *reinterpret_cast<uint4*>(dst + ((size_t)t * 16 + h) * 256 + 8 * j) = packed;
   } else {
-    const int hh = h < 18 ? h - 16 : h - 18;
-    uint16_t* dst = h < 18 ? d.k : d.v;
-    uint8_t* dst8 = h < 18 ? d.k8 : d.v8;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const size_t o = ((size_t)t * 2 + hh) * 256 + lane + 64 * i;
-      dst[o] = (uint16_t)f2bf(x[i]);
-      dst8[o] = (uint8_t)(f2e4m3x2_hw(x[i], 0.f) & 0xffu);
-    }
+    const size_t o = ((size_t)t * 2 + hh) * 256 + 8 * j;
+    *reinterpret_cast<uint4*>((normed ? d.k : d.v) + o) = packed;
+    uint2 e8;
+    e8.x = f2e4m3x2_hw(x[0], x[1]) | (f2e4m3x2_hw(x[2], x[3]) << 16);
+    e8.y = f2e4m3x2_hw(x[4], x[5]) | (f2e4m3x2_hw(x[6], x[7]) << 16);
+    *reinterpret_cast<uint2*>((normed ? d.k8 : d.v8) + o) = e8;
   }
 }
 
@@ -335,8 +496,9 @@ AttnWs attn_ws(int T) {
     o = align_up(o + b, 256);
     return r;
   };
-  w.xq = take((size_t)T * 2048);
-  w.xs = take(sizeof(float) * (size_t)16 * T);
+  const size_t T16 = (size_t)(T + 15) / 16 * 16;  // fragment order pads the tokens to whole tiles
+  w.xq = take(T16 * 2048);
+  w.xs = take(sizeof(float) * 16 * T16);
   w.qkv = take(sizeof(uint16_t) * (size_t)T * 9216);
   w.total = o;
   return w;
@@ -382,6 +544,15 @@ void launch_gemm(const GemmDev& g, hipStream_t st) {
   proj_gemm_kernel<NTT, NKB, PD, TPW><<<8 * ((nrb + 7) / 8) * ntg, 256, 0, st>>>(g);
 }
 
+// grid: the row blocks (N / (16 RT RG), rounded up to a multiple of the 8 XCDs) x token groups of 16 TT
+template <int RT, int TT, int KB, int RG, int KS, int DEPTH>
+void launch_ks(const GemmDev& g, hipStream_t st) {
+  const int nrb = g.N / (16 * RT * RG), ntg = (g.T + 16 * TT - 1) / (16 * TT);
+  ks_gemm_kernel<RT, TT, KB, RG, KS, DEPTH><<<8 * ((nrb + 7) / 8) * ntg, 64 * RG * KS, 0, st>>>(g);
+}
+// token counts from which the projections take the K-sliced GEMM (fragment-order activations)
+constexpr int kKsMinT = 32;
+
 // 8-bit codes (e4m3 or int8) [N, K] row-major -> fragment order; thread = one 16-byte chunk of the output
 __global__ __launch_bounds__(256) void pack_frag_kernel(const uint8_t* q, int64_t N, int K, uint8_t* out) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // output chunk
@@ -411,8 +582,13 @@ extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
   Q36_REQUIRE(a->x && a->wqkv && a->sqkv && a->q_norm_w && a->k_norm_w && a->cos_sin && a->positions && a->q &&
                   a->gate && a->k && a->v && a->k8 && a->v8 && a->workspace,
               "q36_attn_proj: a required pointer is null");
-  Q36_REQUIRE(aligned16(a->x) && aligned16(a->wqkv) && (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0,
-              "q36_attn_proj: x, wqkv must be 16-byte and workspace 256-byte aligned");
+  Q36_REQUIRE(aligned16(a->x) && aligned16(a->wqkv) && aligned16(a->q_norm_w) && aligned16(a->k_norm_w) &&
+                  aligned16(a->cos_sin) && aligned16(a->q) && aligned16(a->gate) && aligned16(a->k) &&
+                  aligned16(a->v) && (reinterpret_cast<uintptr_t>(a->k8) & 7u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(a->v8) & 7u) == 0 &&
+                  (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0,
+              "q36_attn_proj: x, wqkv, the norm weights, cos_sin, q, gate, k, v must be 16-byte, k8 and v8 8-byte "
+              "and workspace 256-byte aligned");
   const AttnWs L = attn_ws(a->T);
   Q36_REQUIRE(a->workspace_bytes >= L.total, "q36_attn_proj: workspace of %zu bytes < %zu required",
               a->workspace_bytes, L.total);
@@ -421,19 +597,23 @@ extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
   uint8_t* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
   float* xs = reinterpret_cast<float*>(ws + L.xs);
   uint16_t* qkv = reinterpret_cast<uint16_t*>(ws + L.qkv);
-  act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr, 2048, xq, xs);
+  const bool ks = a->T >= kKsMinT;
+  const int Tq = ks ? (a->T + 15) / 16 * 16 : a->T;
+  act_quant_kernel<<<Tq, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr, a->T, 2048, ks, xq, xs);
   const GemmDev g = gemm_dev(xq, xs, a->T, 2048, static_cast<const uint8_t*>(a->wqkv), a->sqkv, 9216, qkv);
-  // measured at 128 tokens: two-tile groups with 2 stages in flight beat four-tile groups (the
-  // weight reads from L2 double, the grid doubles to 288 workgroups) and one-tile groups
-  if (a->T > 16)
-    launch_gemm<2, 16, 2>(g, st);
+  // 144-row x 32-token workgroups, 3 row groups x 4 K quarters (12 waves): 256 workgroups at 128
+  // tokens, 17.9 us per graph-timed call against 19.2 us for the streaming GEMM (128 x 32 tiles, 288
+  // workgroups).  Both move about 90 MB through L2 per call (the token groups re-read the weights, the
+  // row blocks the activations), which at ~18 TB/s across the chip is what bounds them.
+  if (ks)
+    launch_ks<3, 2, 4, 3, 4, 2>(g, st);
   else
     launch_gemm<1, 16, 4>(g, st);
   RopeDev r{a->T, a->max_pos, qkv, static_cast<const uint16_t*>(a->q_norm_w),
             static_cast<const uint16_t*>(a->k_norm_w), a->eps, a->cos_sin, a->positions,
             static_cast<uint16_t*>(a->q), static_cast<uint16_t*>(a->gate), static_cast<uint16_t*>(a->k),
             static_cast<uint16_t*>(a->v), static_cast<uint8_t*>(a->k8), static_cast<uint8_t*>(a->v8)};
-  norm_rope_kernel<<<(a->T * 20 + 3) / 4, 256, 0, st>>>(r);
+  norm_rope_kernel<<<(a->T * kRopeItems + 3) / 4, 256, 0, st>>>(r);
   return check_launch("q36_attn_proj");
 }
 
@@ -453,11 +633,13 @@ extern "C" int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream) {
   uint8_t* aq = reinterpret_cast<uint8_t*>(ws + L.aq);
   float* as = reinterpret_cast<float*>(ws + L.as);
   act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->attn), static_cast<const uint16_t*>(a->gate),
-                                         4096, aq, as);
+                                         a->T, 4096, false, aq, as);
   const GemmDev g =
       gemm_dev(aq, as, a->T, 4096, static_cast<const uint8_t*>(a->wo), a->so, 2048, static_cast<uint16_t*>(a->out));
-  // o_proj: 64-row blocks (one 16-row tile per wave), one-tile token groups, 4 stages in flight:
-  // 256 workgroups at 128 tokens; measured 6.8 us against 8.1 us for 128-row blocks (128 workgroups)
+  // 64-row blocks (one 16-row tile per wave), one-tile token groups, 4 stages in flight: 256
+  // workgroups at 128 tokens.  Measured at 128 tokens: 6.8 us against 8.1 us for 128-row blocks; the
+  // K-sliced GEMM (8 slices of 512, 32 x 32 tiles) 1 us slower per call: with every load of a wave in
+  // flight at once the token groups' shared weight lines leave L2 before the last group reads them
   launch_gemm<1, 32, 4, 1>(g, st);
   return check_launch("q36_attn_oproj");
 }
@@ -493,7 +675,7 @@ extern "C" int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream)
   char* ws = static_cast<char*>(a->workspace);
   uint8_t* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
   float* xs = reinterpret_cast<float*>(ws + L.xs);
-  act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr, a->K, xq, xs);
+  act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr, a->T, a->K, false, xq, xs);
   GemmDev g = gemm_dev(xq, xs, a->T, a->K, static_cast<const uint8_t*>(a->w), a->ws, a->N, nullptr);
   g.nseg = a->nseg;
   g.nout = a->n_out;

@@ -141,13 +141,6 @@ __device__ __forceinline__ int bswz(int c, int kc) { return c * kBK + ((kc ^ ((c
 template <int N>
 using ic = std::integral_constant<int, N>;
 
-// x rounded to bf16 (round to nearest even), returned as the float it represents: one
-// v_cvt_pk_bf16_f32 with a zero low half.
-__device__ __forceinline__ float round_bf16(float x) {
-  typedef float v2f __attribute__((ext_vector_type(2)));
-  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(float, __builtin_convertvector((v2f){0.f, x}, v2bf));
-}
 
 // s_waitcnt with only the vector-memory count constrained (gfx9 encoding: vmcnt bits 3:0 and 15:14).
 template <int N>
@@ -393,10 +386,10 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               if constexpr (X2)
-                lg[q] = round_bf16(__builtin_fmaf((float)acc[vi][ti][4 * jg + q], xsr,
+                lg[q] = rbf_hw(__builtin_fmaf((float)acc[vi][ti][4 * jg + q], xsr,
                                                   (float)acc[vi][ti + 1][4 * jg + q] * xs2) * wq[q]);
               else
-                lg[q] = round_bf16(((float)acc[vi][ti][4 * jg + q] * xsr) * wq[q]);
+                lg[q] = rbf_hw(((float)acc[vi][ti][4 * jg + q] * xsr) * wq[q]);
               if (in && lg[q] > bv) bv = lg[q], bi = co + q;
             }
             if constexpr (STORE)

@@ -30,6 +30,17 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
   return u >> 16;
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+// The same rounding for finite values by one v_cvt_pk_bf16_f32 (round to nearest even); NaN becomes
+// the canonical quiet NaN.  rbf_hw: the rounded value as the float it represents; pack_bf2_hw: two
+// values packed, lo in bits 0..15.
+typedef float q36_v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 q36_v2bf __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float rbf_hw(float x) {
+  return __builtin_bit_cast(float, __builtin_convertvector((q36_v2f){0.f, x}, q36_v2bf));
+}
+__device__ __forceinline__ uint32_t pack_bf2_hw(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((q36_v2f){lo, hi}, q36_v2bf));
+}
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
 // float -> OCP e4m3fn code: round to nearest even, saturate to +-448, NaN -> 0x7f.
@@ -89,6 +100,12 @@ __device__ __forceinline__ float expf_q(float x) {
 __device__ __forceinline__ float sigmoid_q(float z) { return 1.f / (1.f + expf_q(-z)); }
 
 // xor-butterfly over the 64 lanes (offsets 32 .. 1): every lane ends with the same total.
+// v of lane l ^ M within each 32-lane half (ds_swizzle bit mode: and 0x1f, xor M), M < 32
+template <int M>
+__device__ __forceinline__ float xor_swz(float v) {
+  static_assert(M > 0 && M < 32, "xor mask within 32 lanes");
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (M << 10)));
+}
 __device__ __forceinline__ float wave_sum_bfly(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o);

@@ -52,12 +52,6 @@ __device__ __forceinline__ v4f mfma_bf16(v8bf a, v8bf b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// x rounded to bf16, as the float it represents (v_cvt_pk_bf16_f32, round to nearest even)
-__device__ __forceinline__ float round_bf16_w(float x) {
-  typedef float v2f __attribute__((ext_vector_type(2)));
-  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(float, __builtin_convertvector((v2f){0.f, x}, v2bf));
-}
 
 // One workgroup: WAVES waves in RG = WAVES / KS row groups of 16 RT rows; the KS waves of a row group
 // split K into KS contiguous chunks (a multiple of 128 columns each) and their fp32 partial sums meet in
@@ -222,7 +216,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8a16_kernel(W16Dev d) {
           float lg4[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            lg4[i] = round_bf16_w(acc[rt][tt][i] * wsv[i]);
+            lg4[i] = rbf_hw(acc[rt][tt][i] * wsv[i]);
             if (lg4[i] > bv) bv = lg4[i], bi = rb + i - blockIdx.x * (RG * RW);
           }
           if (d.logits && t < d.T)

@@ -265,6 +265,8 @@ int q36_gdn_verify_ring(const q36_gdn_ring_args* a, q36_stream_t stream);
  *   q36_attn_oproj: out bf16 [T, 2048] = (bf16(attn * sigmoid(gate)) in e4m3) . wo^T with
  *     attn, gate bf16 [T, 4096], wo e4m3 [2048, 4096] in fragment order, so fp32 [16, 32]
  *     (L/qk_attn_verify.cu:730-737).
+ * Alignment: x, wqkv, attn, gate, wo, the norm weights, cos_sin and q, gate, k, v 16 bytes; k8, v8
+ * 8 bytes.
  * Workspaces: q36_attn_workspace_bytes(T), q36_oproj_workspace_bytes(T), 256-byte aligned. */
 typedef struct q36_attn_args {
   int32_t T, max_pos;

@@ -1,7 +1,8 @@
 """GPU parity of the fused attention projections (libq36 through the C-ABI) against the CPU oracle.
 
 Bar: bf16 outputs (q, gate, k, v, o_proj out) within 1e-2 relative (per-row norm); the e4m3 cache
-rows decode to values within the same bar."""
+codes equal the e4m3 conversion of the kernel's own k / v rows, and decode within 2e-2 of the
+oracle's (one e4m3 step is up to 1/8 relative, so a one-ulp difference in k can move a code)."""
 import numpy as np
 import pytest
 import torch
@@ -33,7 +34,7 @@ def _oracle_weights(w):
     return dict(wqg=q[:8192], sqg=s[:64], wk=q[8192:8704], sk=s[64:68], wv=q[8704:], sv=s[68:72])
 
 
-@pytest.mark.parametrize("T", [1, 37, 128])
+@pytest.mark.parametrize("T", [1, 37, 128, 256])
 def test_attn_proj_parity(attn, oracle_mod, dev, T):
     O = oracle_mod
     print(f"attn_proj T={T}", flush=True)
@@ -47,16 +48,23 @@ def test_attn_proj_parity(attn, oracle_mod, dev, T):
     for key in ("q", "gate", "k", "v"):
         wr, ar, er = assert_bf16_close(bits16(o[key]).reshape(T, -1), r[key].reshape(T, -1), 1e-2, key)
         print(f"{key}: row err {wr:.2e} elem {ar:.2e} exact {er:.4f}", flush=True)
-    for key in ("k8", "v8"):
-        got = O.e4m3_to_f32(bits8(o[key]).reshape(T, -1))
+    for key, src in (("k8", "k"), ("v8", "v")):
+        # the cache write is exact on the kernel's own bf16 row (e4m3 satfinite, round to nearest even)
+        codes = bits8(o[key]).reshape(T, -1)
+        own = O.f32_to_e4m3(O.bf16_to_f32(bits16(o[src]).reshape(T, -1)))
+        assert np.array_equal(codes, own), f"{key}: codes differ from e4m3 of the kernel's own {src}"
+        # against the oracle's codes: a one-ulp bf16 difference in a row can move a code by one e4m3 step
+        # (up to 1/8 relative), so the decoded rows are held to 2e-2
+        got = O.e4m3_to_f32(codes)
         ref = O.e4m3_to_f32(r[key].reshape(T, -1))
-        assert_bf16_close(O.f32_to_bf16(got), O.f32_to_bf16(ref), 1e-2, key)
-        print(f"{key}: exact codes {np.mean(bits8(o[key]).reshape(T, -1) == r[key].reshape(T, -1)):.4f}")
+        assert_bf16_close(O.f32_to_bf16(got), O.f32_to_bf16(ref), 2e-2, key)
+        print(f"{key}: exact codes {np.mean(codes == r[key].reshape(T, -1)):.4f}")
 
 
-@pytest.mark.parametrize("T", [1, 128])
+@pytest.mark.parametrize("T", [1, 37, 128])
 def test_attn_oproj_parity(attn, oracle_mod, dev, T):
     O = oracle_mod
+    print(f"attn_oproj T={T}", flush=True)
     d, w = _setup(attn, dev, T, seed=100 + T)
     ws = attn.Workspace(T, dev)
     gate = (torch.randn((T, 4096), device=dev) * 2).to(torch.bfloat16)
