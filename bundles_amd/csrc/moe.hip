@@ -488,21 +488,46 @@ __global__ __launch_bounds__(256) void route_lists_kernel(MoeDev d) {
 // ------------------------------------------------------------------------------------------
 // Expert work: token lists, MFMA fragments
 // ------------------------------------------------------------------------------------------
-// The expert kernels find an expert's tokens from ids directly: thread t (< M) scans token t's k
-// ids, and a ballot compaction lists the matching slots s = t*k + j in token order (the shared
-// expert lists slot M*k + t of every non-padding token).  h and y are indexed by slot, so no
+// The expert kernels take an expert's tokens from the per-expert slot lists route_topk builds
+// (elist, ecount; the order inside a list changes no output, every result is stored by slot); the
+// shared expert lists slot M*k + t of every non-padding token.  h and y are indexed by slot, so no
 // sorted-position lists sit on the forward path (q36_moe_route still publishes them).
-__device__ __forceinline__ int expert_slots(const MoeDev& d, int e_or_shared, int* slots, int* wtot) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int my = -1;
-  if (tid < d.M) {
-    if (e_or_shared < 0) {
-      if (d.pos == nullptr || d.pos[tid] != 0) my = d.M * d.k + tid;
-    } else {
-      for (int j = 0; j < d.k; ++j)
-        if (d.ids[tid * d.k + j] == e_or_shared) my = tid * d.k + j;
-    }
+// Unit u of an expert kernel: 0 is the shared expert (slots M*k + t of the non-padding tokens),
+// u >= 1 the (u-1)-th entry of the active list, whose expert e the caller has read already (with
+// the active count, in one round trip).  The list is fetched in two steps, so the caller can put its
+// first weight loads between them: slots_request issues the loads (the expert's count and its whole
+// list row, one entry a thread; for the shared expert the positions), slots_finish fills slots[] in
+// LDS and returns the count.  Vector loads complete in issue order, so loads issued after the request
+// do not delay it.
+struct SlotReq {
+  int v;  // routed unit: list entry tid; shared unit: position of token tid (0 marks padding)
+};
+__device__ __forceinline__ SlotReq slots_request(const MoeDev& d, int unit, int e) {
+  const int tid = threadIdx.x;
+  if (unit == 0) {
+    const int pbytes = d.pos ? d.M * 4 : 0;
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc((void*)d.pos, (short)0, pbytes, 0x00020000);
+    return SlotReq{(int)__builtin_amdgcn_raw_buffer_load_b32(prs, tid < d.M ? tid * 4 : pbytes, 0, 0)};
   }
+  const int lbytes = d.M * 4;
+  const __amdgpu_buffer_rsrc_t lrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(d.elist + (size_t)e * d.M), (short)0, lbytes, 0x00020000);
+  return SlotReq{(int)__builtin_amdgcn_raw_buffer_load_b32(lrs, tid < d.M ? tid * 4 : lbytes, 0, 0)};
+}
+__device__ __forceinline__ int slots_finish(const MoeDev& d, int unit, int e, const SlotReq& r, int* slots,
+                                            int* wtot) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (unit != 0) {
+    // the expert's count by a scalar load through the constant address space (the expert kernels
+    // never write ecount; a plain load here is compiled as a vector load, which would complete
+    // behind the weights); issued here, after the caller's weight loads, it does not hold them up
+    const int cnt = ((const __attribute__((address_space(4))) int*)(d.ecount))[e];
+    if (tid < cnt) slots[tid] = r.v;
+    __syncthreads();
+    return cnt;
+  }
+  // the shared expert: slot M*k + t of every non-padding token, in token order (ballot compaction)
+  const int my = tid < d.M && (d.pos == nullptr || r.v != 0) ? d.M * d.k + tid : -1;
   const unsigned long long b = __ballot(my >= 0);
   const int below = __popcll(b & ((1ull << lane) - 1ull));
   if (lane == 0) wtot[wave] = __popcll(b);
@@ -516,24 +541,15 @@ __device__ __forceinline__ int expert_slots(const MoeDev& d, int e_or_shared, in
   __syncthreads();
   return tot;
 }
-// Unit u of an expert kernel: 0 is the shared expert (slots M*k + t of the non-padding tokens),
-// u >= 1 the (u-1)-th entry of the active list.  Fills slots[] in LDS and returns the count
-// (0: nothing to do).  *e_out is the expert (-1 for shared).
-__device__ __forceinline__ int unit_slots(const MoeDev& d, int unit, int* slots, int* wtot, int* e_out) {
-  if (unit == 0) {
-    *e_out = -1;
-    return expert_slots(d, -1, slots, wtot);
-  }
-  if (unit - 1 >= d.ctl[2]) {
-    *e_out = -1;
-    return 0;
-  }
-  const int e = d.eact[unit - 1];
-  const int cnt = d.ecount[e];
-  for (int i = threadIdx.x; i < cnt; i += blockDim.x) slots[i] = d.elist[(size_t)e * d.M + i];
-  __syncthreads();
-  *e_out = e;
-  return cnt;
+// The active count and unit u's expert (u >= 1) in one round trip: eact's entry of an idle unit may
+// hold a stale id, which the caller never uses.  Returns -2 when the unit is idle, -1 for the shared
+// expert, else the expert.
+__device__ __forceinline__ int unit_expert(const MoeDev& d, int unit) {
+  const int nact = d.ctl[2];
+  const int e = d.eact[unit > 0 ? unit - 1 : 0];
+  asm volatile("" ::"s"(nact), "s"(e));  // both loads issued before either is tested
+  if (unit == 0) return -1;
+  return unit - 1 < nact ? e : -2;
 }
 __device__ __forceinline__ int slot_token(const MoeDev& d, int s) {
   const int S = d.M * d.k;
@@ -582,8 +598,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ int wtot[4];
   const int unit = blockIdx.x / kUpGroups, grp = blockIdx.x % kUpGroups;
   const bool shared = unit == 0;
-  if (!shared && unit - 1 >= d.ctl[2]) return;
-  const int e = shared ? -1 : d.eact[unit - 1];
+  const int e = unit_expert(d, unit);
+  if (e == -2) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
   const uint8_t* W = shared ? d.sw13 : d.w13 + (size_t)e * 2 * I * H;
   const float* S = shared ? d.ss13
@@ -608,11 +624,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     Bq[q][2] = __builtin_amdgcn_raw_buffer_load_b128(urs, lo, s * 2048, 2);
     Bq[q][3] = __builtin_amdgcn_raw_buffer_load_b128(urs, lo, s * 2048 + 1024, 2);
   };
-  // the token list comes first: each group's activation rows and scales are requested before its
-  // first weight stages, so they arrive while the weights stream (vector loads complete in issue
-  // order)
-  int e_chk;
-  const int cnt = unit_slots(d, unit, slots, wtot, &e_chk);
+  // the token list is requested, then the first group's first weight stages, as soon as the expert
+  // is known; the activation rows and their scales (which depend on the list) follow
+  const SlotReq req = slots_request(d, unit, e);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int s = 0; s < kUpD; ++s) issue(s, s);
+  __builtin_amdgcn_sched_barrier(0);
+  const int cnt = slots_finish(d, unit, e, req, slots, wtot);
   if (cnt == 0) return;
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)d.xq, (short)0, d.M * H, 0x00020000);
@@ -624,8 +643,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // per 128-byte stage every fragment and scale read first, then the independent MFMAs, then the
   // scaled accumulates (e4m3: in block order from zero), then SwiGLU -> h per slot.  A one-tile
   // group holds its rows' whole K in LDS; a four-tile group one K half at a time.
-  auto group = [&](int g0, auto nttc) {
+  auto group = [&](int g0, auto nttc, auto firstc) {
     constexpr int NTT = decltype(nttc)::value;
+    constexpr bool FIRST = decltype(firstc)::value;  // the weight stages 0 .. kUpD-1 are in flight
     // activation rows in LDS: a one-tile group holds its 16 rows' whole K (padded rows, one
     // buffer); a four-tile group streams K in 4 chunks of 512 bytes through two buffers, so the
     // next chunk's copy overlaps the current chunk's stages and the weight stream never drains.
@@ -675,13 +695,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       wsr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wss, g0 == 0 && tid < NW ? tid * 4 : NW * 4, 0, 0));
     }
     rows_dma(0);
+    if constexpr (!FIRST) {
 #pragma unroll
-    for (int s = 0; s < kUpD; ++s) issue(s, s);
+      for (int s = 0; s < kUpD; ++s) issue(s, s);
+    }
 #pragma unroll
     for (int q = 0; q < TG * NSTG / 256; ++q) xs_t[tid + 256 * q] = xsr[q];
     if constexpr (DT == Q36_MOE_FP8)
       if (g0 == 0 && tid < (2 * I / 128) * NSTG) ws_l[tid] = wsr;
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kUpD) : "memory");  // the rows, not the weights
+    // the rows (and for later groups not the weights, requested after them; the first group's
+    // weights are older than the rows)
+    if constexpr (FIRST)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kUpD) : "memory");
     __syncthreads();
     asm volatile("" ::: "memory");
     Acc ag[NTT], au[NTT];
@@ -778,14 +805,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
   };
-  for (int g0 = 0; g0 < cnt; g0 += TG) {
-    if (g0 > 0) __syncthreads();  // the previous group's epilogue has read xs_t
-    // two tile counts: one tile (most experts at decode sizes) or four (rows past the tokens are
-    // zero); a third instance would cost registers in all of them
-    if (cnt - g0 <= 16)
-      group(g0, std::integral_constant<int, 1>{});
-    else
-      group(g0, std::integral_constant<int, 4>{});
+  // two tile counts: one tile (most experts at decode sizes) or four (rows past the tokens are
+  // zero); a third instance would cost registers in all of them
+  if (cnt <= 16) {
+    group(0, std::integral_constant<int, 1>{}, std::true_type{});
+  } else {
+    group(0, std::integral_constant<int, 4>{}, std::true_type{});
+    for (int g0 = TG; g0 < cnt; g0 += TG) {
+      __syncthreads();  // the previous group's epilogue has read xs_t
+      if (cnt - g0 <= 16)
+        group(g0, std::integral_constant<int, 1>{}, std::false_type{});
+      else
+        group(g0, std::integral_constant<int, 4>{}, std::false_type{});
+    }
   }
 }
 
@@ -803,6 +835,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // tiles go in pairs, so one pair's accumulators and one stage's operands stay in registers.
 constexpr int kDnRows = 64;
 constexpr int kDnCT = kDnRows / 16;
+static_assert(kDnCT == 4, "the down weights are issued as two tile pairs");
 constexpr int kDnGroups = kMoeH / (4 * kDnRows);
 constexpr int kDnTG = 64;
 constexpr int kDnRow = kMoeI + 16;  // padded LDS row: 16 rows' 16-byte reads hit distinct banks
@@ -817,8 +850,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __align__(16) float sn[4 * kDnRows];  // int8 weight scale per output row of the workgroup
   const int unit = blockIdx.x / kDnGroups, grp = blockIdx.x % kDnGroups;
   const bool shared = unit == 0;
-  if (!shared && unit - 1 >= d.ctl[2]) return;
-  const int e = shared ? -1 : d.eact[unit - 1];
+  const int e = unit_expert(d, unit);
+  if (e == -2) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
   const uint8_t* W = shared ? d.sw2 : d.w2 + (size_t)e * H * I;
   const float* S =
@@ -829,19 +862,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W + ((size_t)(n0 >> 4) * NSTG << 11)), (short)0, kDnCT * NSTG << 11, 0x00020000);
   v4i B[kDnCT][NSTG][2];
-  auto issue_weights = [&]() {
+  auto issue_weights = [&](auto c0c) {  // the tile pair c0, c0 + 1
+    constexpr int C0 = decltype(c0c)::value;
 #pragma unroll
-    for (int ct = 0; ct < kDnCT; ++ct)
+    for (int ct = C0; ct < C0 + 2; ++ct)
 #pragma unroll
       for (int s = 0; s < NSTG; ++s) {
         B[ct][s][0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, (ct * NSTG + s) << 11, 2);
         B[ct][s][1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, ((ct * NSTG + s) << 11) + 1024, 2);
       }
   };
-  // the token list comes first: the first group's h rows are loaded before the weights, so their
-  // quantization overlaps the weight stream (vector loads complete in issue order)
-  int e_chk;
-  const int cnt = unit_slots(d, unit, slots, wtot, &e_chk);
+  // the token list is requested and the first tile pair's weights go out as soon as the expert is
+  // known, then the first group's h rows, then the second pair: the rows' quantization waits for
+  // the first pair only and overlaps the second (vector loads complete in issue order)
+  const SlotReq req = slots_request(d, unit, e);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_weights(std::integral_constant<int, 0>{});
+  __builtin_amdgcn_sched_barrier(0);
+  const int cnt = slots_finish(d, unit, e, req, slots, wtot);
   if (cnt == 0) return;
   // weight scales: e4m3 per 128x128 block (the wave's 64 rows sit in one block row), int8 per row
   float wsc[NSTG], snv = 0.f;
@@ -876,7 +914,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (!shared)
         wv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(trs, wok ? slots[g0 + tid] * 4 : tbytes, 0, 0));
       if constexpr (FIRST) {
-        issue_weights();
+        issue_weights(std::integral_constant<int, 2>{});
         if constexpr (DT != Q36_MOE_FP8) sn[tid] = snv;
       }
 #pragma unroll
