@@ -153,6 +153,23 @@ def test_moe_config1_int8_full(q36, oracle_mod, dev):
     assert np.array_equal(bits16(out), r["out"])
 
 
+@pytest.mark.parametrize("M,dtype", [(64, 1), (128, 0)])
+def test_moe_unskewed_many_units(q36, oracle_mod, dev, M, dtype):
+    """An unskewed router at 512 experts: several hundred active units (more active expert workgroups
+    than the chip holds at once), int8 bit-exact and e4m3 within the bar."""
+    print(f"moe unskewed M={M} dtype={dtype}", flush=True)
+    out, v, dbg, r, _ = _run_moe(q36, oracle_mod, dev, M, 512, dtype, seed=11)
+    assert np.array_equal(np_(v["ids"]), r["ids"])
+    n_units = len(np.unique(r["ids"])) + 1
+    assert n_units * 8 > 512, f"only {n_units} units: the case does not exceed one round of workgroups"
+    if dtype == q36.Q36_MOE_INT8:
+        assert np.array_equal(np_(dbg["acc2"]), r["acc2"]), "down int32 accumulators differ"
+        assert np.array_equal(bits16(out), r["out"]), "W8A8 output is expected bit-exact"
+    else:
+        wo, ao, eo = assert_bf16_close(bits16(out), r["out"], 1e-2, "fp8 out")
+        print(f"unskewed fp8 out: row err {wo:.2e} elem {ao:.2e} exact fraction {eo:.4f}", flush=True)
+
+
 def test_moe_config2_fp8_full(q36, oracle_mod, dev):
     """Config 2: e4m3 block-scaled, batch 64, 512 experts top-10, Zipf(1.1)-skewed router."""
     out, v, dbg, r, _ = _run_moe(q36, oracle_mod, dev, 64, 512, 1, seed=0, zipf=1.1)
