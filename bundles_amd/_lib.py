@@ -32,7 +32,7 @@ class MoeArgs(C.Structure):
 
 class MoeWsLayout(C.Structure):
     _fields_ = [(n, SZ) for n in ("logits", "ids", "wts", "counts", "offsets", "perm", "inv_perm", "active", "ctl",
-                                  "xq", "xs", "h", "y", "ecount", "eact", "elist", "total")]
+                                  "xq", "xs", "h", "y", "ecount", "eact", "elist", "tblocks", "total")]
 
 
 class GdnArgs(C.Structure):

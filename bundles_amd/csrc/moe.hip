@@ -65,6 +65,8 @@ struct MoeDev {
   int32_t* ecount;  // tokens per expert, counted by route_topk (zeroed by route_logits)
   int32_t* eact;    // experts with tokens, in the order route_topk met them; ctl[2] counts them
   int32_t* elist;   // [E][M] slots of each expert, in the order route_topk met them
+  int32_t* tblocks;  // routed 64-token blocks past an expert's first: e | j << 16; ctl[4] counts them
+  int nsh;          // the shared expert's 64-token blocks past its first: ceil(M / 64) - 1
   uint8_t* xq;
   float* xs;
   uint16_t* h;
@@ -197,7 +199,10 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
   const int tid = threadIdx.x;
   if (t == 0) {
     for (int e = tid; e < d.E; e += 256) d.ecount[e] = 0;  // route_topk counts into them next
-    if (tid == 0) d.ctl[2] = 0;
+    if (tid == 0) {
+      d.ctl[2] = 0;
+      d.ctl[4] = 0;
+    }
   }
   const int nr = d.H / 2048 > 0 ? d.H / 2048 : 1;
   __shared__ float red[4];
@@ -352,6 +357,8 @@ __global__ __launch_bounds__(256) void route_topk_kernel(MoeDev d) {
     const int pos = atomicAdd(&d.ecount[my_id], 1);
     d.elist[(size_t)my_id * d.M + pos] = t * k + lane;
     if (pos == 0) d.eact[atomicAdd(&d.ctl[2], 1)] = my_id;
+    // every 64th token of an expert opens one more 64-token block for the expert kernels
+    if (pos > 0 && (pos & 63) == 0) d.tblocks[atomicAdd(&d.ctl[4], 1)] = my_id | ((pos >> 6) << 16);
   }
 }
 
@@ -551,6 +558,40 @@ __device__ __forceinline__ int unit_expert(const MoeDev& d, int unit) {
   if (unit == 0) return -1;
   return unit - 1 < nact ? e : -2;
 }
+// The work item of expert-kernel workgroup b (8 consecutive workgroups per item, one per slice, on
+// the 8 XCDs): the first (E + 1) * 8 take token block 0 (tokens 0 .. 63 of the unit's list) of unit
+// b / 8; the ones after take block j >= 1 of a unit with more than 64 tokens -- first the shared
+// expert's blocks 1 .. nsh, then the routed blocks route_topk listed (idle past its count), so a hot
+// expert's tokens are spread over as many workgroups as it has 64-token blocks.  e: -2 idle, -1 the
+// shared expert, else the expert; unit 0 is the shared expert.
+struct WorkItem {
+  int unit, e, tb, grp;
+};
+__device__ __forceinline__ WorkItem work_item(const MoeDev& d) {
+  const int b = blockIdx.x, nprim = (d.E + 1) * 8;
+  WorkItem it;
+  it.grp = b & 7;
+  if (b < nprim) {
+    it.unit = b >> 3;
+    it.tb = 0;
+    it.e = unit_expert(d, it.unit);
+    return it;
+  }
+  const int x = (b - nprim) >> 3;
+  if (x < d.nsh) {
+    it.unit = 0;
+    it.tb = 1 + x;
+    it.e = -1;
+    return it;
+  }
+  const int n = d.ctl[4];
+  const int ent = d.tblocks[x - d.nsh];  // the grid holds at most M * k / 64 routed blocks, fewer than E
+  asm volatile("" ::"s"(n), "s"(ent));  // both loads issued before either is tested
+  it.unit = 1;
+  it.e = x - d.nsh < n ? (ent & 0xffff) : -2;
+  it.tb = ent >> 16;
+  return it;
+}
 __device__ __forceinline__ int slot_token(const MoeDev& d, int s) {
   const int S = d.M * d.k;
   return s >= S ? s - S : s / d.k;
@@ -596,10 +637,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ float ws_l[(2 * I / 128) * NSTG];               // [2I/128][NSTG]
   __shared__ int slots[kMaxM];
   __shared__ int wtot[4];
-  const int unit = blockIdx.x / kUpGroups, grp = blockIdx.x % kUpGroups;
+  static_assert(kUpGroups == 8, "8 workgroups per work item");
+  const WorkItem it = work_item(d);
+  if (it.e == -2) return;
+  const int unit = it.unit, grp = it.grp, e = it.e, g0 = 64 * it.tb;
   const bool shared = unit == 0;
-  const int e = unit_expert(d, unit);
-  if (e == -2) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
   const uint8_t* W = shared ? d.sw13 : d.w13 + (size_t)e * 2 * I * H;
   const float* S = shared ? d.ss13
@@ -632,7 +674,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int s = 0; s < kUpD; ++s) issue(s, s);
   __builtin_amdgcn_sched_barrier(0);
   const int cnt = slots_finish(d, unit, e, req, slots, wtot);
-  if (cnt == 0) return;
+  if (cnt <= g0) return;
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)d.xq, (short)0, d.M * H, 0x00020000);
   constexpr int NXS = DT == Q36_MOE_FP8 ? NSTG : 1;  // activation scales per token
@@ -692,7 +734,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       constexpr int NW = (2 * I / 128) * NSTG;
       static_assert(NW <= 256, "one weight scale per thread");
       const __amdgpu_buffer_rsrc_t wss = __builtin_amdgcn_make_buffer_rsrc((void*)S, (short)0, NW * 4, 0x00020000);
-      wsr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wss, g0 == 0 && tid < NW ? tid * 4 : NW * 4, 0, 0));
+      wsr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wss, tid < NW ? tid * 4 : NW * 4, 0, 0));
     }
     rows_dma(0);
     if constexpr (!FIRST) {
@@ -702,7 +744,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int q = 0; q < TG * NSTG / 256; ++q) xs_t[tid + 256 * q] = xsr[q];
     if constexpr (DT == Q36_MOE_FP8)
-      if (g0 == 0 && tid < (2 * I / 128) * NSTG) ws_l[tid] = wsr;
+      if (tid < (2 * I / 128) * NSTG) ws_l[tid] = wsr;
     // the rows (and for later groups not the weights, requested after them; the first group's
     // weights are older than the rows)
     if constexpr (FIRST)
@@ -805,20 +847,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
   };
-  // two tile counts: one tile (most experts at decode sizes) or four (rows past the tokens are
-  // zero); a third instance would cost registers in all of them
-  if (cnt <= 16) {
-    group(0, std::integral_constant<int, 1>{}, std::true_type{});
-  } else {
-    group(0, std::integral_constant<int, 4>{}, std::true_type{});
-    for (int g0 = TG; g0 < cnt; g0 += TG) {
-      __syncthreads();  // the previous group's epilogue has read xs_t
-      if (cnt - g0 <= 16)
-        group(g0, std::integral_constant<int, 1>{}, std::false_type{});
-      else
-        group(g0, std::integral_constant<int, 4>{}, std::false_type{});
-    }
-  }
+  // the work item's token block, as one tile (most experts at decode sizes) or four (rows past the
+  // tokens are zero); a third instance would cost registers in all of them
+  if (cnt - g0 <= 16)
+    group(g0, std::integral_constant<int, 1>{}, std::true_type{});
+  else
+    group(g0, std::integral_constant<int, 4>{}, std::true_type{});
 }
 
 // ------------------------------------------------------------------------------------------
@@ -848,10 +882,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ float hs[kDnTG][NSTG];      // activation scales per row (e4m3: per 128-group)
   __shared__ float wl[kDnTG];            // routing weight per row of the group
   __shared__ __align__(16) float sn[4 * kDnRows];  // int8 weight scale per output row of the workgroup
-  const int unit = blockIdx.x / kDnGroups, grp = blockIdx.x % kDnGroups;
+  static_assert(kDnGroups == 8, "8 workgroups per work item");
+  const WorkItem it = work_item(d);
+  if (it.e == -2) return;
+  const int unit = it.unit, grp = it.grp, e = it.e, g0 = 64 * it.tb;
   const bool shared = unit == 0;
-  const int e = unit_expert(d, unit);
-  if (e == -2) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
   const uint8_t* W = shared ? d.sw2 : d.w2 + (size_t)e * H * I;
   const float* S =
@@ -880,7 +915,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   issue_weights(std::integral_constant<int, 0>{});
   __builtin_amdgcn_sched_barrier(0);
   const int cnt = slots_finish(d, unit, e, req, slots, wtot);
-  if (cnt == 0) return;
+  if (cnt <= g0) return;
   // weight scales: e4m3 per 128x128 block (the wave's 64 rows sit in one block row), int8 per row
   float wsc[NSTG], snv = 0.f;
   if constexpr (DT == Q36_MOE_FP8) {
@@ -1032,15 +1067,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   };
-  if (cnt <= 16) {
-    group(0, std::integral_constant<int, 1>{}, std::true_type{});
-  } else {
-    group(0, std::integral_constant<int, 4>{}, std::true_type{});
-    for (int g0 = kDnTG; g0 < cnt; g0 += kDnTG) {
-      __syncthreads();  // the previous group's operand reads are done
-      group(g0, std::integral_constant<int, 4>{}, std::false_type{});
-    }
-  }
+  static_assert(kDnTG == 64, "a work item is one 64-token block");
+  if (cnt - g0 <= 16)
+    group(g0, std::integral_constant<int, 1>{}, std::true_type{});
+  else
+    group(g0, std::integral_constant<int, 4>{}, std::true_type{});
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1248,6 +1279,7 @@ int layout(int M, int E, int H, int I, int k, int dtype, q36_moe_ws_layout* L) {
   L->ecount = take(sizeof(int32_t) * E);
   L->eact = take(sizeof(int32_t) * E);
   L->elist = take(sizeof(int32_t) * (size_t)E * M);
+  L->tblocks = take(sizeof(int32_t) * (size_t)E);
   L->xq = take((size_t)M * H);
   L->xs = take(sizeof(float) * (size_t)M * (dtype == Q36_MOE_FP8 ? H / 128 : 1));
   L->h = take(sizeof(uint16_t) * (S + M) * I);
@@ -1292,6 +1324,7 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
               reinterpret_cast<int32_t*>(ws + L.inv_perm), reinterpret_cast<int32_t*>(ws + L.active),
               reinterpret_cast<int32_t*>(ws + L.ctl), reinterpret_cast<int32_t*>(ws + L.ecount),
               reinterpret_cast<int32_t*>(ws + L.eact), reinterpret_cast<int32_t*>(ws + L.elist),
+              reinterpret_cast<int32_t*>(ws + L.tblocks), (a->M + 63) / 64 - 1,
               reinterpret_cast<uint8_t*>(ws + L.xq),
               reinterpret_cast<float*>(ws + L.xs), reinterpret_cast<uint16_t*>(ws + L.h),
               reinterpret_cast<uint16_t*>(ws + L.y), a->dbg_acc13, a->dbg_acc2,
@@ -1322,14 +1355,21 @@ int launch_lists(const MoeDev& d, hipStream_t st) {
   return check_launch("q36_moe_route");
 }
 
+// Expert-kernel grid: 8 workgroups per unit's first 64-token block, then 8 per further block: the
+// shared expert's nsh, and room for every routed one (an expert past 64 tokens only when M > 64; at
+// most M k / 64 blocks in all, fewer than E)
+int expert_grid(const MoeDev& d) {
+  const int nrb = d.M > 64 ? d.M * d.k / 64 : 0;
+  return 8 * (d.E + 1 + d.nsh + nrb);
+}
 template <int DT>
 int launch_up_t(const MoeDev& d, hipStream_t st) {
-  moe_up_kernel<DT><<<(d.E + 1) * kUpGroups, 256, 0, st>>>(d);
+  moe_up_kernel<DT><<<expert_grid(d), 256, 0, st>>>(d);
   return check_launch("q36_moe_up");
 }
 template <int DT>
 int launch_down_t(const MoeDev& d, hipStream_t st) {
-  moe_down_kernel<DT><<<(d.E + 1) * kDnGroups, 256, 0, st>>>(d);
+  moe_down_kernel<DT><<<expert_grid(d), 256, 0, st>>>(d);
   return check_launch("q36_moe_down");
 }
 int launch_up(const MoeDev& d, int dtype, hipStream_t st) {

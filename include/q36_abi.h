@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define Q36_ABI_VERSION 2
+#define Q36_ABI_VERSION 3
 #define Q36_OK 0
 #define Q36_EINVAL 1
 #define Q36_ELAUNCH 2
@@ -123,6 +123,8 @@ typedef struct q36_moe_ws_layout {
   size_t ecount;   /* int32 [E] tokens per expert (route-internal) */
   size_t eact;     /* int32 [E] experts with tokens, unordered (route-internal; ctl[2] counts) */
   size_t elist;    /* int32 [E, M] slots of each expert, unordered (route-internal) */
+  size_t tblocks;  /* int32 [E] 64-token blocks past an expert's first, e | j << 16, unordered
+                    * (route-internal; ctl[4] counts them) */
   size_t total;
 } q36_moe_ws_layout;
 

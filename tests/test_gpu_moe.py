@@ -162,12 +162,33 @@ def test_moe_unskewed_many_units(q36, oracle_mod, dev, M, dtype):
     assert np.array_equal(np_(v["ids"]), r["ids"])
     n_units = len(np.unique(r["ids"])) + 1
     assert n_units * 8 > 512, f"only {n_units} units: the case does not exceed one round of workgroups"
+    _check_out(q36, dtype, dbg, out, r, "unskewed")
+
+
+@pytest.mark.parametrize("M,dtype,padded", [(256, 0, False), (256, 1, False), (200, 0, True)])
+def test_moe_hot_experts_many_blocks(q36, oracle_mod, dev, M, dtype, padded):
+    """Zipf-skewed routing past 64 rows: the hot experts (and the shared expert) hold several 64-token
+    blocks, each taken by its own expert workgroups."""
+    print(f"moe hot experts M={M} dtype={dtype} padded={padded}", flush=True)
+    out, v, dbg, r, pos = _run_moe(q36, oracle_mod, dev, M, 512, dtype, seed=21, zipf=1.1, padded=padded)
+    assert np.array_equal(np_(v["ids"]), r["ids"])
+    ids = r["ids"][r["ids"] >= 0]
+    top = np.bincount(ids, minlength=512).max()
+    assert top > 128, f"the hottest expert has {top} tokens: fewer than three 64-token blocks"
+    if padded:
+        assert not bits16(out)[np_(pos) == 0].any(), "padded rows must be zero"
+    _check_out(q36, dtype, dbg, out, r, "hot experts", accs=not padded)
+
+
+def _check_out(q36, dtype, dbg, out, r, what, accs=True):
     if dtype == q36.Q36_MOE_INT8:
-        assert np.array_equal(np_(dbg["acc2"]), r["acc2"]), "down int32 accumulators differ"
+        if accs:  # (padded rows' slots hold nothing on either side only for the output)
+            assert np.array_equal(np_(dbg["acc13"]), r["acc13"]), "up int32 accumulators differ"
+            assert np.array_equal(np_(dbg["acc2"]), r["acc2"]), "down int32 accumulators differ"
         assert np.array_equal(bits16(out), r["out"]), "W8A8 output is expected bit-exact"
     else:
         wo, ao, eo = assert_bf16_close(bits16(out), r["out"], 1e-2, "fp8 out")
-        print(f"unskewed fp8 out: row err {wo:.2e} elem {ao:.2e} exact fraction {eo:.4f}", flush=True)
+        print(f"{what} fp8 out: row err {wo:.2e} elem {ao:.2e} exact fraction {eo:.4f}", flush=True)
 
 
 def test_moe_config2_fp8_full(q36, oracle_mod, dev):
