@@ -236,9 +236,12 @@ def moe_phases(x, positions, router_w, gate_w, ew: ExpertWeights, topk: int, ws:
     returns the list of (name, callable) so a caller can schedule or time each one."""
     a = _args(x, positions, router_w, gate_w, ew, topk, ws, out, router_bias, None)
     L = _lib.lib()
+    # the argument struct holds raw device addresses: the callables keep the tensors they point into
+    # alive, so a caller that drops its own references does not leave them pointing at freed memory
+    keep = (x, positions, router_w, gate_w, ew, ws, out, router_bias)
 
     def call(fn, name):
-        def run():
+        def run(_keep=keep):
             check(fn(C.byref(a), _lib.stream_handle(stream)), name)
         return run
     return [("route", call(L.q36_moe_route, "q36_moe_route")), ("up", call(L.q36_moe_up, "q36_moe_up")),
