@@ -266,7 +266,10 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
       tmax[rt] = fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1])) * sl2;
       need |= tmax[rt] > m[rt] + kLazy;
     }
-    if (__builtin_amdgcn_ballot_w64(need)) {
+    // Rare (a row max grew past its reference by 2^8), and marked so: with the branch at its default
+    // weight the compiler placed the output accumulators' AGPR -> VGPR copies for it above the branch,
+    // some 120 copies every step.
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(need) != 0, 0)) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         const float mn = fmaxf(m[rt], tmax[rt]);
