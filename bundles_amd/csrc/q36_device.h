@@ -22,12 +22,14 @@ __device__ __forceinline__ float bf2f(uint32_t h16) { return __uint_as_float(h16
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// float -> bf16 bits, round to nearest even (NaN kept quiet).
+// float -> bf16 bits, round to nearest even (NaN kept quiet, sign and high payload kept).  Both
+// results are computed and one selected: written as an early return for NaN, the compiler emitted a
+// divergent branch (exec-mask save and restore) around every rounding.
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t q = (u >> 16) | 0x40u;
+  return (u & 0x7fffffffu) > 0x7f800000u ? q : r;
 }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 // The same rounding for finite values by one v_cvt_pk_bf16_f32 (round to nearest even); NaN becomes
