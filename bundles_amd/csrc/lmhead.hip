@@ -141,6 +141,14 @@ __device__ __forceinline__ int bswz(int c, int kc) { return c * kBK + ((kc ^ ((c
 template <int N>
 using ic = std::integral_constant<int, N>;
 
+// threadIdx.x through an empty asm: values derived from it are recomputed where they are used
+// instead of being kept (or spilled) across the K loop
+__device__ __forceinline__ int opaque_tid() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 
 // s_waitcnt with only the vector-memory count constrained (gfx9 encoding: vmcnt bits 3:0 and 15:14).
 template <int N>
@@ -243,8 +251,9 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
         (void*)(d.ws + t.v0), (short)0, min(d.V - t.v0, kBN) * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(d.xs + t.r0), (short)0, min(d.Rs - t.r0, kBM) * 4, 0x00020000);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, &sc_l[par][0][64 * wv], 4, 4 * lane + 256 * wv, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, &sc_l[par][1][64 * wv], 4, 4 * lane + 256 * wv, 0, 0, 0);
+    const int so = 4 * (opaque_tid() & 63) + 256 * wv;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ws, &sc_l[par][0][64 * wv], 4, so, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xs, &sc_l[par][1][64 * wv], 4, so, 0, 0, 0);
   };
   // Fragments: lane l reads tile row 32 t + l % 32, K bytes 16 (l / 32) of each 32-byte half step
   // (LDS chunk 2 h + l / 32); the MFMA gives lane l token l % 32 and vocab rows
@@ -334,6 +343,35 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     const Tile tn = more ? tile(j) : t;
+#pragma unroll
+    for (int k = 0; k < NMF; ++k) mfma_one(ic<1>{}, F_{}, k);
+    // The lane's indices are derived afresh from the thread id here: values computed before the K
+    // loop and kept across it were spilled (the loop holds 224 of the 256 registers), and their
+    // reloads, queued behind the next tile's loads, held the epilogue until those loads landed.
+    // One term: this tile's scales go into registers (the fragment registers are free by now)
+    // before the next tile's scale loads are issued, since a read of the scale buffer after them
+    // waits for them.  Two terms: the 64 registers this takes made the K loop spill, and the
+    // epilogue reads the buffer (and waits for the next tile's scales).
+    const int et = opaque_tid(), ewm = (et >> 6) >> 1, ewn = (et >> 6) & 1, el32 = et & 31, elh = (et >> 5) & 1;
+    constexpr int NTB = X2 ? TB / 2 : TB;
+    constexpr bool kRegScales = !X2;
+    float4 wsr[kRegScales ? VB : 1][4];
+    auto wscale = [&](int vi, int jg) {
+      return *reinterpret_cast<const float4*>(&sc_l[par][0][ewn * 128 + vi * 32 + 8 * jg + 4 * elh]);
+    };
+    float xsr[NTB], xs2[NTB];
+    if constexpr (kRegScales) {
+#pragma unroll
+      for (int vi = 0; vi < VB; ++vi)
+#pragma unroll
+        for (int jg = 0; jg < 4; ++jg) wsr[vi][jg] = wscale(vi, jg);
+#pragma unroll
+      for (int tb = 0; tb < NTB; ++tb) {
+        xsr[tb] = sc_l[par][1][ewm * TW + tb * 32 + el32];
+        xs2[tb] = 0.f;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
     if (more) {
       issue_scales(tn, par ^ 1);
 #pragma unroll
@@ -346,8 +384,6 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
       for (int i = 0; i < CPW; ++i) issue_step(tn, 3, ic<3>{}, i);
     }
     asm volatile("" ::: "memory");
-#pragma unroll
-    for (int k = 0; k < NMF; ++k) mfma_one(ic<1>{}, F_{}, k);
     // Epilogue: lane l holds tokens r0 + wm*TW + 32 ti + l % 32 and, per token, vocab columns
     // cb + 32 vi + 8 (j / 4) + 4 (l / 32) + j % 4, visited in increasing order.  Each logit
     // (acc * xs) * ws is rounded to bf16 once (hardware round-to-nearest-even); the lane keeps the
@@ -356,21 +392,23 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     // it with lane l ^ 32 and the other column wave through LDS, and the tile's best per row goes
     // out as one 64-bit atomic max.  Columns past V are skipped (nin: the lane's columns in range,
     // counted from its first; V % 16 == 0 keeps each group of 4 all in or all out).
-    const float* wsl = sc_l[par][0];
-    const float* xsl = sc_l[par][1];
-    const int nin = d.V - t.v0 - (wn * 128 + 4 * lh);
+    const int nin = d.V - t.v0 - (ewn * 128 + 4 * elh);
     // One term: token block ti is rows wm*TW + 32 ti of the tile.  Two terms: blocks 2b and 2b + 1
     // hold the two terms of the same 32 tokens (act_row), token wm*TW/2 + 32 b + l32 of the tile.
-    constexpr int NTB = X2 ? TB / 2 : TB;
     const int tok0 = X2 ? t.r0 / 2 : t.r0;
+    if constexpr (!kRegScales) {
+#pragma unroll
+      for (int tb = 0; tb < NTB; ++tb) {
+        xsr[tb] = sc_l[par][1][ewm * TW + 2 * tb * 32 + el32];
+        xs2[tb] = sc_l[par][1][ewm * TW + (2 * tb + 1) * 32 + el32];
+      }
+    }
     {
 #pragma unroll
       for (int tb = 0; tb < NTB; ++tb) {
         const int ti = X2 ? 2 * tb : tb;
-        const int rl = X2 ? wm * (TW / 2) + tb * 32 + l32 : wm * TW + ti * 32 + l32;  // token of the tile
+        const int rl = X2 ? ewm * (TW / 2) + tb * 32 + el32 : ewm * TW + ti * 32 + el32;  // token of the tile
         const int row = tok0 + rl;
-        const float xsr = xsl[wm * TW + ti * 32 + l32];
-        const float xs2 = X2 ? xsl[wm * TW + (ti + 1) * 32 + l32] : 0.f;
         float bv = -__builtin_inff();
         int bi = 0;  // column offset from cbase
 #pragma unroll
@@ -378,18 +416,20 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
 #pragma unroll
           for (int jg = 0; jg < 4; ++jg) {
             const int co = vi * 32 + 8 * jg;
-            const int cl = wn * 128 + co + 4 * lh;  // first of the lane's 4 columns, in the tile
-            const float4 w4 = *reinterpret_cast<const float4*>(&wsl[cl]);
+            const int cl = ewn * 128 + co + 4 * elh;  // first of the lane's 4 columns, in the tile
+            float4 w4;
+            if constexpr (kRegScales) w4 = wsr[vi][jg];
+            else w4 = wscale(vi, jg);
             const float wq[4] = {w4.x, w4.y, w4.z, w4.w};
             float lg[4];
             const bool in = co < nin;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               if constexpr (X2)
-                lg[q] = rbf_hw(__builtin_fmaf((float)acc[vi][ti][4 * jg + q], xsr,
-                                                  (float)acc[vi][ti + 1][4 * jg + q] * xs2) * wq[q]);
+                lg[q] = rbf_hw(__builtin_fmaf((float)acc[vi][ti][4 * jg + q], xsr[tb],
+                                                  (float)acc[vi][ti + 1][4 * jg + q] * xs2[tb]) * wq[q]);
               else
-                lg[q] = rbf_hw(((float)acc[vi][ti][4 * jg + q] * xsr) * wq[q]);
+                lg[q] = rbf_hw(((float)acc[vi][ti][4 * jg + q] * xsr[tb]) * wq[q]);
               if (in && lg[q] > bv) bv = lg[q], bi = co + q;
             }
             if constexpr (STORE)
@@ -400,16 +440,23 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
           }
         uint32_t b16 = __float_as_uint(bv + 0.f) >> 16;
         b16 = (b16 & 0x8000u) ? (~b16 & 0xffffu) : (b16 | 0x8000u);
-        uint32_t best = (b16 << 16) | (0xffffu - (uint32_t)(wn * 128 + 4 * lh + bi));
-        best = max(best, (uint32_t)__shfl_xor((int)best, 32));
-        if (lh == 0) rkey[wn][rl] = best;
+        uint32_t best = (b16 << 16) | (0xffffu - (uint32_t)(ewn * 128 + 4 * elh + bi));
+        // lane l and l ^ 32 exchange by v_permlane32_swap (a shuffle would keep the lane id live,
+        // or spilled, across the K loop)
+        const auto bsw = __builtin_amdgcn_permlane32_swap(best, best, false, false);
+        best = max(bsw[0], bsw[1]);
+        if (elh == 0) rkey[ewn][rl] = best;
       }
     }
-    __syncthreads();
-    if (tid < (X2 ? kBM / 2 : kBM) && tok0 + tid < d.R) {
-      const uint32_t k = max(rkey[0][tid], rkey[1][tid]);
+    // LDS-only barrier for the key exchange: a full __syncthreads also waits for the next tile's
+    // loads in flight
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (et < (X2 ? kBM / 2 : kBM) && tok0 + et < d.R) {
+      const uint32_t k = max(rkey[0][et], rkey[1][et]);
       const uint32_t col = (uint32_t)t.v0 + (0xffffu - (k & 0xffffu));
-      atomicMax(&d.keys[tok0 + tid], ((unsigned long long)(k >> 16) << 32) | (unsigned long long)(0xffffffffu - col));
+      atomicMax(&d.keys[tok0 + et], ((unsigned long long)(k >> 16) << 32) | (unsigned long long)(0xffffffffu - col));
     }
     if (!more) break;
     t = tn;
