@@ -521,15 +521,20 @@ __device__ __forceinline__ SlotReq slots_request(const MoeDev& d, int unit, int 
       __builtin_amdgcn_make_buffer_rsrc((void*)(d.elist + (size_t)e * d.M), (short)0, lbytes, 0x00020000);
   return SlotReq{(int)__builtin_amdgcn_raw_buffer_load_b32(lrs, tid < d.M ? tid * 4 : lbytes, 0, 0)};
 }
+// toks (when given) receives each slot's token row, one division per thread here instead of one per
+// row copy later
 __device__ __forceinline__ int slots_finish(const MoeDev& d, int unit, int e, const SlotReq& r, int* slots,
-                                            int* wtot) {
+                                            int* wtot, int* toks) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (unit != 0) {
     // the expert's count by a scalar load through the constant address space (the expert kernels
     // never write ecount; a plain load here is compiled as a vector load, which would complete
     // behind the weights); issued here, after the caller's weight loads, it does not hold them up
     const int cnt = ((const __attribute__((address_space(4))) int*)(d.ecount))[e];
-    if (tid < cnt) slots[tid] = r.v;
+    if (tid < cnt) {
+      slots[tid] = r.v;
+      if (toks) toks[tid] = r.v / d.k;  // a routed slot is token * k + pick
+    }
     __syncthreads();
     return cnt;
   }
@@ -544,7 +549,10 @@ __device__ __forceinline__ int slots_finish(const MoeDev& d, int unit, int e, co
     base += w < wave ? wtot[w] : 0;
     tot += wtot[w];
   }
-  if (my >= 0) slots[base + below] = my;
+  if (my >= 0) {
+    slots[base + below] = my;
+    if (toks) toks[base + below] = tid;
+  }
   __syncthreads();
   return tot;
 }
@@ -592,10 +600,6 @@ __device__ __forceinline__ WorkItem work_item(const MoeDev& d) {
   it.tb = ent >> 16;
   return it;
 }
-__device__ __forceinline__ int slot_token(const MoeDev& d, int s) {
-  const int S = d.M * d.k;
-  return s >= S ? s - S : s / d.k;
-}
 
 constexpr int kMoeH = 2048, kMoeI = 512;
 
@@ -636,6 +640,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __align__(16) float xs_t[TG * NSTG];            // [NSTG][TG] (token fastest)
   __shared__ float ws_l[(2 * I / 128) * NSTG];               // [2I/128][NSTG]
   __shared__ int slots[kMaxM];
+  __shared__ int toks[kMaxM];  // token row of each slot
   __shared__ int wtot[4];
   static_assert(kUpGroups == 8, "8 workgroups per work item");
   const WorkItem it = work_item(d);
@@ -673,7 +678,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
   for (int s = 0; s < kUpD; ++s) issue(s, s);
   __builtin_amdgcn_sched_barrier(0);
-  const int cnt = slots_finish(d, unit, e, req, slots, wtot);
+  const int cnt = slots_finish(d, unit, e, req, slots, wtot, toks);
   if (cnt <= g0) return;
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)d.xq, (short)0, d.M * H, 0x00020000);
@@ -698,25 +703,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     static_assert(BUFB <= kUpBuf0 && (NC == 1 || BUFB <= kUpBuf1), "activation rows exceed their buffers");
     static_assert(NC == 1 || kUpD <= SPC, "a chunk must issue a full window of weight stages");
     using Acc = typename std::conditional<DT == Q36_MOE_FP8, v4f, v4i>::type;
-    // chunk c of the group's rows into its buffer by buffer DMA (rows past the group read as zero)
+    // The byte offset of each row this lane copies (its token row, or past the activations for rows
+    // past the group, which read as zero), formed once for all chunks.  The token reads are made
+    // unconditional: left to the compiler they sat in branches, one LDS round trip per copy.
+    // One tile: wave w copies rows w, w + 4, ..., 1 KB per call (lane l: bytes 16 l ..).  Four
+    // tiles: one call fills two rows (lanes 0-31 row 2m, lanes 32-63 row 2m + 1), wave w takes the
+    // row pairs w, w + 4, ..., and a lane fetches the piece that belongs at its position.
+    constexpr int NRC = NC == 1 ? 4 : 8 * NTT / 4;
+    int rowoff[NRC];
+#pragma unroll
+    for (int k = 0; k < NRC; ++k) {
+      const int rr = NC == 1 ? wave + 4 * k : 2 * (wave + 4 * k) + (lane >> 5), ti = g0 + rr;
+      int tk = toks[ti & (kMaxM - 1)];
+      asm volatile("" : "+v"(tk));
+      rowoff[k] = ti < cnt ? tk * H : d.M * H;
+    }
+    // chunk c of the group's rows into its buffer by buffer DMA
     auto rows_dma = [&](int c) {
       if constexpr (NC == 1) {
-        // wave w copies rows w, w + 4, ..., 1 KB per call (lane l: bytes 16 l ..)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const int rr = wave + 4 * k, ti = g0 + rr;
-          const int voff = ti < cnt ? slot_token(d, slots[ti]) * H + lane * 16 : d.M * H;
+          const int rr = wave + 4 * k;
+          const int voff = rowoff[k] < d.M * H ? rowoff[k] + lane * 16 : d.M * H;
 #pragma unroll
           for (int h = 0; h < KC / 1024; ++h) dma16(xrs, a_b0 + rr * ROWB + h * 1024, voff + h * 1024);
         }
       } else {
-        // one call fills two rows (lanes 0-31 row 2m, lanes 32-63 row 2m + 1); wave w takes the
-        // row pairs w, w + 4, ...; a lane fetches the piece that belongs at its position
         uint8_t* buf = (c & 1) ? a_b1 : a_b0;
 #pragma unroll
-        for (int k = 0; k < 8 * NTT / 4; ++k) {
-          const int m = wave + 4 * k, rr = 2 * m + (lane >> 5), ti = g0 + rr, p = lane & 31;
-          const int voff = ti < cnt ? slot_token(d, slots[ti]) * H + c * KC + 16 * (p ^ (rr & 15)) : d.M * H;
+        for (int k = 0; k < NRC; ++k) {
+          const int m = wave + 4 * k, rr = 2 * m + (lane >> 5), p = lane & 31;
+          const int voff = rowoff[k] < d.M * H ? rowoff[k] + c * KC + 16 * (p ^ (rr & 15)) : d.M * H;
           dma16(xrs, buf + 2 * m * KC, voff);
         }
       }
@@ -727,7 +744,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int q = 0; q < TG * NSTG / 256; ++q) {
       const int i = tid + 256 * q, ti = g0 + i % TG, sx = i / TG;
-      const int off = ti < cnt && sx < NXS ? (slot_token(d, slots[ti]) * NXS + sx) * 4 : xsbytes;
+      int tk = toks[ti & (kMaxM - 1)];
+      asm volatile("" : "+v"(tk));
+      const int off = ti < cnt && sx < NXS ? (tk * NXS + sx) * 4 : xsbytes;
       xsr[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, off, 0, 0));
     }
     if constexpr (DT == Q36_MOE_FP8) {
@@ -914,7 +933,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __builtin_amdgcn_sched_barrier(0);
   issue_weights(std::integral_constant<int, 0>{});
   __builtin_amdgcn_sched_barrier(0);
-  const int cnt = slots_finish(d, unit, e, req, slots, wtot);
+  const int cnt = slots_finish(d, unit, e, req, slots, wtot, nullptr);
   if (cnt <= g0) return;
   // weight scales: e4m3 per 128x128 block (the wave's 64 rows sit in one block row), int8 per row
   float wsc[NSTG], snv = 0.f;
