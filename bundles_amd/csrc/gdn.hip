@@ -54,7 +54,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   const int unit = blockIdx.x;
   const int bq = unit / GHV, hv = unit % GHV, hk = hv / 2;
   const int T = d.T;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r0 = tid >> 3, c8 = tid & 7;
   // state register j (< 8): row r0 + 64 (j / 4), columns 32 (j % 4) + 4 c8 .. +3
   auto soff = [&](int j) { return (r0 + 64 * (j >> 2)) * GK + 32 * (j & 3) + 4 * c8; };
