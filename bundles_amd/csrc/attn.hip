@@ -13,6 +13,9 @@
 // Kernels: act_quant (bf16 -> e4m3 + scales, optionally gated), proj_gemm (each wave streams two
 // 16-row weight tiles over K from HBM; the token group's activations come through an LDS chunk
 // ring shared by the workgroup), norm_rope (one wave per token and head).
+#include <type_traits>
+#include <utility>
+
 #include "q36_device.h"
 #include "q36_host.h"
 
@@ -391,6 +394,195 @@ ks_gemm_kernel(GemmDev g) {
 }
 
 // ------------------------------------------------------------------------------------------
+// Tiled e4m3 projection GEMM for 64 tokens and more: the same Y = bf16(sum_kb blocksum_kb(t, n) *
+// xs[t, kb] * ws[n / 128, kb]) (running sums fma(blocksum, xs * ws, acc) in increasing kb order from
+// zero, so the bits equal the streaming and K-sliced GEMMs'), with both operands in MFMA fragment
+// order (the weights as packed, the activations from act_quant's fragment mode).
+// Workgroup = one 128-row block (one weight scale per K block) x BT tokens, 8 waves, two a SIMD:
+// wave w owns row tiles 4 (w & 1) .. +3 and token tiles TTW (w >> 1) .. +TTW-1 (TTW = BT / 64).  K
+// goes in 128-byte steps (one K block, one MFMA deep) through a 4-stage LDS ring that buffer loads
+// fill straight from global memory, four steps ahead; a stage holds the block's 8 weight tiles and
+// BT / 16 token tiles, 2 KB each, exactly as they lie in memory.  The fragments (and scales) of step
+// s + 1 are read while the MFMAs of step s run.  Per call every weight byte passes through L2
+// ceil(T / BT) times and every activation byte N / 128 times (the streaming GEMM's 16- or 32-token
+// groups re-read the weights T / 16 or T / 32 times).
+// ------------------------------------------------------------------------------------------
+template <int N>
+using ic = std::integral_constant<int, N>;
+// s_waitcnt with only the vector-memory count constrained (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+template <int N>
+__device__ __forceinline__ void tg_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// f(ic<0>{}), f(ic<1>{}), ... in order, each step's index a compile-time constant
+template <typename F, int... KS>
+__device__ __forceinline__ void for_steps(F& f, std::integer_sequence<int, KS...>) {
+  (f(ic<KS>{}), ...);
+}
+template <int BT, int NKB>
+__device__ __forceinline__ void tile_gemm_body(const GemmDev& g) {
+  constexpr int WB = 8 * 2048, AB = (BT / 16) * 2048;  // stage bytes: weight tiles, token tiles
+  constexpr int NCH = (WB + AB) / 1024, LPS = NCH / 8;  // 1 KB copies a stage, per wave
+  constexpr int TTW = BT / 64;
+  static_assert(NCH % 8 == 0 && NKB >= 4 && TTW >= 1, "tile shape");
+  // one object per stage and operand: the compiler tracks the buffer-to-LDS loads of each apart
+  __shared__ __align__(1024) uint8_t w_s0[WB], w_s1[WB], w_s2[WB], w_s3[WB];
+  __shared__ __align__(1024) uint8_t a_s0[AB], a_s1[AB], a_s2[AB], a_s3[AB];
+  __shared__ __align__(16) float xs_l[NKB * BT];  // [kb][token of the tile]
+  __shared__ float ws_l[NKB];
+  auto w_st = [&](auto st) -> uint8_t* {
+    if constexpr (decltype(st)::value == 0) return w_s0;
+    else if constexpr (decltype(st)::value == 1) return w_s1;
+    else if constexpr (decltype(st)::value == 2) return w_s2;
+    else return w_s3;
+  };
+  auto a_st = [&](auto st) -> uint8_t* {
+    if constexpr (decltype(st)::value == 0) return a_s0;
+    else if constexpr (decltype(st)::value == 1) return a_s1;
+    else if constexpr (decltype(st)::value == 2) return a_s2;
+    else return a_s3;
+  };
+  // XCD-aware order: workgroup b runs on XCD b % 8, which owns the row blocks rb = xcd (mod 8) with
+  // every token group of each, so a weight block is fetched into one L2 for all its token groups
+  const int nrb = g.N / 128, ntg = (g.T + BT - 1) / BT;
+  const int xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
+  const int rb = xcd + 8 * (jj / ntg);
+  if (rb >= nrb) return;
+  const int t0 = (jj % ntg) * BT;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), wr = wv & 1, wt = wv >> 1;
+  // token tiles of this group that exist (act_quant pads T to whole tiles); the rest read as zero:
+  // the tile offset rides in the VGPR offset, which the buffer range check covers
+  const int Tq = (g.T + 15) & ~15, ntile = min(BT, Tq - t0) >> 4;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g.W + (size_t)rb * 8 * NKB * 2048), (short)0, 8 * NKB * 2048, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g.A + (size_t)(t0 >> 4) * NKB * 2048), (short)0, ntile * NKB * 2048, 0x00020000);
+  // copy i of this wave for step ks: 1 KB chunk q = LPS w + i of the stage (weight tile q / 2 half
+  // q % 2, then the token tiles' halves)
+  auto dma = [&](bool wpart, uint8_t* lds, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wpart ? wrs : ars, lds, 16, voff, soff, 0, 0);
+  };
+  auto issue = [&](auto st, int ks) {
+#pragma unroll
+    for (int i = 0; i < LPS; ++i) {
+      const int q = wv * LPS + i;
+      if (q < 16) {
+        dma(true, w_st(st) + q * 1024, lane * 16 + (q >> 1) * NKB * 2048 + (q & 1) * 1024, ks * 2048);
+      } else {
+        const int qa = q - 16;
+        dma(false, a_st(st) + qa * 1024, lane * 16 + (qa >> 1) * NKB * 2048 + (qa & 1) * 1024, ks * 2048);
+      }
+    }
+  };
+  // the group's scales: activations [NKB][BT] and the block's weight scales, through registers
+  constexpr int NXS = NKB * BT / 512;
+  const int xsbytes = g.T * NKB * 4;
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc((void*)g.As, (short)0, xsbytes, 0x00020000);
+  float xsr[NXS];
+#pragma unroll
+  for (int q = 0; q < NXS; ++q) {
+    const int i = tid + 512 * q, tt = i % BT, kb = i / BT;
+    const int off = t0 + tt < g.T ? ((t0 + tt) * NKB + kb) * 4 : xsbytes;
+    xsr[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, off, 0, 0));
+  }
+  const float wsv = tid < NKB ? g.Ws[(size_t)rb * NKB + tid] : 0.f;
+  issue(ic<0>{}, 0);
+  issue(ic<1>{}, 1);
+  issue(ic<2>{}, 2);
+  issue(ic<3>{}, 3);
+  tg_wait_vm<3 * LPS>();  // the scales and step 0
+#pragma unroll
+  for (int q = 0; q < NXS; ++q) xs_l[tid + 512 * q] = xsr[q];
+  if (tid < NKB) ws_l[tid] = wsv;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  v4f acc[4][TTW];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int tt = 0; tt < TTW; ++tt) acc[rt][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+  v8i wf[2][4], af[2][TTW];
+  float xw[2][TTW];
+  const int lo = lane * 16;
+  auto read_frags = [&](auto st, auto fb, int ks) {
+    constexpr int f = decltype(fb)::value;
+    const uint8_t* wsp = w_st(st);
+    const uint8_t* asp = a_st(st);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const uint8_t* p = wsp + (4 * wr + rt) * 2048 + lo;
+      wf[f][rt] = cat8a(*reinterpret_cast<const v4i*>(p), *reinterpret_cast<const v4i*>(p + 1024));
+    }
+#pragma unroll
+    for (int tt = 0; tt < TTW; ++tt) {
+      const uint8_t* p = asp + (TTW * wt + tt) * 2048 + lo;
+      af[f][tt] = cat8a(*reinterpret_cast<const v4i*>(p), *reinterpret_cast<const v4i*>(p + 1024));
+    }
+    const float wsk = ws_l[ks];
+#pragma unroll
+    for (int tt = 0; tt < TTW; ++tt) xw[f][tt] = xs_l[ks * BT + (TTW * wt + tt) * 16 + (lane & 15)] * wsk;
+  };
+  read_frags(ic<0>{}, ic<0>{}, 0);
+  auto step = [&](auto ksc) {
+    constexpr int ks = decltype(ksc)::value, f = ks & 1;
+    // this wave's copies of step ks + 1 have landed (those of ks + 2 and ks + 3 may fly), its reads
+    // of step ks are done, and after the barrier every wave's are: stage ks % 4 is free
+    constexpr int ahead = NKB - 2 - ks;
+    tg_wait_vm<LPS * (ahead >= 2 ? 2 : ahead > 0 ? ahead : 0)>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    using cur = ic<ks % 4>;
+    using nxt = ic<(ks + 1) % 4>;
+    using nfb = ic<1 - f>;
+    if constexpr (ks + 4 < NKB) issue(cur{}, ks + 4);
+    if constexpr (ks + 1 < NKB) read_frags(nxt{}, nfb{}, ks + 1);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int tt = 0; tt < TTW; ++tt) {
+        const v4f r = mfma_e4m3(wf[f][rt], af[f][tt]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[rt][tt][i] = __builtin_fmaf(r[i], xw[f][tt], acc[rt][tt][i]);
+      }
+    // the running sums are formed here (left alone, the compiler may keep every step's MFMA
+    // results live and sink the chain)
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int tt = 0; tt < TTW; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[rt][tt][i]));
+  };
+  for_steps(step, std::make_integer_sequence<int, NKB>{});
+  // lane: token t0 + BT / 4 wt + 16 tt + l % 16, rows 128 rb + 64 wr + 16 rt + 4 (l / 16) .. +3 (four
+  // columns never straddle a segment: the boundaries are multiples of 4)
+#pragma unroll
+  for (int tt = 0; tt < TTW; ++tt) {
+    const int t = t0 + (TTW * wt + tt) * 16 + (lane & 15);
+    if (t < g.T) {
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        const int col = rb * 128 + (4 * wr + rt) * 16 + 4 * (lane >> 4);
+        if (col < g.nout) {
+          const int sg = (g.nseg > 1 && col >= g.c0[1]) + (g.nseg > 2 && col >= g.c0[2]) + (g.nseg > 3 && col >= g.c0[3]);
+          *reinterpret_cast<uint2*>(g.ys[sg] + (size_t)t * g.ld[sg] + (col - g.c0[sg])) =
+              make_uint2(pack_bf2(acc[rt][tt][0], acc[rt][tt][1]), pack_bf2(acc[rt][tt][2], acc[rt][tt][3]));
+        }
+      }
+    }
+  }
+}
+
+template <int BT, int NKB>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void tile_gemm_kernel(GemmDev g) {
+  tile_gemm_body<BT, NKB>(g);
+}
+
+// ------------------------------------------------------------------------------------------
 // per-(token, head) epilogue of the QKV projection: one wave per item, 18 items per token (16 q heads
 // with their gates, 2 kv heads).  Lanes 0-31 hold the normed head (q, or k), 8 consecutive dims a
 // lane, lanes 32-63 its companion (the gate, or v); every access is 16 bytes a lane.  q and k: Gemma
@@ -531,8 +723,9 @@ LinWs lin_ws(int T, int K) {
     o = align_up(o + b, 256);
     return r;
   };
-  w.xq = take((size_t)T * K);
-  w.xs = take(sizeof(float) * (size_t)(K / 128) * T);
+  const size_t T16 = (size_t)(T + 15) / 16 * 16;  // fragment order (the tiled GEMM) pads to whole tiles
+  w.xq = take(T16 * K);
+  w.xs = take(sizeof(float) * (size_t)(K / 128) * T16);
   w.total = o;
   return w;
 }
@@ -552,6 +745,24 @@ void launch_ks(const GemmDev& g, hipStream_t st) {
 }
 // token counts from which the projections take the K-sliced GEMM (fragment-order activations)
 constexpr int kKsMinT = 32;
+
+// The tiled GEMM past this many tokens, for K = 2048 (its activations in fragment order).  Token
+// groups of 64 while the grid stays within one workgroup per CU, else of 128.  Measured (graph-timed
+// bench legs and kernel traces): at 256 tokens it takes 18.7 us for the GDN in_proj and the attention
+// QKV against 24.1 and 23.2 us for the streaming and K-sliced GEMMs; at 128 tokens 12.4 against
+// 11.7 us, and for K = 4096 (2048 rows: 32-64 workgroups) 18.7 against 11.7 us.  Its copies into
+// LDS are latency-bound: at most three 24-32 KB steps in flight a CU (the LDS holds four), about 30-45
+// GB/s a CU, where the streaming GEMM spreads the same bytes over every CU's waves.
+constexpr int kTileMinT = 129;
+template <int NKB>
+void launch_tile(const GemmDev& g, hipStream_t st) {
+  const int nrb = g.N / 128, g64 = (g.T + 63) / 64;
+  const int grid64 = 8 * ((nrb + 7) / 8) * g64;
+  if (grid64 <= 256 || g.T <= 64)
+    tile_gemm_kernel<64, NKB><<<grid64, 512, 0, st>>>(g);
+  else
+    tile_gemm_kernel<128, NKB><<<8 * ((nrb + 7) / 8) * ((g.T + 127) / 128), 512, 0, st>>>(g);
+}
 
 // 8-bit codes (e4m3 or int8) [N, K] row-major -> fragment order; thread = one 16-byte chunk of the output
 __global__ __launch_bounds__(256) void pack_frag_kernel(const uint8_t* q, int64_t N, int K, uint8_t* out) {
@@ -605,7 +816,9 @@ extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
   // tokens, 17.9 us per graph-timed call against 19.2 us for the streaming GEMM (128 x 32 tiles, 288
   // workgroups).  Both move about 90 MB through L2 per call (the token groups re-read the weights, the
   // row blocks the activations), which at ~18 TB/s across the chip is what bounds them.
-  if (ks)
+  if (a->T >= kTileMinT)
+    launch_tile<16>(g, st);
+  else if (ks)
     launch_ks<3, 2, 4, 3, 4, 2>(g, st);
   else
     launch_gemm<1, 16, 4>(g, st);
@@ -675,7 +888,9 @@ extern "C" int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream)
   char* ws = static_cast<char*>(a->workspace);
   uint8_t* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
   float* xs = reinterpret_cast<float*>(ws + L.xs);
-  act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr, a->T, a->K, false, xq, xs);
+  const bool tiled = a->T >= kTileMinT && a->K == 2048;
+  act_quant_kernel<<<tiled ? (a->T + 15) / 16 * 16 : a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr,
+                                                                         a->T, a->K, tiled, xq, xs);
   GemmDev g = gemm_dev(xq, xs, a->T, a->K, static_cast<const uint8_t*>(a->w), a->ws, a->N, nullptr);
   g.nseg = a->nseg;
   g.nout = a->n_out;
@@ -684,7 +899,9 @@ extern "C" int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream)
     g.ld[i] = i < a->nseg ? a->seg[i].ld : 0;
     g.ys[i] = i < a->nseg ? static_cast<uint16_t*>(a->seg[i].out) : nullptr;
   }
-  if (a->K == 4096)
+  if (tiled)
+    launch_tile<16>(g, st);
+  else if (a->K == 4096)
     launch_gemm<1, 32, 4, 1>(g, st);
   else if (a->T > 16)
     launch_gemm<2, 16, 2>(g, st);

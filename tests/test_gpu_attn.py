@@ -75,6 +75,27 @@ def test_attn_oproj_parity(attn, oracle_mod, dev, T):
     print(f"oproj: row err {wr:.2e} elem {ar:.2e} exact {er:.4f}", flush=True)
 
 
+@pytest.mark.parametrize("T", [150, 256])
+def test_attn_proj_rows_do_not_depend_on_the_batch(attn, dev, T):
+    """The first 16 tokens of a T-token call equal a 16-token call (the streaming GEMM) bit for bit, q,
+    gate, k, v and the cache codes: past 128 tokens the QKV takes the tiled GEMM (64-token groups at
+    150, 128 at 256), whose sums run in the same order.  (From 32 to 128 tokens it takes the K-sliced
+    GEMM, which adds its four K quarters apart, so its bits may differ.)  Likewise the o_proj."""
+    print(f"attn_proj batch invariance T={T}", flush=True)
+    d, w = _setup(attn, dev, T, seed=500 + T)
+    o = attn.attn_proj(d["x"], w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"],
+                       attn.Workspace(T, dev))
+    o16 = attn.attn_proj(d["x"][:16].contiguous(), w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"],
+                         d["positions"][:16].contiguous(), attn.Workspace(16, dev))
+    gate = (torch.randn((T, 4096), device=dev) * 2).to(torch.bfloat16)
+    out = attn.attn_oproj(d["attn"], gate, w, attn.Workspace(T, dev))
+    out16 = attn.attn_oproj(d["attn"][:16].contiguous(), gate[:16].contiguous(), w, attn.Workspace(16, dev))
+    torch.cuda.synchronize()
+    for key in ("q", "gate", "k", "v", "k8", "v8"):
+        assert torch.equal(o[key][:16], o16[key]), key
+    assert torch.equal(out[:16], out16), "o_proj"
+
+
 def test_pack_frag_layout(attn, dev):
     """q36_pack_frag8 against the documented byte map, on a ragged-looking shape."""
     N, K = 48, 384

@@ -50,6 +50,24 @@ def test_fp8_linear_parity(glue, oracle_mod, dev, T, N, K):
     print(f"row err {wr:.2e} elem {ar:.2e} exact {er:.4f}", flush=True)
 
 
+@pytest.mark.parametrize("T,N,K", [(64, 9216, 2048), (150, 9216, 2048), (200, 12416, 2048), (256, 12416, 2048),
+                                   (256, 2048, 4096)])
+def test_fp8_linear_rows_do_not_depend_on_the_batch(glue, dev, T, N, K):
+    """Rows 0..36 of a T-token call equal a 37-token call (the streaming GEMM) bit for bit.  Past 128
+    tokens with K = 2048 the call takes the tiled GEMM (64-token groups at 150, 128-token groups at 200
+    and 256, ragged last token tile at 150 and 200): both form fma(blocksum, xs * ws, acc) over the K
+    blocks in order from zero, and each token is quantized on its own."""
+    print(f"fp8_linear batch invariance T={T} N={N} K={K}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(T + K)
+    x = torch.randn((T, K), generator=g).to(torch.bfloat16).to(dev)
+    w = glue.prepare_fp8_weight((torch.randn((N, K), generator=g) * 0.02).to(torch.bfloat16).to(dev))
+    big = glue.fp8_linear(x, w, glue.LinearWorkspace(T, K, dev))
+    small = glue.fp8_linear(x[:37].contiguous(), w, glue.LinearWorkspace(37, K, dev))
+    torch.cuda.synchronize()
+    assert torch.equal(big[:37], small)
+    assert torch.isfinite(big.float()).all()
+
+
 def test_fp8_linear_segments_match_the_single_output(glue, dev):
     """The GDN in_proj split: q|k|v 8192, z 4096, b 32, a 32 (12352 columns, 12416 weight rows), the
     first segment written into a wider strided buffer."""
