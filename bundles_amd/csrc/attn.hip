@@ -852,8 +852,12 @@ extern "C" int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream) {
   // 64-row blocks (one 16-row tile per wave), one-tile token groups, 4 stages in flight: 256
   // workgroups at 128 tokens.  Measured at 128 tokens: 6.8 us against 8.1 us for 128-row blocks; the
   // K-sliced GEMM (8 slices of 512, 32 x 32 tiles) 1 us slower per call: with every load of a wave in
-  // flight at once the token groups' shared weight lines leave L2 before the last group reads them
-  launch_gemm<1, 32, 4, 1>(g, st);
+  // flight at once the token groups' shared weight lines leave L2 before the last group reads them.
+  // Past 128 tokens two-tile token groups keep the grid at one round.
+  if (a->T > 128)
+    launch_gemm<2, 32, 4, 1>(g, st);
+  else
+    launch_gemm<1, 32, 4, 1>(g, st);
   return check_launch("q36_attn_oproj");
 }
 
@@ -901,6 +905,8 @@ extern "C" int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream)
   }
   if (tiled)
     launch_tile<16>(g, st);
+  else if (a->K == 4096 && a->T > 128)
+    launch_gemm<2, 32, 4, 1>(g, st);
   else if (a->K == 4096)
     launch_gemm<1, 32, 4, 1>(g, st);
   else if (a->T > 16)

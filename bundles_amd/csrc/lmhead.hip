@@ -315,8 +315,9 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   using T_ = std::true_type;
   using F_ = std::false_type;
   for (;;) {
-    // the scales and step 0 of this tile: the oldest loads in flight (the epilogue's row atomics,
-    // issued after them, may finish first, hence one fewer than the three later steps' loads)
+    // step 0 of this tile: the oldest loads in flight but for its scales when they went out first
+    // (the epilogue's row atomic, and with two terms the scales, go out after steps 0-3, and the
+    // atomic may finish first: with at most 3 LPS - 1 left, every load of step 0 has landed)
     if constexpr (STORE) wait_vm<0>(); else wait_vm<3 * LPS - 1>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -348,32 +349,35 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     // The lane's indices are derived afresh from the thread id here: values computed before the K
     // loop and kept across it were spilled (the loop holds 224 of the 256 registers), and their
     // reloads, queued behind the next tile's loads, held the epilogue until those loads landed.
-    // One term: this tile's scales go into registers (the fragment registers are free by now)
-    // before the next tile's scale loads are issued, since a read of the scale buffer after them
-    // waits for them.  Two terms: the 64 registers this takes made the K loop spill, and the
-    // epilogue reads the buffer (and waits for the next tile's scales).
+    // A read of the scale buffer issued after the next tile's scale loads waits for them (the
+    // compiler cannot tell the parities apart).  One term: this tile's scales go into registers
+    // first, then the next tile's scales and steps are requested (measured 1 % faster than
+    // requesting the scales after the epilogue).  Two terms: the 64 registers this takes made the K
+    // loop spill, so the epilogue reads the buffer and the next tile's scales are requested after it
+    // (they are needed a whole tile later).
     const int et = opaque_tid(), ewm = (et >> 6) >> 1, ewn = (et >> 6) & 1, el32 = et & 31, elh = (et >> 5) & 1;
     constexpr int NTB = X2 ? TB / 2 : TB;
     constexpr bool kRegScales = !X2;
-    float4 wsr[kRegScales ? VB : 1][4];
     auto wscale = [&](int vi, int jg) {
       return *reinterpret_cast<const float4*>(&sc_l[par][0][ewn * 128 + vi * 32 + 8 * jg + 4 * elh]);
     };
+    float4 wsr[kRegScales ? VB : 1][4];
     float xsr[NTB], xs2[NTB];
+#pragma unroll
+    for (int tb = 0; tb < NTB; ++tb) {
+      const int ti = X2 ? 2 * tb : tb;
+      xsr[tb] = sc_l[par][1][ewm * TW + ti * 32 + el32];
+      xs2[tb] = X2 ? sc_l[par][1][ewm * TW + (ti + 1) * 32 + el32] : 0.f;
+    }
     if constexpr (kRegScales) {
 #pragma unroll
       for (int vi = 0; vi < VB; ++vi)
 #pragma unroll
         for (int jg = 0; jg < 4; ++jg) wsr[vi][jg] = wscale(vi, jg);
-#pragma unroll
-      for (int tb = 0; tb < NTB; ++tb) {
-        xsr[tb] = sc_l[par][1][ewm * TW + tb * 32 + el32];
-        xs2[tb] = 0.f;
-      }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     if (more) {
-      issue_scales(tn, par ^ 1);
+      if constexpr (kRegScales) issue_scales(tn, par ^ 1);
 #pragma unroll
       for (int i = 0; i < CPW; ++i) issue_step(tn, 0, ic<0>{}, i);
 #pragma unroll
@@ -396,13 +400,6 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     // One term: token block ti is rows wm*TW + 32 ti of the tile.  Two terms: blocks 2b and 2b + 1
     // hold the two terms of the same 32 tokens (act_row), token wm*TW/2 + 32 b + l32 of the tile.
     const int tok0 = X2 ? t.r0 / 2 : t.r0;
-    if constexpr (!kRegScales) {
-#pragma unroll
-      for (int tb = 0; tb < NTB; ++tb) {
-        xsr[tb] = sc_l[par][1][ewm * TW + 2 * tb * 32 + el32];
-        xs2[tb] = sc_l[par][1][ewm * TW + (2 * tb + 1) * 32 + el32];
-      }
-    }
     {
 #pragma unroll
       for (int tb = 0; tb < NTB; ++tb) {
@@ -453,6 +450,9 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    // two terms: every wave has read this tile's scales, the next tile's may now be requested
+    if constexpr (!kRegScales)
+      if (more) issue_scales(tn, par ^ 1);
     if (et < (X2 ? kBM / 2 : kBM) && tok0 + et < d.R) {
       const uint32_t k = max(rkey[0][et], rkey[1][et]);
       const uint32_t col = (uint32_t)t.v0 + (0xffffu - (k & 0xffffu));
