@@ -68,10 +68,13 @@ def test_fp8_linear_rows_do_not_depend_on_the_batch(glue, dev, T, N, K):
     assert torch.isfinite(big.float()).all()
 
 
-def test_fp8_linear_segments_match_the_single_output(glue, dev):
+@pytest.mark.parametrize("T", [24, 200])
+def test_fp8_linear_segments_match_the_single_output(glue, dev, T):
     """The GDN in_proj split: q|k|v 8192, z 4096, b 32, a 32 (12352 columns, 12416 weight rows), the
-    first segment written into a wider strided buffer."""
-    T, K = 24, 2048
+    first segment written into a wider strided buffer; at 24 tokens through the streaming GEMM, at
+    200 through the tiled one (ragged last token tile)."""
+    print(f"fp8_linear segments T={T}", flush=True)
+    K = 2048
     g = torch.Generator(device="cpu").manual_seed(3)
     x = torch.randn((T, K), generator=g).to(torch.bfloat16).to(dev)
     w = glue.prepare_fp8_weight((torch.randn((12352, K), generator=g) * 0.02).to(torch.bfloat16).to(dev))
