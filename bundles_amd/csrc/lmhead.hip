@@ -12,11 +12,12 @@
 // Kernels:
 //   lmh_prep   one wave per row: norm (sum of squares in the fixed 64-lane order), int8 quant,
 //              and the row's argmax key reset to 0.
-//   lmh_gemm   persistent, one 256-thread workgroup per CU walking 256 x 256 output tiles (4 waves
-//              of 128 x 128, 32x32x32 int8 MFMAs with the weights as operand A, int32 accumulators
-//              in AGPRs); K in 64-byte steps through a 4-stage LDS ring filled by buffer loads
-//              straight into LDS four steps ahead, fragments double-buffered in registers, and the
-//              next tile's first steps requested before the epilogue.  Epilogue: bf16 logits, the
+//   lmh_gemm   persistent, one 512-thread workgroup per CU walking 256 x 256 output tiles (8 waves,
+//              two a SIMD, each 128 vocab rows x 64 tokens, 32x32x32 int8 MFMAs with the weights as
+//              operand A, int32 accumulators); K in 64-byte steps through a 4-stage LDS ring
+//              filled by buffer loads straight into LDS four steps ahead, fragments
+//              double-buffered in registers, and the next tile's first steps requested before the
+//              epilogue.  Epilogue: bf16 logits, the
 //              first column of each row's largest value folded into an order-preserving key, and one
 //              64-bit atomic max per row and tile: the result does not depend on the order the
 //              workgroups finish in.  lmh_gemm_logits: the same, writing the bf16 logits too.
@@ -157,7 +158,7 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Persistent GEMM + argmax: one 256-thread workgroup per CU walks its XCD's tiles.  The XCDs form
+// Persistent GEMM + argmax: one 512-thread workgroup per CU walks its XCD's tiles.  The XCDs form
 // ngrp row groups (2 when the row tiles split evenly, else 1): XCD x serves the rpg = nrt / ngrp
 // row tiles of group x % ngrp and the vocab tiles v = x / ngrp (mod 8 / ngrp).  Its workgroups take
 // tiles j = loc, loc + nloc, ... (loc = blockIdx / 8, nloc = gridDim / 8), tile j being row tile
