@@ -48,7 +48,8 @@ struct LmhDev {
   const int8_t* wq;
   const float* ws;
   int32_t* ids;
-  uint16_t* logits;
+  uint16_t* logits;   // bf16 [R, V] or null
+  float* logits32;    // fp32 [R, V] (bf16-rounded values) or null; at most one of the two is set
   int8_t* xq;
   float* xs;
   unsigned long long* keys;
@@ -178,7 +179,8 @@ __device__ __forceinline__ void wait_vm() {
 // row groups of XCDs (see lmh_gemm_body): two when there are at least 4 row tiles, evenly split
 __host__ __device__ __forceinline__ int lmh_groups(int nrt) { return nrt >= 4 && nrt % 2 == 0 ? 2 : 1; }
 
-template <bool STORE, bool X2, int NW>
+// STORE: 0 no logits, 1 bf16 logits, 2 fp32 logits (the bf16-rounded values widened)
+template <int STORE, bool X2, int NW>
 __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   // NW waves: two vocab halves (wn) x NW / 2 token groups (wm); a wave owns 128 vocab columns (VB = 4
   // blocks of 32) x TW tokens (TB blocks of 32)
@@ -430,11 +432,15 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
                 lg[q] = rbf_hw(((float)acc[vi][ti][4 * jg + q] * xsr[tb]) * wq[q]);
               if (in && lg[q] > bv) bv = lg[q], bi = co + q;
             }
-            if constexpr (STORE)
+            if constexpr (STORE == 1)
               if (row < d.R && in)
                 *reinterpret_cast<uint2*>(d.logits + (size_t)row * d.V + t.v0 + cl) =
                     make_uint2((__float_as_uint(lg[0]) >> 16) | (__float_as_uint(lg[1]) & 0xffff0000u),
                                (__float_as_uint(lg[2]) >> 16) | (__float_as_uint(lg[3]) & 0xffff0000u));
+            if constexpr (STORE == 2)
+              if (row < d.R && in)
+                *reinterpret_cast<float4*>(d.logits32 + (size_t)row * d.V + t.v0 + cl) =
+                    make_float4(lg[0], lg[1], lg[2], lg[3]);
           }
         uint32_t b16 = __float_as_uint(bv + 0.f) >> 16;
         b16 = (b16 & 0x8000u) ? (~b16 & 0xffffu) : (b16 | 0x8000u);
@@ -468,13 +474,13 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
 template <bool X2>
 __global__ __launch_bounds__(64 * kLmhWaves) __attribute__((amdgpu_waves_per_eu(kLmhWaves / 4, kLmhWaves / 4))) void
 lmh_gemm_kernel(LmhDev d) {
-  lmh_gemm_body<false, X2, kLmhWaves>(d);
+  lmh_gemm_body<0, X2, kLmhWaves>(d);
 }
-// the same with the bf16 logits written out
-template <bool X2>
+// the same with the logits written out (F32: as fp32)
+template <bool X2, bool F32>
 __global__ __launch_bounds__(64 * kLmhWaves) __attribute__((amdgpu_waves_per_eu(kLmhWaves / 4, kLmhWaves / 4))) void
 lmh_gemm_logits_kernel(LmhDev d) {
-  lmh_gemm_body<true, X2, kLmhWaves>(d);
+  lmh_gemm_body<F32 ? 2 : 1, X2, kLmhWaves>(d);
 }
 
 __global__ __launch_bounds__(256) void lmh_ids_kernel(LmhDev d) {
@@ -538,9 +544,12 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
               a->workspace_bytes, L.total);
   char* ws = static_cast<char*>(a->workspace);
   const int x2 = a->mode == Q36_LMH_W8A8X2, w16 = a->mode == Q36_LMH_W8A16;
+  Q36_REQUIRE(!a->logits_f32 || a->logits, "q36_lmhead_argmax: logits_f32 set without a logits buffer");
+  Q36_REQUIRE(aligned16(a->logits), "q36_lmhead_argmax: logits must be 16-byte aligned");
+  const bool f32 = a->logits && a->logits_f32;
   LmhDev d{a->R, a->V, act_rows(a->R, x2), x2, w16, static_cast<const uint16_t*>(a->h), static_cast<const uint16_t*>(a->norm_w), a->eps,
-           static_cast<const int8_t*>(a->wq), a->ws, a->ids, static_cast<uint16_t*>(a->logits),
-           reinterpret_cast<int8_t*>(ws + L.xq), reinterpret_cast<float*>(ws + L.xs),
+           static_cast<const int8_t*>(a->wq), a->ws, a->ids, f32 ? nullptr : static_cast<uint16_t*>(a->logits),
+           f32 ? static_cast<float*>(a->logits) : nullptr, reinterpret_cast<int8_t*>(ws + L.xq), reinterpret_cast<float*>(ws + L.xs),
            reinterpret_cast<unsigned long long*>(ws + L.keys)};
   hipStream_t st = static_cast<hipStream_t>(stream);
   lmh_prep_kernel<<<(a->R + 3) / 4, 256, 0, st>>>(d);
@@ -553,6 +562,7 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
     g.q = d.wq;
     g.ws = d.ws;
     g.logits = d.logits;
+    g.logits32 = d.logits32;
     g.keys = d.keys;
     launch_w8a16(g, 0, st);
     lmh_ids_kernel<<<(a->R + 255) / 256, 256, 0, st>>>(d);
@@ -563,10 +573,14 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
   // busiest XCD's tiles
   const int ngrp = lmh_groups(nrt), vstep = 8 / ngrp;
   const int blocks = 8 * std::max(1, std::min(lmh_cus() / 8, ((nvt + vstep - 1) / vstep) * (nrt / ngrp)));
-  if (d.logits && x2)
-    lmh_gemm_logits_kernel<true><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+  if (d.logits32 && x2)
+    lmh_gemm_logits_kernel<true, true><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+  else if (d.logits32)
+    lmh_gemm_logits_kernel<false, true><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+  else if (d.logits && x2)
+    lmh_gemm_logits_kernel<true, false><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
   else if (d.logits)
-    lmh_gemm_logits_kernel<false><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+    lmh_gemm_logits_kernel<false, false><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
   else if (x2)
     lmh_gemm_kernel<true><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
   else

@@ -18,6 +18,8 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int WAVE = 64;
 
+// One 16-byte global load.
+__device__ __forceinline__ v4i ldg16(const uint8_t* p) { return *reinterpret_cast<const v4i*>(p); }
 __device__ __forceinline__ float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

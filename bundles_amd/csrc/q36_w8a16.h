@@ -13,6 +13,7 @@ struct W16Dev {
   // mode 0
   const float* ws;        // fp32 [N]
   uint16_t* logits;       // bf16 [T, N] or null
+  float* logits32;        // fp32 [T, N] (the bf16-rounded values) or null
   unsigned long long* keys;  // [T] argmax keys (zero on entry)
   // mode 1
   const uint16_t* s16;    // fp16 [K / 128][s_ld]

@@ -101,17 +101,19 @@ __global__ __launch_bounds__(64 * WAVES) void w8a16_kernel(W16Dev d) {
     v4i wq[D][RT], xa[D][NTT], xb[D][NTT];
     uint2 scl[D / 2][RT];  // mode 1: the fp16 scales of the group starting at an even step
     // Loads are issued without a branch (a conditional load makes the compiler wait for every
-    // outstanding load at the join): a step past the chunk gets an offset past both descriptors' ranges,
-    // which returns zeros and moves no data.
+    // outstanding load at the join): a step past the chunk gets a VGPR offset past both descriptors'
+    // ranges, which returns zeros and moves no data.  The out-of-range amount rides in the VGPR offset
+    // because only that one is range-checked; the SGPR offset carries in-range step offsets only.
+    // (nsteps is a compile-time constant and the step loop unrolls, so `in` folds away per step.)
     auto issue = [&](int u, int s) {
       const bool in = s < nsteps;
-      const int wo = in ? 64 * s : (1 << 30), xo = in ? 128 * s : (1 << 30);
+      const int wo = in ? 64 * s : 0, xo = in ? 128 * s : 0, oob = in ? 0 : (1 << 30);
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) wq[u][rt] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wv[rt], wo, 2);
+      for (int rt = 0; rt < RT; ++rt) wq[u][rt] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wv[rt] + oob, wo, 2);
 #pragma unroll
       for (int tt = 0; tt < NTT; ++tt) {
-        xa[u][tt] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv[tt], xo, 0);
-        xb[u][tt] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv[tt], xo + 16, 0);
+        xa[u][tt] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv[tt] + oob, xo, 0);
+        xb[u][tt] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv[tt] + oob, xo + 16, 0);
       }
       if constexpr (MODE == 1) {
         if (!(u & 1)) {
@@ -223,6 +225,8 @@ __global__ __launch_bounds__(64 * WAVES) void w8a16_kernel(W16Dev d) {
             *reinterpret_cast<uint2*>(d.logits + (size_t)t * d.N + rb) =
                 make_uint2((__float_as_uint(lg4[0]) >> 16) | (__float_as_uint(lg4[1]) & 0xffff0000u),
                            (__float_as_uint(lg4[2]) >> 16) | (__float_as_uint(lg4[3]) & 0xffff0000u));
+          if (d.logits32 && t < d.T)
+            *reinterpret_cast<float4*>(d.logits32 + (size_t)t * d.N + rb) = make_float4(lg4[0], lg4[1], lg4[2], lg4[3]);
         }
       }
       // order-preserving bf16 key, first row on ties (the larger 0xffff - row)

@@ -61,6 +61,48 @@ class EngineView:
         return None
 
 
+RING_ENTRIES = 16  # the ring verify serves the 16-entry compact circular ReplaySSM ring
+MAX_DRAFT = 8     # verify tokens per request the ring kernel serves
+
+
+def gdn_pool_refusal(lin, pool, params, forward_batch) -> str | None:
+    """Why the ring verify cannot serve this engine's recurrent pools (None: it can).  The served layout
+    the reference requires before its verify kernel runs (L/gdn_fused.py:19-34): no multi-item scoring,
+    the compact circular ReplaySSM ring (ring pools present, no spec-fold layout, not KDA, no beta ring,
+    16 entries); here any of these sends the batch to the stock mixer instead of raising."""
+    if getattr(lin, "mis_metadata", None) is not None:
+        return "multi-item scoring"
+    if (getattr(params, "replayssm_d", None) is None or getattr(params, "replayssm_rawv", None) is None
+            or getattr(params, "replayssm_rawk", None) is None or getattr(pool, "replayssm_cache_base", None) is None):
+        return "no ReplaySSM ring pools"
+    if getattr(pool, "replayssm_spec_fold", True):
+        return "spec-fold ring layout"
+    if getattr(pool, "replayssm_is_kda", False):
+        return "KDA ring"
+    if getattr(params, "replayssm_beta", None) is not None:
+        return "ring with a beta pool"
+    if params.replayssm_d.shape[-2] != RING_ENTRIES:
+        return f"{params.replayssm_d.shape[-2]}-entry ring"
+    spec = getattr(forward_batch, "spec_info", None)
+    draft = getattr(spec, "draft_token_num", None)
+    if draft is None or not 1 <= int(draft) <= MAX_DRAFT:
+        return f"{draft}-token drafts"
+    return None
+
+
+def kv_backend_refusal(full) -> str | None:
+    """Why the verify attention cannot serve this attention backend (None: it can): one-token pages,
+    chain drafts, no MLA (the backend half of L/attn_fused.py:48-60; the layer half is checked when the
+    node is prepared)."""
+    if getattr(full, "page_size", 1) != 1:
+        return f"page size {getattr(full, 'page_size', None)}"
+    if int(getattr(full, "topk", 1) or 1) > 1:
+        return "tree drafts (topk > 1)"
+    if getattr(full, "use_mla", False):
+        return "MLA"
+    return None
+
+
 def _e4m3_codes(t: torch.Tensor) -> torch.Tensor | None:
     if t.dtype == torch.float8_e4m3fn:
         return t.view(torch.uint8)
@@ -85,8 +127,10 @@ class SglangView(EngineView):
             return None
         fm, pool = lin.forward_metadata, lin.req_to_token_pool.mamba_pool
         p = lin.req_to_token_pool.mamba2_layer_cache(layer_id)
-        if fm.retrieve_next_token is not None or fm.retrieve_next_sibling is not None:
+        if getattr(fm, "retrieve_next_token", None) is not None or getattr(fm, "retrieve_next_sibling", None) is not None:
             return None  # tree drafts: the kernel serves chain verification only
+        if gdn_pool_refusal(lin, pool, p, forward_batch) is not None:
+            return None
         return GdnPools(p.conv[0], p.intermediate_conv_window[0], p.temporal, p.replayssm_d, p.replayssm_rawv,
                         p.replayssm_k, p.replayssm_rawk, p.replayssm_g, fm.query_start_loc, fm.mamba_cache_indices,
                         forward_batch.req_pool_indices, lin.verify_intermediate_state_indices,
@@ -96,7 +140,7 @@ class SglangView(EngineView):
     def kv_view(self, layer_id, forward_batch):
         be = self._backend()
         full = getattr(be, "full_attn_backend", None)
-        if full is None or getattr(full, "page_size", 1) != 1:
+        if full is None or kv_backend_refusal(full) is not None:
             return None
         k, v = full.token_to_kv_pool.get_kv_buffer(layer_id)
         k8, v8 = _e4m3_codes(k), _e4m3_codes(v)

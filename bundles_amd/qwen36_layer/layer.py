@@ -162,6 +162,20 @@ def _install_moe(module, replica, dtype, topk, max_tokens):
 
 
 # ---- GDN mixer -----------------------------------------------------------------------------------------
+def gdn_layer_refusal(core, norm) -> str | None:
+    """Why the ring verify cannot serve this recurrent layer (None: it can): the layer half of the
+    reference's served-layout check (L/gdn_fused.py:30-34), a bias-free SiLU conv and the swish-gated
+    RMSNorm applied before the gate over whole heads.  Attributes a module does not have are taken as
+    the served model's."""
+    if getattr(core, "bias", None) is not None or getattr(core, "activation", "silu") not in ("silu", "swish"):
+        return "a conv with a bias or a non-SiLU activation"
+    if (getattr(norm, "norm_before_gate", True) is not True
+            or getattr(norm, "group_size", None) not in (None, norm.weight.numel())
+            or getattr(norm, "activation", "silu") not in ("silu", "swish") or getattr(norm, "bias", None) is not None):
+        return "a gated norm other than the swish-gated RMSNorm"
+    return None
+
+
 class _GdnMixer:
     """The recurrent mixer's target-verify step: in_proj (e4m3 blocks, columns split q|k|v, z, b, a),
     q36_gdn_verify_ring over the engine's pools (conv, delta rule, ring appends, gated norm), out_proj."""
@@ -180,6 +194,8 @@ class _GdnMixer:
         if core.A_log.dtype != torch.float32 or core.A_log.numel() != GDN_HV:
             raise RuntimeError("linear_attn.attn.A_log must be fp32 [32]")
         self.lin, self.replica, self.engine, self.max_tokens = lin, replica_lin, engine, max_tokens
+        # a layer outside the served layout keeps the stock mixer for every batch
+        self.refusal = gdn_layer_refusal(core, norm)
         self.layer_id = int(getattr(core, "layer_id", getattr(lin, "layer_id", -1)))
         self.stock = type(lin).forward
         self.conv_w, self.A_log, self.dt_bias = core.conv_weights, core.A_log, core.dt_bias.contiguous()
@@ -198,8 +214,8 @@ class _GdnMixer:
         x = hidden_states
         rows = x.shape[0] if isinstance(x, torch.Tensor) and x.dim() == 2 else 0
         pools = (self.engine.gdn_pools(self.layer_id, forward_batch)
-                 if verify_batch(forward_batch) and 0 < rows <= self.max_tokens and x.dtype == torch.bfloat16
-                 else None)
+                 if self.refusal is None and verify_batch(forward_batch) and 0 < rows <= self.max_tokens
+                 and x.dtype == torch.bfloat16 else None)
         if pools is None or rows % pools.draft:
             return self.stock(self.replica, hidden_states, forward_batch)
         sc = _Scratch.get(x.device, rows)
@@ -237,6 +253,28 @@ def _install_gdn(module, replica, engine, max_tokens, dense8_rows):
 
 
 # ---- attention mixer --------------------------------------------------------------------------------------
+def attn_layer_refusal(module) -> str | None:
+    """Why the verify attention cannot serve this attention layer (None: it can): the layer half of the
+    reference's served-layout check (L/attn_fused.py:48-60), an output gate, one q/k norm epsilon, an
+    unscaled e4m3 cache, full causal self-attention (no sliding window, no cross-attention, no logit
+    cap).  Attributes a module does not have are taken as the served model's."""
+    attn = getattr(module, "attn", None)
+    if not getattr(module, "attn_output_gate", True):
+        return "no output gate"
+    if float(module.q_norm.variance_epsilon) != float(module.k_norm.variance_epsilon):
+        return "different q and k norm epsilons"
+    if getattr(attn, "k_scale", None) is not None or getattr(attn, "v_scale", None) is not None:
+        return "a scaled KV cache"
+    sw = getattr(attn, "sliding_window_size", None)
+    if sw is not None and sw > -1:
+        return "a sliding window"
+    if getattr(attn, "is_cross_attention", False):
+        return "cross-attention"
+    if getattr(attn, "logit_cap", None) not in (None, 0, 0.0):
+        return "a logit cap"
+    return None
+
+
 class _AttnMixer:
     """The gated attention mixer's target-verify step: q36_attn_proj (q/gate/k/v, q/k norm, partial
     RoPE, e4m3 K/V rows), q36_attn_decode over the engine's KV cache (the new rows written first), and
@@ -258,6 +296,8 @@ class _AttnMixer:
         if int(getattr(rot, "rotary_dim", 64)) != 64 or rot.cos_sin_cache.shape[-1] != 64:
             raise RuntimeError("this node serves RoPE on the first 64 dims of each head")
         self.replica, self.engine, self.max_tokens = replica, engine, max_tokens
+        # a layer outside the served layout keeps the stock attention for every batch
+        self.refusal = attn_layer_refusal(module)
         self.layer_id = int(getattr(module.attn, "layer_id", getattr(module, "layer_id", -1)))
         self.stock = type(module).self_attention
         self.scale = float(getattr(module.attn, "scaling", d ** -0.5))
@@ -272,8 +312,8 @@ class _AttnMixer:
         x = hidden_states
         rows = x.shape[0] if isinstance(x, torch.Tensor) and x.dim() == 2 else 0
         kv = (self.engine.kv_view(self.layer_id, forward_batch)
-              if verify_batch(forward_batch) and 0 < rows <= self.max_tokens and x.dtype == torch.bfloat16
-              else None)
+              if self.refusal is None and verify_batch(forward_batch) and 0 < rows <= self.max_tokens
+              and x.dtype == torch.bfloat16 else None)
         if kv is None or rows % kv.draft or not 1 <= kv.draft <= 4:
             return self.stock(self.replica, positions, hidden_states, forward_batch)
         sc = _Scratch.get(x.device, rows)

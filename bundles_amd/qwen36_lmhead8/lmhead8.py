@@ -17,9 +17,16 @@ from .._lib import LmheadArgs, check, ptr
 
 
 def quantize_rows(w: torch.Tensor, stream=None):
-    """bf16 [N, K] -> (int8 [N, K], fp32 scale [N])."""
-    from ..qwen36_layer.moe import quantize_rows_i8
-    return quantize_rows_i8(w, stream=stream)
+    """bf16 [N, K] -> (int8 [N, K], fp32 scale [N]): s = amax / 127, codes rounded half away from
+    zero (H/lmhead8.py:95-108,129-143), by q36_quant_rows_i8."""
+    if w.dtype != torch.bfloat16 or w.dim() != 2 or not w.is_cuda:
+        raise ValueError(f"quantize_rows: expects a 2-D bf16 CUDA tensor, got {w.dtype} {tuple(w.shape)}")
+    w = w.contiguous()
+    N, K = w.shape
+    q = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    s = torch.empty(N, dtype=torch.float32, device=w.device)
+    check(_lib.lib().q36_quant_rows_i8(ptr(w), N, K, ptr(q), ptr(s), _lib.stream_handle(stream)), "q36_quant_rows_i8")
+    return q, s
 
 
 class Workspace:
@@ -31,8 +38,10 @@ class Workspace:
 def w8a8_lmhead_argmax(h, q, scale, ws: Workspace, norm_w=None, eps: float = 1e-6, want_logits: bool = False,
                        ids=None, stream=None, two_term: bool = False, logits=None, w8a16: bool = False):
     """h bf16 [R, 2048] -> ids int32 [R] (and bf16 logits [R, V] when want_logits, into `logits` when
-    given).  two_term: the reference's two-term activation form (H/w8a8.py:25-37); w8a16: the bf16
-    rows times the int8 weights unquantized (H/lmhead8.py:57-91; R <= 64, V a multiple of 32)."""
+    given: bf16, or fp32 receiving the same bf16-rounded values, as the reference writes stock's fp32
+    next_token_logits_buffer, H/node.py:68-88,136-149).  two_term: the reference's two-term activation
+    form (H/w8a8.py:25-37); w8a16: the bf16 rows times the int8 weights unquantized (H/lmhead8.py:57-91;
+    R <= 64, V a multiple of 32)."""
     R, H = h.shape
     V = q.shape[0]
     if R > ws.R_max:
@@ -43,11 +52,12 @@ def w8a8_lmhead_argmax(h, q, scale, ws: Workspace, norm_w=None, eps: float = 1e-
     ids = torch.empty(R, dtype=torch.int32, device=h.device) if ids is None else ids
     if want_logits and logits is None:
         logits = torch.empty((R, V), dtype=torch.bfloat16, device=h.device)
-    if logits is not None and (logits.dtype != torch.bfloat16 or tuple(logits.shape) != (R, V) or
-                               not logits.is_contiguous()):
-        raise ValueError(f"w8a8_lmhead_argmax: logits must be contiguous bf16 [{R}, {V}]")
+    if logits is not None and (logits.dtype not in (torch.bfloat16, torch.float32) or tuple(logits.shape) != (R, V)
+                               or not logits.is_contiguous()):
+        raise ValueError(f"w8a8_lmhead_argmax: logits must be contiguous bf16 or fp32 [{R}, {V}]")
     a = LmheadArgs(R, H, V, ptr(h), ptr(norm_w), eps, ptr(q), ptr(scale), ptr(ids), ptr(logits), ptr(ws.buf),
                    ws.buf.numel(),
-                   _lib.Q36_LMH_W8A16 if w8a16 else _lib.Q36_LMH_W8A8X2 if two_term else _lib.Q36_LMH_W8A8)
+                   _lib.Q36_LMH_W8A16 if w8a16 else _lib.Q36_LMH_W8A8X2 if two_term else _lib.Q36_LMH_W8A8,
+                   int(logits is not None and logits.dtype == torch.float32))
     check(_lib.lib().q36_lmhead_argmax(C.byref(a), _lib.stream_handle(stream)), "q36_lmhead_argmax")
     return (ids, logits) if (want_logits or logits is not None) else ids

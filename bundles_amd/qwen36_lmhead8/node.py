@@ -19,9 +19,15 @@ Design:
                reference hands more than 256 rows to a bf16 matmul).
   greedy ids   the same launch finds each row's first largest logit; Int8Head keeps them on the node
                (last_ids) for a sampler that reads them instead of taking the argmax again.
-Heads the int8 path does not serve (no dense 2-D bf16 CUDA weight of width 2048, LoRA-wrapped heads, an
-embedding bias, strided or non-bf16 hidden states, more than MAX_ROWS rows) reach the processor as they
-came, so its stock code runs.
+  logits buffer for a decode or target-verify call of at least LOGITS_BUF_MIN_ROWS rows, the logits go
+               straight into the processor's fp32 next_token_logits_buffer (bf16-rounded values) when
+               its shape is exactly [rows, vocab]: stock then copies that tensor onto itself, a no-op
+               (H/node.py:68-88,136-149); otherwise a fresh bf16 tensor is returned.
+Heads the int8 path does not serve reach the processor as they came, so its stock code runs
+(H/node.py:34-56): a processor that wants fp32 logits, an RL on-policy target or a tensor-parallel
+all-gather of the logits; LoRA-wrapped heads; pre-quantized heads (a quant method other than the
+unquantized one) and heads on the Intel AMX backend; no dense 2-D bf16 CUDA weight of width 2048; an
+embedding bias, strided or non-bf16 hidden states, more than MAX_ROWS rows.
 """
 from __future__ import annotations
 
@@ -35,6 +41,7 @@ HIDDEN = 2048
 MAX_ROWS = 4096       # rows a call may carry on the int8 path (the workspace is sized once for this)
 MAX_TWO_TERM = 256    # row batches up to this size take the two-term activation form
 W8A16_BELOW = 64      # row batches below this size keep the activations in bf16
+LOGITS_BUF_MIN_ROWS = 16  # row batches from this size write stock's fp32 logits buffer directly
 
 
 def row_mode(rows: int, vocab: int = 151936) -> str:
@@ -47,6 +54,67 @@ def row_mode(rows: int, vocab: int = 151936) -> str:
 def _servable_weight(w) -> bool:
     return (isinstance(w, torch.Tensor) and w.dim() == 2 and w.is_cuda and w.dtype == torch.bfloat16
             and w.shape[1] == HIDDEN and w.shape[0] % 16 == 0 and w.stride(1) == 1)
+
+
+def _stock_logits_module():
+    try:
+        from sglang.srt.layers import logits_processor as stock_logits
+    except ImportError:
+        return None
+    return stock_logits
+
+
+def _prequantized(head) -> bool:
+    """A head whose logits come from its own quant method (a quantized checkpoint's lm_head): the
+    processor's own rule when SGLang is importable, else any quant method other than the unquantized
+    one."""
+    qm = getattr(head, "quant_method", None)
+    stock = _stock_logits_module()
+    if stock is not None and hasattr(stock, "should_apply_lm_head_quant_method"):
+        return bool(stock.should_apply_lm_head_quant_method(head, qm))
+    return qm is not None and not type(qm).__name__.startswith("Unquantized")
+
+
+def _amx(head) -> bool:
+    stock = _stock_logits_module()
+    probe = getattr(stock, "use_intel_amx_backend", None) if stock is not None else None
+    if callable(probe):
+        return bool(probe(head))
+    return bool(getattr(head, "use_intel_amx_backend", False))
+
+
+def processor_refusal(processor) -> str | None:
+    """Why the int8 head cannot stand in for this processor's lm_head (None: it can; H/node.py:34-38)."""
+    if getattr(processor, "use_fp32_lm_head", False):
+        return "fp32 lm_head"
+    if getattr(processor, "rl_on_policy_target", None) is not None:
+        return "RL on-policy target"
+    if getattr(processor, "do_tensor_parallel_all_gather", False) or \
+            getattr(processor, "do_tensor_parallel_all_gather_dp_attn", False):
+        return "tensor-parallel all-gather of the logits"
+    return None
+
+
+def _meta(args, kwargs):
+    return kwargs["logits_metadata"] if "logits_metadata" in kwargs else args[3] if len(args) > 3 else None
+
+
+def logits_buffer(processor, args, kwargs) -> torch.Tensor | None:
+    """Stock's fp32 next_token_logits_buffer for a decode / target-verify call, else None.  In those
+    modes the processor computes logits once and copies them into this buffer when the shapes match;
+    writing the bf16-rounded logits into it directly makes that copy a no-op with the same bytes
+    (H/node.py:68-88).  A processor that scales its logits afterwards gets no buffer."""
+    meta = _meta(args, kwargs)
+    mode = getattr(meta, "forward_mode", None)
+    is_decode, is_verify = getattr(mode, "is_decode", None), getattr(mode, "is_target_verify", None)
+    if not (callable(is_decode) and callable(is_verify)) or not (is_decode() or is_verify()):
+        return None
+    if getattr(processor, "logit_scale", None) is not None:
+        return None
+    buf = getattr(meta, "next_token_logits_buffer", None)
+    if not isinstance(buf, torch.Tensor) or buf.dtype != torch.float32 or buf.dim() != 2 or not buf.is_contiguous():
+        return None
+    return buf
 
 
 def _version(w: torch.Tensor):
@@ -76,6 +144,7 @@ class LogitsNode:
         self.copy: HeadCopy | None = None
         self.workspace: lmhead8.Workspace | None = None
         self.last_ids: torch.Tensor | None = None
+        self.out_buf: torch.Tensor | None = None  # this call's fp32 logits buffer (set by __call__)
 
     # -- the int8 copy and scratch, made outside capture only --
     def copy_for(self, w: torch.Tensor) -> HeadCopy | None:
@@ -109,20 +178,32 @@ class LogitsNode:
         ws = self.workspace_for(h.device) if hc is not None else None
         if ws is None:
             return None
-        mode = row_mode(h.shape[0], hc.q.shape[0])
-        ids, logits = lmhead8.w8a8_lmhead_argmax(h.contiguous(), hc.q, hc.scale, ws, want_logits=True,
+        rows, vocab = h.shape[0], hc.q.shape[0]
+        mode = row_mode(rows, vocab)
+        buf = self.out_buf
+        out = (buf if buf is not None and rows >= LOGITS_BUF_MIN_ROWS and tuple(buf.shape) == (rows, vocab)
+               and vocab == getattr(self.processor, "vocab_size", -1) and buf.device == weight.device else None)
+        ids, logits = lmhead8.w8a8_lmhead_argmax(h.contiguous(), hc.q, hc.scale, ws, want_logits=True, logits=out,
                                                  two_term=mode == "two_term", w8a16=mode == "w8a16")
         self.last_ids = ids
         return logits
 
+    def serves(self, head) -> bool:
+        """Whether the int8 head stands in for `head` in this processor (H/node.py:34-56)."""
+        return processor_refusal(self.processor) is None and Int8Head.serves(head)
+
     def __call__(self, *args, **kwargs):
         if "lm_head" in kwargs:
             head = kwargs["lm_head"]
-            if Int8Head.serves(head):
+            if self.serves(head):
                 kwargs = dict(kwargs, lm_head=Int8Head(self, head))
-        elif len(args) > 2 and Int8Head.serves(args[2]):
+        elif len(args) > 2 and self.serves(args[2]):
             args = args[:2] + (Int8Head(self, args[2]),) + args[3:]
-        return self.stock_forward(self.processor, *args, **kwargs)
+        self.out_buf = logits_buffer(self.processor, args, kwargs)
+        try:
+            return self.stock_forward(self.processor, *args, **kwargs)
+        finally:
+            self.out_buf = None
 
 
 class Int8Head:
@@ -135,7 +216,10 @@ class Int8Head:
 
     @staticmethod
     def serves(head) -> bool:
+        """The head-side rules: no LoRA wrapper, not pre-quantized, not on AMX, a dense bf16 weight."""
         if head is None or (hasattr(head, "set_lora") and hasattr(head, "apply_lora")):
+            return False
+        if _prequantized(head) or _amx(head):
             return False
         return _servable_weight(getattr(head, "weight", None))
 

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define Q36_ABI_VERSION 3
+#define Q36_ABI_VERSION 4
 #define Q36_OK 0
 #define Q36_EINVAL 1
 #define Q36_ELAUNCH 2
@@ -404,7 +404,8 @@ int q36_attn_decode(const q36_decode_args* a, q36_stream_t stream);
  * NULL to skip; y = bf16((h * rstd) * (1 + w))) -> per-row int8 (s = amax/127, half away) ->
  * acc = xq . wq^T (int32, wq int8 [V, H], ws fp32 [V]) -> logit = bf16((acc * xs) * ws) ->
  * ids int32 [R] = first index of the row's largest logit.  logits bf16 [R, V] is optional (NULL
- * skips the store).  V % 16 == 0.  Workspace: q36_lmhead_workspace_bytes(R), 256-byte aligned
+ * skips the store); with logits_f32 nonzero it is fp32 [R, V] instead and receives the same
+ * bf16-rounded values widened (stock's fp32 next_token_logits_buffer, H/node.py:68-88,136-149).  V % 16 == 0.  Workspace: q36_lmhead_workspace_bytes(R), 256-byte aligned
  * (enough for every mode).
  * mode Q36_LMH_W8A8X2: two activation terms (H/w8a8.py:25-37 quantize_act two_term, the reference's
  * arithmetic from 64 rows): q1, s1 as above, then q2, s2 the same rule on the residual
@@ -427,6 +428,7 @@ typedef struct q36_lmhead_args {
   void* workspace;
   size_t workspace_bytes;
   int32_t mode; /* Q36_LMH_W8A8, Q36_LMH_W8A8X2 or Q36_LMH_W8A16 */
+  int32_t logits_f32; /* 0: logits is bf16 [R, V]; nonzero: fp32 [R, V] (bf16-rounded values) */
 } q36_lmhead_args;
 size_t q36_lmhead_workspace_bytes(int32_t R);
 int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream);

@@ -40,8 +40,25 @@ def assert_bf16_close(got_bits, ref_bits, rtol=1e-2, what=""):
     rms = np.sqrt(np.mean(r2 * r2, axis=1, keepdims=True)) + 1e-30
     elem = np.abs(g2 - r2) / (np.abs(r2) + rms)
     worst = float(row.max()) if row.size else 0.0
+    exact = float(np.mean(g2 == r2)) if g2.size else 1.0
+    print(f"{what}: row error {worst:.3e} (bar {rtol:g}), worst elementwise |g-r|/|r| "
+          f"{elementwise_rel(g2, r2):.3e}, exact {exact:.4f}", flush=True)
     assert worst <= rtol, f"{what}: worst row relative error {worst:.3e} > {rtol}"
-    return worst, float(elem.max()) if elem.size else 0.0, float(np.mean(g2 == r2))
+    return worst, float(elem.max()) if elem.size else 0.0, exact
+
+
+def elementwise_rel(g2: np.ndarray, r2: np.ndarray) -> float:
+    """Worst |g - r| / |r| over the elements whose |r| is at least one bf16 ulp of their row's largest
+    |r| (2^(e - 7) for a row maximum in [2^e, 2^(e+1))): smaller references are rounding noise of the
+    row's scale, where a relative error says nothing."""
+    if not g2.size:
+        return 0.0
+    rmax = np.max(np.abs(r2), axis=1, keepdims=True)
+    ulp = np.where(rmax > 0, np.exp2(np.floor(np.log2(np.where(rmax > 0, rmax, 1.0))) - 7), np.inf)
+    keep = np.abs(r2) >= ulp
+    if not keep.any():
+        return 0.0
+    return float(np.max(np.abs(g2 - r2)[keep] / np.abs(r2)[keep]))
 
 
 def assert_f32_close(got, ref, rtol=1e-4, what=""):

@@ -104,6 +104,38 @@ def test_decode_bench_shape(attn, oracle_mod, dev):
     assert torch.equal(out, out2), "two runs of the same inputs differ"
 
 
+def test_decode_config5_batch(attn, oracle_mod, dev):
+    """The decode leg's literal batch: 256 sequences x 1 new token over 4096 cached keys each (1 Mi
+    cache rows, 512 MB a cache, made on the GPU).  Every request runs; the oracle checks a strided
+    sixteenth of them (requests 0, 16, .., 240 plus the last) on their own rows of the cache."""
+    B, NT, L = 256, 1, 4096
+    print(f"attn_decode B={B} NT={NT} ctx={L}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(55)
+    slots = B * L + 64
+    kc = torch.empty((slots, HKV, D), dtype=torch.uint8, device=dev)
+    vc = torch.empty_like(kc)
+    for c in (kc, vc):
+        for i in range(0, slots, 1 << 17):
+            n = min(1 << 17, slots - i)
+            c[i:i + n] = _e4m3(torch.randn((n, HKV, D), generator=g, device=dev))
+    q = torch.randn((B * NT, HQ, D), generator=g, device=dev).to(torch.bfloat16)
+    pt = torch.randperm(slots, generator=g, device=dev)[:B * L].to(torch.int32).view(B, L).contiguous()
+    seqlens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    ws = attn.DecodeWorkspace(B, dev)
+    out = attn.attn_decode(q, kc, vc, pt, seqlens, NT, SCALE, ws)
+    torch.cuda.synchronize()
+    sub = list(range(0, B, 16)) + [B - 1]
+    rows = pt[sub].reshape(-1).long()
+    h = dict(q=q.view(B, NT, HQ, D)[sub].reshape(-1, HQ, D).cpu(), kc=kc[rows].cpu(), vc=vc[rows].cpu(),
+             pt=torch.arange(len(sub) * L, dtype=torch.int32).view(len(sub), L),
+             seqlens=torch.full((len(sub),), L, dtype=torch.int32))
+    ref = _oracle(oracle_mod, h, NT)
+    got = out.view(B, NT, HQ, D)[sub].reshape(-1, HQ, D)
+    _check(got, ref, f"decode B={B} ctx={L} (strided subset of {len(sub)})")
+    assert torch.isfinite(out.float()).all()
+    del kc, vc
+
+
 def test_decode_writes_new_rows_first(attn, oracle_mod, dev):
     """out_loc: the new tokens' K/V rows land in their slots (bit-exact, other rows untouched) and
     the attention sees them; slots past the cache are skipped."""

@@ -112,3 +112,20 @@ def test_lmhead_ties_pick_first_index(lmh, dev):
     torch.cuda.synchronize()
     lg = logits.float().cpu().numpy()
     assert np.array_equal(np_(ids), lg.argmax(axis=1))  # numpy argmax = first maximal index
+
+
+@pytest.mark.parametrize("R,mode", [(16, "w8a16"), (64, "two_term"), (300, "one_term"), (300, "two_term")])
+def test_lmhead_fp32_logits_buffer(lmh, dev, R, mode):
+    """logits into an fp32 buffer (stock's next_token_logits_buffer, H/node.py:68-88): the same
+    bf16-rounded values as the bf16 output, widened, and the same ids, in every arithmetic form."""
+    V = 4096
+    print(f"lmhead fp32 logits R={R} mode={mode}", flush=True)
+    d, q, s = _setup(lmh, dev, R, V, seed=900 + R)
+    ws = lmh.Workspace(R, dev)
+    kw = dict(two_term=mode == "two_term", w8a16=mode == "w8a16")
+    ids16, lg16 = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, want_logits=True, **kw)
+    buf = torch.full((R, V), float("nan"), dtype=torch.float32, device=dev)
+    ids32, lg32 = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, logits=buf, **kw)
+    torch.cuda.synchronize()
+    assert lg32.data_ptr() == buf.data_ptr()
+    assert torch.equal(lg32, lg16.float()) and torch.equal(ids32, ids16)

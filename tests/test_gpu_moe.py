@@ -86,6 +86,38 @@ def test_route_bit_exact(q36, oracle_mod, dev, M, zipf, padded):
     assert int(np_(v["ctl"])[0]) == 0, "route ticket must be left at zero"
 
 
+def test_route_tie_rule(q36, oracle_mod, dev):
+    """Equal bf16 logits rank by id ascending (the tie rule of the top-k, logit desc then id asc): 13
+    experts share one router row and one bias of +10, so their logits are bitwise equal and the largest
+    of every token; the 10 picks of each token must be the 10 lowest of those ids in ascending order,
+    as the oracle has them.  Padded rows (position 0) stay out of the lists."""
+    from bundles_amd import synth
+    O = oracle_mod
+    M, E, k = 64, 512, 10
+    print("route tie rule M=64", flush=True)
+    d = synth.moe_inputs(M, dev, seed=77, E=E)
+    tied = [511, 3, 300, 7, 256, 100, 255, 200, 301, 400, 450, 480, 500]
+    rw = d["router_w"].clone()
+    rw[tied] = rw[42]
+    bias = torch.zeros(E, dtype=torch.float32, device=dev)
+    bias[tied] = 10.0
+    pos = torch.arange(1, M + 1, dtype=torch.int32, device=dev)
+    pos[::7] = 0
+    ws = q36.Workspace(E, 2048, 512, k, q36.Q36_MOE_FP8, dev)
+    v = q36.route(d["x"], pos, rw, k, ws, router_bias=bias)
+    torch.cuda.synchronize()
+    r = O.route(bits16(d["x"]), bits16(rw), k, bias=np_(bias), pos=np_(pos))
+    lg = np_(v["logits"])
+    assert (lg[:, tied] == lg[:, tied[:1]]).all(), "the tied experts' logits are not equal"
+    ids = np_(v["ids"])
+    live = np_(pos) != 0
+    assert (ids[live] == np.array(sorted(tied)[:k], dtype=np.int32)).all()
+    assert np.array_equal(ids, r["ids"])
+    assert np.array_equal(np_(v["wts"]).view(np.uint32), r["wts"].view(np.uint32))
+    for key in ("counts", "offsets", "perm", "inv_perm"):
+        assert np.array_equal(np_(v[key]), r[key]), key
+
+
 def _run_moe(q36, O, dev, M, E, dtype, seed, zipf=None, padded=False, debug=True):
     from bundles_amd import synth
     d = synth.moe_inputs(M, dev, seed=seed, E=E, zipf=zipf)

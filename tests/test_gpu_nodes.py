@@ -272,13 +272,26 @@ def test_layer_node_attention_verify(dev):
 
 
 class _Processor(torch.nn.Module):
-    """Stand-in for the served logits processor: logits = lm_head.quant_method.apply(...)."""
+    """Stand-in for the served logits processor: logits = lm_head.quant_method.apply(...); in decode
+    and verify modes the logits are then copied into the metadata's fp32 buffer when the shapes match
+    (stock's _copy_logits_to_buffer), and the buffer is what the processor returns."""
+
+    def __init__(self, vocab_size=None):
+        super().__init__()
+        self.vocab_size = vocab_size
+        self.logit_scale = None
 
     def forward(self, input_ids, hidden_states, lm_head, logits_metadata=None):
         qm = getattr(lm_head, "quant_method", None)
         if qm is not None:
-            return qm.apply(lm_head, hidden_states)
-        return torch.matmul(hidden_states, lm_head.weight.T)
+            logits = qm.apply(lm_head, hidden_states)
+        else:
+            logits = torch.matmul(hidden_states, lm_head.weight.T)
+        buf = getattr(logits_metadata, "next_token_logits_buffer", None)
+        if buf is not None and buf.shape == logits.shape:
+            buf.copy_(logits)
+            return buf
+        return logits
 
 
 @pytest.mark.parametrize("R", [8, 64, 100, 300])
@@ -320,3 +333,44 @@ def test_lmhead_node_logits_and_ids(dev, R):
     assert not node.Int8Head.serves(head32)
     out = node.forward(prepared, None, h.float(), head32)
     assert out.dtype == torch.float32
+
+
+@pytest.mark.parametrize("R", [8, 16, 64, 300])
+def test_lmhead_node_writes_the_fp32_logits_buffer(dev, R):
+    """A decode call with stock's fp32 next_token_logits_buffer of exactly [rows, vocab]: from 16 rows the
+    int8 head writes the bf16-rounded logits into it directly (stock's copy is then of the buffer onto
+    itself); below 16 rows a bf16 tensor comes back and stock copies it.  The buffer ends holding the
+    same values either way (H/node.py:68-88,136-149)."""
+    from bundles_amd.qwen36_lmhead8 import lmhead8, node
+    V = 4096
+    print(f"lmhead node fp32 buffer R={R}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(40 + R)
+    h = torch.randn((R, 2048), generator=g, device=dev).to(torch.bfloat16)
+    head = _Holder(weight=(torch.randn((V, 2048), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+    prepared = node.prepare(_Processor(vocab_size=V))
+    buf = torch.full((R, V), float("nan"), dtype=torch.float32, device=dev)
+    meta = types.SimpleNamespace(forward_mode=_Mode("decode"), next_token_logits_buffer=buf)
+    seen = []
+    apply0 = node.Int8Head.apply
+
+    def spy(self, layer, hidden_states, embedding_bias=None):
+        out = apply0(self, layer, hidden_states, embedding_bias)
+        seen.append(out)
+        return out
+    node.Int8Head.apply = spy
+    try:
+        out = node.forward(prepared, None, h, head, meta)
+    finally:
+        node.Int8Head.apply = apply0
+    q, s = lmhead8.quantize_rows(head.weight.data)
+    mode = node.row_mode(R, V)
+    ids, ref = lmhead8.w8a8_lmhead_argmax(h, q, s, lmhead8.Workspace(R, dev), want_logits=True,
+                                          two_term=mode == "two_term", w8a16=mode == "w8a16")
+    torch.cuda.synchronize()
+    assert out.data_ptr() == buf.data_ptr() and torch.equal(buf, ref.float())
+    assert (seen[0].data_ptr() == buf.data_ptr()) is (R >= node.LOGITS_BUF_MIN_ROWS)
+    assert torch.equal(prepared.last_ids, ids)
+    # a prefill (extend) call gets no buffer: a fresh bf16 tensor comes back
+    meta_x = types.SimpleNamespace(forward_mode=_Mode("extend"), next_token_logits_buffer=None)
+    out_x = node.forward(prepared, None, h, head, meta_x)
+    assert out_x.dtype == torch.bfloat16 and torch.equal(out_x, ref)
