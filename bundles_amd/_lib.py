@@ -31,8 +31,8 @@ class MoeArgs(C.Structure):
 
 
 class MoeWsLayout(C.Structure):
-    _fields_ = [(n, SZ) for n in ("logits", "ids", "wts", "counts", "offsets", "perm", "inv_perm", "active", "ctl",
-                                  "xq", "xs", "h", "y", "ecount", "eact", "elist", "tblocks", "total")]
+    _fields_ = [(n, SZ) for n in ("logits", "gate", "ids", "wts", "counts", "offsets", "perm", "inv_perm", "active", "ctl",
+                                  "xq", "xs", "h", "y", "ecount", "eact", "elist", "total")]
 
 
 class GdnArgs(C.Structure):

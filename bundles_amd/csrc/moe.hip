@@ -9,7 +9,8 @@
 //
 // Launch sequence on the caller's stream (no host synchronisation, graph-capturable):
 //   1. route_logits  router GEMV (bf16 logits, canonical reduction order) + per-token activation
-//                    quantization; also clears the per-expert counters for step 2
+//                    quantization and shared-expert gate sigmoid(x . gate_w); also clears the
+//                    per-expert counters for step 2
 //   2. route_topk    softmax / top-k / renormalise, one wave per token; each pick appends its slot
 //                    (t * k + j) to its expert's slot list through an atomic counter (the order
 //                    inside a list changes no output: every result is stored by slot)
@@ -20,7 +21,7 @@
 //                    unit's tokens (staged in LDS), SwiGLU -> h per slot
 //   4. moe_down      one workgroup per (unit, 128 output rows): the unit's h rows re-quantized
 //                    once in LDS, MFMA, x routing weight -> y per slot
-//   5. moe_combine   out = bf16(fma(sigmoid(x . gate_w), y_shared, sum_j y_j)), j in pick order
+//   5. moe_combine   out = bf16(fma(gate, y_shared, sum_j y_j)), j in pick order, gate from step 1
 // The shared expert is unit 0 of the up/down grids and covers every token.
 #include <string.h>
 
@@ -36,6 +37,11 @@ namespace {
 
 constexpr int kMaxM = 256;
 constexpr int kMaxE = 1024;
+// Token block of an expert work item: a workgroup takes at most 64 of a unit's tokens (one, two or
+// four 16-token tiles); an expert past 64 tokens gets one more work item per further 64.  (Blocks of
+// 32 were measured at decode batch 64: the hot experts' extra workgroups push the grid past one
+// round of two workgroups a CU, and the layer got slower, 60.1 against 59.2 us.)
+constexpr int kTokBlock = 64, kTokBlockShift = 6;
 
 struct MoeDev {
   int M, E, H, I, k;
@@ -54,6 +60,7 @@ struct MoeDev {
   const uint16_t* gate_w;
   uint16_t* out;
   float* logits;
+  float* gate;      // [M] sigmoid(x . gate_w) of each token (route_logits, when gate_w is given)
   int32_t* ids;
   float* wts;
   int32_t* counts;
@@ -63,10 +70,10 @@ struct MoeDev {
   int32_t* active;
   int32_t* ctl;
   int32_t* ecount;  // tokens per expert, counted by route_topk (zeroed by route_logits)
-  int32_t* eact;    // experts with tokens, in the order route_topk met them; ctl[2] counts them
+  int32_t* eact;    // [2E] routed work items e | j << 16 (token block j of expert e), in the order
+                    // route_topk opened them; ctl[2] counts them
   int32_t* elist;   // [E][M] slots of each expert, in the order route_topk met them
-  int32_t* tblocks;  // routed 64-token blocks past an expert's first: e | j << 16; ctl[4] counts them
-  int nsh;          // the shared expert's 64-token blocks past its first: ceil(M / 64) - 1
+  int nsh;          // the shared expert's token blocks past its first: ceil(M / kTokBlock) - 1
   uint8_t* xq;
   float* xs;
   uint16_t* h;
@@ -193,14 +200,35 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
     }
     return;
   }
-  // Quantization workgroup: one token.  Thread tid owns the 8-element chunks tid + 256 r.
+  // Quantization workgroup: one token.  Thread tid owns the 8-element chunks tid + 256 r.  Wave 0
+  // also forms the shared expert's gate sigmoid(x . gate_w) in the canonical order (lane l owns the
+  // 8-element chunks l + 64 j, fma in (j, element) order from zero, then an xor butterfly), so the
+  // combine reads one value instead of a dot product.
   const int t = bid - n_router_wg;
   const int tid = threadIdx.x;
+  if (wave == 0 && d.gate_w != nullptr) {
+    v4i xg[kRouteH / 512], gg[kRouteH / 512];
+#pragma unroll
+    for (int j = 0; j < kRouteH / 512; ++j) {
+      const int c = lane + 64 * j;
+      xg[j] = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)t * kRouteH + 8 * c));
+      gg[j] = ldg16(reinterpret_cast<const uint8_t*>(d.gate_w + 8 * c));
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRouteH / 512; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc = __builtin_fmaf(bf_lo((uint32_t)xg[j][q]), bf_lo((uint32_t)gg[j][q]), acc);
+        acc = __builtin_fmaf(bf_hi((uint32_t)xg[j][q]), bf_hi((uint32_t)gg[j][q]), acc);
+      }
+    acc = wave_sum_bfly(acc);
+    if (lane == 0) d.gate[t] = sigmoid_q(acc);
+  }
   if (t == 0) {
     for (int e = tid; e < d.E; e += 256) d.ecount[e] = 0;  // route_topk counts into them next
     if (tid == 0) {
       d.ctl[2] = 0;
-      d.ctl[4] = 0;
     }
   }
   const int nr = d.H / 2048 > 0 ? d.H / 2048 : 1;
@@ -355,9 +383,9 @@ __global__ __launch_bounds__(256) void route_topk_kernel(MoeDev d) {
     // not depend on it)
     const int pos = atomicAdd(&d.ecount[my_id], 1);
     d.elist[(size_t)my_id * d.M + pos] = t * k + lane;
-    if (pos == 0) d.eact[atomicAdd(&d.ctl[2], 1)] = my_id;
-    // every 64th token of an expert opens one more 64-token block for the expert kernels
-    if (pos > 0 && (pos & 63) == 0) d.tblocks[atomicAdd(&d.ctl[4], 1)] = my_id | ((pos >> 6) << 16);
+    // an expert's first token, and every 64th after it, opens a token block: one work item of the
+    // expert kernels, appended to the one compact list they read
+    if ((pos & (kTokBlock - 1)) == 0) d.eact[atomicAdd(&d.ctl[2], 1)] = my_id | ((pos >> kTokBlockShift) << 16);
   }
 }
 
@@ -555,47 +583,30 @@ __device__ __forceinline__ int slots_finish(const MoeDev& d, int unit, int e, co
   __syncthreads();
   return tot;
 }
-// The active count and unit u's expert (u >= 1) in one round trip: eact's entry of an idle unit may
-// hold a stale id, which the caller never uses.  Returns -2 when the unit is idle, -1 for the shared
-// expert, else the expert.
-__device__ __forceinline__ int unit_expert(const MoeDev& d, int unit) {
-  const int nact = d.ctl[2];
-  const int e = d.eact[unit > 0 ? unit - 1 : 0];
-  asm volatile("" ::"s"(nact), "s"(e));  // both loads issued before either is tested
-  if (unit == 0) return -1;
-  return unit - 1 < nact ? e : -2;
-}
 // The work item of expert-kernel workgroup b (8 consecutive workgroups per item, one per slice, on
-// the 8 XCDs): the first (E + 1) * 8 take token block 0 (tokens 0 .. 63 of the unit's list) of unit
-// b / 8; the ones after take block j >= 1 of a unit with more than 64 tokens -- first the shared
-// expert's blocks 1 .. nsh, then the routed blocks route_topk listed (idle past its count), so a hot
-// expert's tokens are spread over as many workgroups as it has 64-token blocks.  e: -2 idle, -1 the
-// shared expert, else the expert; unit 0 is the shared expert.
+// the 8 XCDs).  Items 0 .. nsh are the shared expert's token blocks; the items after them are the
+// routed blocks route_topk listed, compact at the front of the grid (idle past its count), so the
+// workgroups with work are dispatched first and a hot expert's later blocks start with the rest.
+// The list entry and its count come in one round trip (the entry's index does not depend on the
+// count).  e: -2 idle, -1 the shared expert, else the expert; unit 0 is the shared expert, 1 routed.
 struct WorkItem {
   int unit, e, tb, grp;
 };
 __device__ __forceinline__ WorkItem work_item(const MoeDev& d) {
-  const int b = blockIdx.x, nprim = (d.E + 1) * 8;
+  const int b = blockIdx.x, x = b >> 3, r = x - 1 - d.nsh;
   WorkItem it;
   it.grp = b & 7;
-  if (b < nprim) {
-    it.unit = b >> 3;
-    it.tb = 0;
-    it.e = unit_expert(d, it.unit);
-    return it;
-  }
-  const int x = (b - nprim) >> 3;
-  if (x < d.nsh) {
-    it.unit = 0;
-    it.tb = 1 + x;
-    it.e = -1;
-    return it;
-  }
-  const int n = d.ctl[4];
-  const int ent = d.tblocks[x - d.nsh];  // the grid holds at most M * k / 64 routed blocks, fewer than E
+  const int n = d.ctl[2];
+  const int ent = d.eact[min(max(r, 0), 2 * d.E - 1)];
   asm volatile("" ::"s"(n), "s"(ent));  // both loads issued before either is tested
+  if (r < 0) {
+    it.unit = 0;
+    it.e = -1;
+    it.tb = x;
+    return it;
+  }
   it.unit = 1;
-  it.e = x - d.nsh < n ? (ent & 0xffff) : -2;
+  it.e = r < n ? (ent & 0xffff) : -2;
   it.tb = ent >> 16;
   return it;
 }
@@ -620,7 +631,7 @@ constexpr int kMoeH = 2048, kMoeI = 512;
 // increasing block order from zero.
 constexpr int kUpD = 2;                    // weight stages in flight per wave
 constexpr int kUpBuf0 = 16 * (kMoeH + 16);  // 16 padded whole-K rows, or one 64 x 512-byte chunk
-constexpr int kUpBuf1 = 64 * 512;           // the other chunk buffer
+constexpr int kUpBuf1 = 16 * (kMoeH + 16);  // the second tile's 16 rows, or the other chunk
 constexpr int kUpGroups = kMoeI / 16 / 4;  // workgroups per unit (4 chunks each)
 // Buffer load of 16 bytes per lane straight into LDS (lane l writes lds + 16 l); offsets past the
 // buffer's size read as zero.
@@ -631,9 +642,9 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, void* lds, int 
 template <int DT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void moe_up_kernel(MoeDev d) {
   constexpr int H = kMoeH, I = kMoeI, NSTG = H / 128, TG = 64;
-  // activation rows: buffer 0 holds a one-tile group's 16 padded whole-K rows or the even K
-  // chunks of a four-tile group, buffer 1 the odd chunks.  Separate objects, so the compiler sees
-  // that a copy into one buffer does not touch reads of the other.
+  // activation rows: buffer 0 holds tile 0's 16 padded whole-K rows (one- and two-tile groups) or
+  // the even K chunks of a four-tile group, buffer 1 tile 1's rows or the odd chunks.  Separate
+  // objects, so the compiler sees that a copy into one buffer does not touch reads of the other.
   __shared__ __align__(16) uint8_t a_b0[kUpBuf0];
   __shared__ __align__(16) uint8_t a_b1[kUpBuf1];
   __shared__ __align__(16) float xs_t[TG * NSTG];            // [NSTG][TG] (token fastest)
@@ -644,7 +655,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   static_assert(kUpGroups == 8, "8 workgroups per work item");
   const WorkItem it = work_item(d);
   if (it.e == -2) return;
-  const int unit = it.unit, grp = it.grp, e = it.e, g0 = 64 * it.tb;
+  const int unit = it.unit, grp = it.grp, e = it.e, g0 = it.tb << kTokBlockShift;
   const bool shared = unit == 0;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
   const uint8_t* W = shared ? d.sw13 : d.w13 + (size_t)e * 2 * I * H;
@@ -687,28 +698,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int n = ch * 16 + lr;
   // One group of up to TG tokens with NTT 16-token tiles (rows past the group's tokens are zero):
   // per 128-byte stage every fragment and scale read first, then the independent MFMAs, then the
-  // scaled accumulates (e4m3: in block order from zero), then SwiGLU -> h per slot.  A one-tile
-  // group holds its rows' whole K in LDS; a four-tile group one K half at a time.
+  // scaled accumulates (e4m3: in block order from zero), then SwiGLU -> h per slot.  One- and
+  // two-tile groups hold their rows' whole K in LDS (a tile a buffer); a four-tile group streams K.
   auto group = [&](int g0, auto nttc, auto firstc) {
     constexpr int NTT = decltype(nttc)::value;
     constexpr bool FIRST = decltype(firstc)::value;  // the weight stages 0 .. kUpD-1 are in flight
-    // activation rows in LDS: a one-tile group holds its 16 rows' whole K (padded rows, one
-    // buffer); a four-tile group streams K in 4 chunks of 512 bytes through two buffers, so the
+    // activation rows in LDS: one- and two-tile groups hold their rows' whole K (padded rows, tile t
+    // in buffer t); a four-tile group streams K in 4 chunks of 512 bytes through two buffers, so the
     // next chunk's copy overlaps the current chunk's stages and the weight stream never drains.
     // Ring rows are unpadded: 16-byte piece p of row r sits at position p ^ (r % 16), which puts
     // the 16 rows of one MFMA read on distinct banks.
-    constexpr int NC = NTT == 1 ? 1 : 4, KC = H / NC, SPC = NSTG / NC;
-    constexpr int ROWB = NC == 1 ? KC + 16 : KC, BUFB = 16 * NTT * ROWB;
-    static_assert(BUFB <= kUpBuf0 && (NC == 1 || BUFB <= kUpBuf1), "activation rows exceed their buffers");
+    static_assert(NTT == 1 || NTT == 2 || NTT == 4, "one, two or four token tiles");
+    constexpr int NC = NTT == 4 ? 4 : 1, KC = H / NC, SPC = NSTG / NC;
+    constexpr int ROWB = NC == 1 ? KC + 16 : KC, BUFB = 16 * (NC == 1 ? 1 : NTT) * ROWB;
+    static_assert(BUFB <= kUpBuf0 && BUFB <= kUpBuf1, "activation rows exceed their buffers");
     static_assert(NC == 1 || kUpD <= SPC, "a chunk must issue a full window of weight stages");
     using Acc = typename std::conditional<DT == Q36_MOE_FP8, v4f, v4i>::type;
     // The byte offset of each row this lane copies (its token row, or past the activations for rows
     // past the group, which read as zero), formed once for all chunks.  The token reads are made
     // unconditional: left to the compiler they sat in branches, one LDS round trip per copy.
-    // One tile: wave w copies rows w, w + 4, ..., 1 KB per call (lane l: bytes 16 l ..).  Four
-    // tiles: one call fills two rows (lanes 0-31 row 2m, lanes 32-63 row 2m + 1), wave w takes the
-    // row pairs w, w + 4, ..., and a lane fetches the piece that belongs at its position.
-    constexpr int NRC = NC == 1 ? 4 : 8 * NTT / 4;
+    // One or two tiles: wave w copies rows w, w + 4, ..., 1 KB per call (lane l: bytes 16 l ..).
+    // Four tiles: one call fills two rows (lanes 0-31 row 2m, lanes 32-63 row 2m + 1), wave w takes
+    // the row pairs w, w + 4, ..., and a lane fetches the piece that belongs at its position.
+    constexpr int NRC = NC == 1 ? 4 * NTT : 8 * NTT / 4;
     int rowoff[NRC];
 #pragma unroll
     for (int k = 0; k < NRC; ++k) {
@@ -721,11 +733,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     auto rows_dma = [&](int c) {
       if constexpr (NC == 1) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int rr = wave + 4 * k;
+        for (int k = 0; k < NRC; ++k) {
+          const int rr = wave + 4 * k;  // rows 0-15 tile 0 (buffer 0), 16-31 tile 1 (buffer 1)
+          uint8_t* dst = (rr < 16 ? a_b0 : a_b1) + (rr & 15) * ROWB;
           const int voff = rowoff[k] < d.M * H ? rowoff[k] + lane * 16 : d.M * H;
 #pragma unroll
-          for (int h = 0; h < KC / 1024; ++h) dma16(xrs, a_b0 + rr * ROWB + h * 1024, voff + h * 1024);
+          for (int h = 0; h < KC / 1024; ++h) dma16(xrs, dst + h * 1024, voff + h * 1024);
         }
       } else {
         uint8_t* buf = (c & 1) ? a_b1 : a_b0;
@@ -787,7 +800,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         asm volatile("" ::: "memory");
       }
       if (c + 1 < NC) rows_dma(c + 1);
-      const uint8_t* buf = (c & 1) ? a_b1 : a_b0;
 #pragma unroll
       for (int sl = 0; sl < SPC; ++sl) {
         const int s = c * SPC + sl;
@@ -795,7 +807,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         v4i a[NTT][2];
 #pragma unroll
         for (int tt = 0; tt < NTT; ++tt) {
-          const int row = tt * 16 + lr;
+          // whole K: tile tt's rows in buffer tt; chunks: chunk c in buffer c % 2, rows of every tile
+          const uint8_t* buf = NC == 1 ? (tt == 0 ? a_b0 : a_b1) : ((c & 1) ? a_b1 : a_b0);
+          const int row = NC == 1 ? lr : tt * 16 + lr;
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const int piece = sl * 8 + lgp * 2 + h;  // 16-byte piece within the row's chunk
@@ -865,10 +879,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
   };
-  // the work item's token block, as one tile (most experts at decode sizes) or four (rows past the
-  // tokens are zero); a third instance would cost registers in all of them
-  if (cnt - g0 <= 16)
+  // the work item's token block (at most 64 tokens) as one, two or four 16-token tiles (rows past
+  // the tokens are zero)
+  const int nb = min(cnt - g0, kTokBlock);
+  if (nb <= 16)
     group(g0, std::integral_constant<int, 1>{}, std::true_type{});
+  else if (nb <= 32)
+    group(g0, std::integral_constant<int, 2>{}, std::true_type{});
   else
     group(g0, std::integral_constant<int, 4>{}, std::true_type{});
 }
@@ -903,7 +920,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   static_assert(kDnGroups == 8, "8 workgroups per work item");
   const WorkItem it = work_item(d);
   if (it.e == -2) return;
-  const int unit = it.unit, grp = it.grp, e = it.e, g0 = 64 * it.tb;
+  const int unit = it.unit, grp = it.grp, e = it.e, g0 = it.tb << kTokBlockShift;
   const bool shared = unit == 0;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, lgp = lane >> 4;
   const uint8_t* W = shared ? d.sw2 : d.w2 + (size_t)e * H * I;
@@ -1085,9 +1102,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   };
-  static_assert(kDnTG == 64, "a work item is one 64-token block");
-  if (cnt - g0 <= 16)
+  static_assert(kDnTG == 64, "a work item is one token block of at most 64 tokens");
+  const int nb = min(cnt - g0, kTokBlock);
+  if (nb <= 16)
     group(g0, std::integral_constant<int, 1>{}, std::true_type{});
+  else if (nb <= 32)
+    group(g0, std::integral_constant<int, 2>{}, std::true_type{});
   else
     group(g0, std::integral_constant<int, 4>{}, std::true_type{});
 }
@@ -1108,33 +1128,19 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool valid = d.pos == nullptr || d.pos[t] != 0;
   const int S = d.M * d.k;
-  __shared__ float gate_s, rstd_s;
-  __shared__ int prow[17];
+  __shared__ float rstd_s;
   __shared__ float zs[kCombH / 8][8];
-  if (tid <= d.k) prow[tid] = tid < d.k ? t * d.k + tid : S + t;
-  if (valid && wave == 0) {
-    float acc = 0.f;
-    for (int j = 0; j < kCombH / 512; ++j) {
-      const int c = lane + 64 * j;
-      const v4i xv = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)t * kCombH + 8 * c));
-      const v4i gv = ldg16(reinterpret_cast<const uint8_t*>(d.gate_w + 8 * c));
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        acc = __builtin_fmaf(bf_lo((uint32_t)xv[q]), bf_lo((uint32_t)gv[q]), acc);
-        acc = __builtin_fmaf(bf_hi((uint32_t)xv[q]), bf_hi((uint32_t)gv[q]), acc);
-      }
-    }
-    acc = wave_sum_bfly(acc);
-    if (lane == 0) gate_s = sigmoid_q(acc);
-  }
-  __syncthreads();
   const int c = tid;  // the thread's 8-element chunk (H = 2048: one per thread)
   uint4 o = make_uint4(0u, 0u, 0u, 0u);
   if (valid) {
+    // every y row of the token and its gate in one round trip (rows past k repeat the shared row)
+    const float gate = d.gate[t];
     v4i yv[17];
 #pragma unroll
-    for (int j = 0; j < 17; ++j)
-      yv[j] = ldg16(reinterpret_cast<const uint8_t*>(d.y + (size_t)prow[j <= d.k ? j : d.k] * kCombH + 8 * c));
+    for (int j = 0; j < 17; ++j) {
+      const int row = j < d.k ? t * d.k + j : S + t;
+      yv[j] = ldg16(reinterpret_cast<const uint8_t*>(d.y + (size_t)row * kCombH + 8 * c));
+    }
     float acc[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[q] = 0.f;
@@ -1152,7 +1158,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
 #pragma unroll
     for (int j = 1; j < 17; ++j)
       if (j == d.k) sv = yv[j];
-    const float g = gate_s;
+    const float g = gate;
     uint32_t w[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -1214,6 +1220,7 @@ int layout(int M, int E, int H, int I, int k, int dtype, q36_moe_ws_layout* L) {
   const size_t S = (size_t)M * k;
   L->ctl = take(sizeof(int32_t) * 64);
   L->logits = take(sizeof(float) * (size_t)M * E);
+  L->gate = take(sizeof(float) * (size_t)M);
   L->ids = take(sizeof(int32_t) * S);
   L->wts = take(sizeof(float) * S);
   L->counts = take(sizeof(int32_t) * E);
@@ -1222,9 +1229,8 @@ int layout(int M, int E, int H, int I, int k, int dtype, q36_moe_ws_layout* L) {
   L->inv_perm = take(sizeof(int32_t) * S);
   L->active = take(sizeof(int32_t) * E);
   L->ecount = take(sizeof(int32_t) * E);
-  L->eact = take(sizeof(int32_t) * E);
+  L->eact = take(sizeof(int32_t) * 2 * (size_t)E);
   L->elist = take(sizeof(int32_t) * (size_t)E * M);
-  L->tblocks = take(sizeof(int32_t) * (size_t)E);
   L->xq = take((size_t)M * H);
   L->xs = take(sizeof(float) * (size_t)M * (dtype == Q36_MOE_FP8 ? H / 128 : 1));
   L->h = take(sizeof(uint16_t) * (S + M) * I);
@@ -1263,13 +1269,14 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
               a->positions, static_cast<const uint8_t*>(a->w13), a->s13, static_cast<const uint8_t*>(a->w2), a->s2,
               static_cast<const uint8_t*>(a->sw13), a->ss13, static_cast<const uint8_t*>(a->sw2), a->ss2,
               static_cast<const uint16_t*>(a->gate_w), static_cast<uint16_t*>(a->out),
-              reinterpret_cast<float*>(ws + L.logits), reinterpret_cast<int32_t*>(ws + L.ids),
+              reinterpret_cast<float*>(ws + L.logits), reinterpret_cast<float*>(ws + L.gate),
+              reinterpret_cast<int32_t*>(ws + L.ids),
               reinterpret_cast<float*>(ws + L.wts), reinterpret_cast<int32_t*>(ws + L.counts),
               reinterpret_cast<int32_t*>(ws + L.offsets), reinterpret_cast<int32_t*>(ws + L.perm),
               reinterpret_cast<int32_t*>(ws + L.inv_perm), reinterpret_cast<int32_t*>(ws + L.active),
               reinterpret_cast<int32_t*>(ws + L.ctl), reinterpret_cast<int32_t*>(ws + L.ecount),
               reinterpret_cast<int32_t*>(ws + L.eact), reinterpret_cast<int32_t*>(ws + L.elist),
-              reinterpret_cast<int32_t*>(ws + L.tblocks), (a->M + 63) / 64 - 1,
+              (a->M + kTokBlock - 1) / kTokBlock - 1,
               reinterpret_cast<uint8_t*>(ws + L.xq),
               reinterpret_cast<float*>(ws + L.xs), reinterpret_cast<uint16_t*>(ws + L.h),
               reinterpret_cast<uint16_t*>(ws + L.y), a->dbg_acc13, a->dbg_acc2,
@@ -1300,11 +1307,11 @@ int launch_lists(const MoeDev& d, hipStream_t st) {
   return check_launch("q36_moe_route");
 }
 
-// Expert-kernel grid: 8 workgroups per unit's first 64-token block, then 8 per further block: the
-// shared expert's nsh, and room for every routed one (an expert past 64 tokens only when M > 64; at
-// most M k / 64 blocks in all, fewer than E)
+// Expert-kernel grid: 8 workgroups per work item: the shared expert's 1 + nsh blocks, and room for
+// every routed block (one per active expert, at most E, and the further ones: an expert past 64
+// tokens only when M > 64, at most M k / 64 of them, fewer than E, so the list holds 2E)
 int expert_grid(const MoeDev& d) {
-  const int nrb = d.M > 64 ? d.M * d.k / 64 : 0;
+  const int nrb = d.M > kTokBlock ? d.M * d.k / kTokBlock : 0;
   return 8 * (d.E + 1 + d.nsh + nrb);
 }
 template <int DT>

@@ -108,6 +108,7 @@ typedef struct q36_moe_args {
 
 typedef struct q36_moe_ws_layout {
   size_t logits;   /* fp32 [M,E] bf16-rounded router logits (+bias) */
+  size_t gate;     /* fp32 [M] shared-expert gate sigmoid(x . gate_w) (route-internal) */
   size_t ids;      /* int32 [M,topk], -1 for padding rows */
   size_t wts;      /* fp32 [M,topk] renormalised routing weights */
   size_t counts;   /* int32 [E] */
@@ -121,24 +122,25 @@ typedef struct q36_moe_ws_layout {
   size_t h;        /* bf16 [M*topk+M, I] by slot (t*topk + j; shared M*topk + t) */
   size_t y;        /* bf16 [M*topk+M, H] by slot, routing weight applied */
   size_t ecount;   /* int32 [E] tokens per expert (route-internal) */
-  size_t eact;     /* int32 [E] experts with tokens, unordered (route-internal; ctl[2] counts) */
+  size_t eact;     /* int32 [2E] work items of the expert kernels, e | j << 16 (token block j of expert e),
+                    * unordered (route-internal; ctl[2] counts them) */
   size_t elist;    /* int32 [E, M] slots of each expert, unordered (route-internal) */
-  size_t tblocks;  /* int32 [E] 64-token blocks past an expert's first, e | j << 16, unordered
-                    * (route-internal; ctl[4] counts them) */
   size_t total;
 } q36_moe_ws_layout;
 
 size_t q36_moe_workspace_bytes(int32_t M, int32_t E, int32_t H, int32_t I, int32_t topk, int32_t dtype);
 int q36_moe_workspace_layout(int32_t M, int32_t E, int32_t H, int32_t I, int32_t topk, int32_t dtype,
                              q36_moe_ws_layout* out);
-/* Routing only: logits, ids, wts and the expert lists, plus the quantized x. */
+/* Routing only: logits, ids, wts and the expert lists, plus the quantized x and, when gate_w is
+ * given, the shared expert's gate sigmoid(x . gate_w) per token (the combine reads it). */
 int q36_moe_route(const q36_moe_args* a, q36_stream_t stream);
 /* The phases of the block, each one stream-ordered launch set over the same workspace, for
  * callers that schedule them apart (the reference exposes the same split: up
  * L/qk_moe_up16.cu:329, down L/qk_moe_dn16.cu:301, combine_norm L/qk_route.cu:1270).
  *   q36_moe_up:      routed + shared gate/up GEMM and SwiGLU -> h   (needs q36_moe_route first)
  *   q36_moe_down:    down GEMM x routing weight -> y               (needs q36_moe_up first)
- *   q36_moe_combine: out = bf16(fma(sigmoid(x . gate_w), y_shared, sum_j y_j)) */
+ *   q36_moe_combine: out = bf16(fma(sigmoid(x . gate_w), y_shared, sum_j y_j))
+ *                    (the gate as the preceding q36_moe_route with gate_w formed it) */
 int q36_moe_up(const q36_moe_args* a, q36_stream_t stream);
 int q36_moe_down(const q36_moe_args* a, q36_stream_t stream);
 int q36_moe_combine(const q36_moe_args* a, q36_stream_t stream);
