@@ -72,19 +72,22 @@ def _moe_layers(torch, dev, n_layers, zipf, seed0):
     return x, layers
 
 
-def bench_moe(args, torch, dev, n_layers=1, zipf=1.1, seed0=0):
-    """One MoE layer over a batch of 64 tokens, replayed as a captured graph.  With n_layers > 1 the
-    graph cycles that many layers with distinct expert sets (each step = one layer), so the working
-    set (n_layers x the active experts' bytes) exceeds the 256 MB last-level cache and every weight
-    byte comes from HBM; n_layers = 1 replays one layer, whose weights stay cache-resident (warm)."""
+def bench_moe(args, torch, dev, n_layers=1, zipf=1.1, seed0=0, prebuilt=None, M=64):
+    """One MoE layer over a batch of M tokens (64: the configuration), replayed as a captured graph.
+    With n_layers > 1 the graph cycles that many layers with distinct expert sets (each step = one
+    layer), so the working set (n_layers x the active experts' bytes) exceeds the 256 MB last-level
+    cache and every weight byte comes from HBM; n_layers = 1 replays one layer, whose weights stay
+    cache-resident (warm).  prebuilt: (x, layers) from _moe_layers, whose first M rows are used."""
     from bundles_amd.qwen36_layer import moe
 
-    M, E, H, I, K = 64, 512, 2048, 512, 10
-    x, layers = _moe_layers(torch, dev, n_layers, zipf, seed0)
+    E, H, I, K = 512, 2048, 512, 10
+    x, layers = prebuilt if prebuilt is not None else _moe_layers(torch, dev, n_layers, zipf, seed0)
+    n_layers = len(layers)
+    x = x[:M].contiguous()
 
     def run_layer(L):
         d = L["d"]
-        moe.moe_row_batch(x, None, d["router_w"], d["gate_w"], L["ew"], K, L["ws"], out=L["out"],
+        moe.moe_row_batch(x, None, d["router_w"], d["gate_w"], L["ew"], K, L["ws"], out=L["out"][:M],
                           router_bias=d["router_bias"])
 
     def step_all():
@@ -121,7 +124,7 @@ def bench_moe(args, torch, dev, n_layers=1, zipf=1.1, seed0=0):
     # launches of one phase run back to back, cycling the layers (each layer's workspace keeps the
     # lists and rows its earlier phases wrote), so with several layers every launch reads its weights
     # from HBM
-    phases = [dict(moe.moe_phases(x, None, L["d"]["router_w"], L["d"]["gate_w"], L["ew"], K, L["ws"], L["out"],
+    phases = [dict(moe.moe_phases(x, None, L["d"]["router_w"], L["d"]["gate_w"], L["ew"], K, L["ws"], L["out"][:M],
                                   router_bias=L["d"]["router_bias"])) for L in layers]
     order = ("route", "up", "down", "combine")
     phase_ms = {}
@@ -151,8 +154,93 @@ def bench_moe(args, torch, dev, n_layers=1, zipf=1.1, seed0=0):
         bytes_up=int(bytes_up), bytes_down=int(bytes_down), bytes_layer=int(bytes_layer),
         up_gbs=bytes_up / (phase_ms["up"] * 1e-3) / 1e9, down_gbs=bytes_down / (phase_ms["down"] * 1e-3) / 1e9,
         layer_gbs=bytes_layer / (ms_graph * 1e-3) / 1e9,
+        frac_hbm_layer=bytes_layer / (ms_graph * 1e-3) / 1e9 / HBM_PEAK_GBS,
     )
     res["_host"] = (layers[0]["ew"], dict(layers[0]["d"], x=x))
+    return res
+
+
+SMALL_LAYERS = 8  # MoE layers cycled by the small-batch legs (their active experts exceed the 256 MB cache)
+
+
+def bench_small(args, torch, dev):
+    """The decode-sized paths at the row counts a speculative-decode step sends them (1 - 32 rows),
+    each cold (weights cycled past the 256 MB last-level cache) with its HBM fraction:
+      moe_m{1,4,8,16}   the fp8 MoE layer (config 2 shapes, Zipf router), 8 layers cycled in one graph
+      dense8_*          the DENSE8 W8A16 projections of the recurrent block: in_proj [12352, 2048]
+                        (12 copies cycled) and out_proj / o_proj [2048, 4096] (36 copies)
+      lmhead_w8a16      the int8 lm_head [151936, 2048] in its W8A16 form + argmax (2 copies)
+    Each dense / lm_head point is a graph of one call per copy, replayed; per call."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import formats, glue
+    from bundles_amd.qwen36_lmhead8 import lmhead8
+    res = {}
+    built = _moe_layers(torch, dev, SMALL_LAYERS, 1.1, 1000)
+    for M in (1, 4, 8, 16):
+        r = bench_moe(args, torch, dev, prebuilt=built, M=M)
+        r.pop("_host")
+        res[f"moe_m{M}"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()
+                            if k in ("ms_graph", "tokens_per_s", "phase_ms", "unique_experts", "bytes_layer",
+                                     "layer_gbs", "frac_hbm_layer", "working_set_mb", "up_gbs", "down_gbs")}
+        print(f"bench: MoE M={M} done ({r['ms_graph'] * 1e3:.1f} us/layer, U={r['unique_experts']})",
+              file=sys.stderr, flush=True)
+    del built
+    torch.cuda.empty_cache()
+
+    def graph_time(calls):
+        for c in calls:
+            c()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for c in calls:
+                c()
+        g.replay()
+        torch.cuda.synchronize()
+        reps = max(3, args.steps // 4)
+        return events_time(g.replay, reps, torch) / len(calls)
+
+    gen = torch.Generator(device=dev).manual_seed(7)
+    for name, N, K, copies in (("dense8_in_proj", 12352, 2048, 12), ("dense8_o_proj", 2048, 4096, 36)):
+        ws_ = []
+        for _ in range(copies):
+            w = (torch.randn((N, K), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+            ws_.append(formats.quant_dense8(w))
+            del w
+        pts = {}
+        for T in (1, 4, 16, 32):
+            x = torch.randn((T, K), generator=gen, device=dev).to(torch.bfloat16)
+            y = torch.empty((T, N), dtype=torch.bfloat16, device=dev)
+            calls = [lambda q=q, s=s: glue.dense8_linear(x, q, s, segments=[(0, y)]) for q, s in ws_]
+            ms = graph_time(calls)
+            algo = N * K + (K // 128) * N * 2 + T * K * 2 + T * N * 2
+            pts[f"t{T}"] = dict(us=round(ms * 1e3, 2), bytes=algo, gbs=round(algo / (ms * 1e-3) / 1e9, 1),
+                                frac_hbm=round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        res[name] = dict(rows=N, k=K, copies_cycled=copies, **pts)
+        print(f"bench: {name} done", file=sys.stderr, flush=True)
+        del ws_
+        torch.cuda.empty_cache()
+
+    V = 151936
+    heads = []
+    for c in range(2):
+        d = synth.lmhead_inputs(32, V, dev, seed=50 + c)
+        heads.append(lmhead8.quantize_rows(d["w"]))
+        del d["w"]
+    wsl = lmhead8.Workspace(32, dev)
+    pts = {}
+    for R in (1, 4, 16, 32):
+        h = torch.randn((R, 2048), generator=gen, device=dev).to(torch.bfloat16)
+        ids = torch.empty(R, dtype=torch.int32, device=dev)
+        calls = [lambda q=q, s=s: lmhead8.w8a8_lmhead_argmax(h, q, s, wsl, ids=ids, w8a16=True) for q, s in heads]
+        ms = graph_time(calls)
+        algo = V * 2048 + V * 4 + R * 2048 * 2 + R * 4
+        pts[f"r{R}"] = dict(us=round(ms * 1e3, 2), bytes=algo, gbs=round(algo / (ms * 1e-3) / 1e9, 1),
+                            frac_hbm=round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+    res["lmhead_w8a16"] = dict(vocab=V, copies_cycled=2, **pts)
+    print("bench: W8A16 lm_head done", file=sys.stderr, flush=True)
+    del heads
+    torch.cuda.empty_cache()
     return res
 
 
@@ -520,7 +608,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="moe,moe_high_u,gdn,gdn_ring,lmhead,attn,decode,hybrid",
+    ap.add_argument("--only", default="moe,moe_high_u,gdn,gdn_ring,lmhead,attn,decode,hybrid,small",
                     help="comma list of the nodes to run (the headline needs moe; without it the line "
                          "carries the listed legs only)")
     ap.add_argument("--copy-calib", action="store_true",
@@ -553,7 +641,7 @@ def main():
         print(f"bench: MoE unskewed router done ({moe_hiu['ms_graph'] * 1e3:.1f} us/layer, "
               f"U={moe_hiu['unique_experts']})", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
-    gdn_res = ring_res = lmh_res = attn_res = dec_res = hyb_res = None
+    gdn_res = ring_res = lmh_res = attn_res = dec_res = hyb_res = small_res = None
     if "gdn" in only:
         print("bench: GDN verify 32 x 5", file=sys.stderr, flush=True)
         gdn_res = bench_gdn(args, torch, dev)
@@ -577,6 +665,10 @@ def main():
               flush=True)
         hyb_res = bench_hybrid(args, torch, dev)
         torch.cuda.empty_cache()
+    if "small" in only:
+        print("bench: decode-sized paths (MoE at 1-16 rows, DENSE8 projections, W8A16 lm_head)", file=sys.stderr,
+              flush=True)
+        small_res = bench_small(args, torch, dev)
     if args.copy_calib:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -591,7 +683,7 @@ def main():
         line = {"metric": "per-leg run (no headline: --only without moe)", "value": None, "n_gpus": 1,
                 "legs": sorted(only)}
         legs = {"lmhead": lmh_res, "attn": attn_res, "decode": dec_res, "hybrid": hyb_res, "gdn": gdn_res,
-                "gdn_ring": ring_res}
+                "gdn_ring": ring_res, "small": small_res}
         for k, v in legs.items():
             if v is not None:
                 line[k] = {kk: (round(vv, 3) if isinstance(vv, float) else vv) for kk, vv in v.items()
@@ -625,6 +717,8 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "moe_up_kernel<fp8>", "achieved": round(up_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(up_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("moe_up_kernel<fp8>")},
+        # the whole layer (route, up, down, combine) against the same peak: algorithmic bytes / layer time
+        "frac_hbm_layer": round(moe_res["frac_hbm_layer"], 4),
         "cpu_baseline": cpu,
         "moe": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in moe_res.items()},
         "moe_warm": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in moe_warm.items()
@@ -672,6 +766,8 @@ def main():
                         "tokens, 4096 cached keys; one captured graph per step; us_per_step with the GDN verify "
                         "in the served ring form (8 committed entries, conv states restored each step inside the "
                         "graph), us_per_step_snapshot with per-position snapshots"}
+    if small_res:
+        line["small_batch"] = small_res
     if gdn_res:
         line["gdn_verify"] = {
             "us_per_step": round(gdn_res["us_per_step"], 2), "bytes": gdn_res["bytes"],
