@@ -355,11 +355,61 @@ def bench_attn(args, torch, dev):
     torch.cuda.synchronize()
     ms_pg = events_time(gp.replay, max(1, args.steps // inner), torch) / inner
     ms_og = events_time(go.replay, max(1, args.steps // inner), torch) / inner
+    # the node's form: x quantized by the add-norm that writes it, the o_proj input by the attention's
+    # epilogue (the same bits), so the projections skip their act_quant launches; the producers' extra
+    # cost is measured on the add-norm (its e4m3 output against none)
+    from bundles_amd.qwen36_layer import glue
+    gen = torch.Generator(device=dev).manual_seed(11)
+    res_ = torch.randn((T, 2048), generator=gen, device=dev).to(torch.bfloat16)
+    delta_ = torch.randn((T, 2048), generator=gen, device=dev).to(torch.bfloat16)
+    nw_ = (torch.randn(2048, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
+    hn_ = torch.empty_like(res_)
+    xq = attn_fused.proj_rows(T, dev)
+    glue.add_rmsnorm(delta_, res_.clone(), nw_, 1e-6, out=hn_, q8=xq)
+    ref_q = attn_fused.attn_proj(hn_, w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"],
+                                 ws)["q"].clone()
+    # the o_proj input from a real verify attention (32 requests x 4 tokens over 512 cached keys)
+    NT, nb, ctx = 4, T // 4, 512
+    kc = torch.randn((nb * ctx, 2, 256), generator=gen, device=dev).to(torch.float8_e4m3fn).view(torch.uint8)
+    vc = torch.randn((nb * ctx, 2, 256), generator=gen, device=dev).to(torch.float8_e4m3fn).view(torch.uint8)
+    pt = torch.arange(nb * ctx, dtype=torch.int32, device=dev).view(nb, ctx).contiguous()
+    sl = torch.full((nb,), ctx, dtype=torch.int32, device=dev)
+    aq = attn_fused.oproj_rows(T, dev)
+    att = attn_fused.attn_decode(o["q"], kc, vc, pt, sl, NT, 1.0 / 16, attn_fused.DecodeWorkspace(nb, dev),
+                                 gate=gate, oq=aq)
+    ref_out = attn_fused.attn_oproj(att.view(T, 4096), gate, w, ws).clone()
+
+    def proj_q():
+        attn_fused.attn_proj(None, w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"], ws, out=o,
+                             xq=xq)
+
+    def oproj_q():
+        attn_fused.attn_oproj(None, None, w, ws, out=out, aq=aq)
+
+    proj_q()
+    oproj_q()
+    torch.cuda.synchronize()
+    same = bool(torch.equal(o["q"], ref_q) and torch.equal(out, ref_out))
+
+    def graph_ms(fn):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(inner):
+                fn()
+        torch.cuda.synchronize()
+        return events_time(g.replay, max(1, args.steps // inner), torch) / inner
+
+    ms_pq, ms_oq = graph_ms(proj_q), graph_ms(oproj_q)
+    ms_n0 = graph_ms(lambda: glue.add_rmsnorm(delta_, res_, nw_, 1e-6, out=hn_))
+    ms_n1 = graph_ms(lambda: glue.add_rmsnorm(delta_, res_, nw_, 1e-6, out=hn_, q8=xq))
     wbytes = 9216 * 2048 + 72 * 16 * 4 + 2048 * 4096 + 16 * 32 * 4
     abytes = T * 2048 * 2 + T * (8192 + 1024) * 2 + T * 1024 + 2 * T * 4096 * 2 + T * 2048 * 2
     tot = wbytes + abytes
     return dict(us_proj=ms_p * 1e3, us_oproj=ms_o * 1e3, us_proj_graph=ms_pg * 1e3, us_oproj_graph=ms_og * 1e3,
-                bytes=tot, gbs=tot / ((ms_p + ms_o) * 1e-3) / 1e9)
+                bytes=tot, gbs=tot / ((ms_p + ms_o) * 1e-3) / 1e9,
+                us_proj_prequant_graph=ms_pq * 1e3, us_oproj_prequant_graph=ms_oq * 1e3,
+                prequant_same_bits=same, us_add_norm=ms_n0 * 1e3, us_add_norm_with_codes=ms_n1 * 1e3,
+                gbs_prequant=tot / ((ms_pq + ms_oq) * 1e-3) / 1e9)
 
 
 def bench_decode(args, torch, dev):
@@ -408,21 +458,23 @@ def bench_hybrid(args, torch, dev):
     B, T, ctx = 64, 4, 4096
     w = hybrid.make_weights(dev, seed=0)
     res = {}
-    for form in ("ring", "snapshot"):
+    for form in ("ring", "snapshot", "ring_own_quant"):
         res[form] = _hybrid_form(args, torch, dev, hybrid, synth, w, B, T, ctx, form)
         torch.cuda.empty_cache()
     out = dict(res["ring"])
     out["us_per_step_snapshot"] = res["snapshot"]["us_per_step"]
+    out["us_per_step_own_quant"] = res["ring_own_quant"]["us_per_step"]
     return out
 
 
 def _hybrid_form(args, torch, dev, hybrid, synth, w, B, T, ctx, form):
-    st = hybrid.make_state(B, T, ctx, dev, seed=1, gdn_form=form)
-    ws = hybrid.HybridWorkspace(B, T, w.E, dev, snapshots=form == "snapshot")
+    st = hybrid.make_state(B, T, ctx, dev, seed=1, gdn_form="snapshot" if form == "snapshot" else "ring")
+    # ring_own_quant: every projection quantizes its own input (no producer-written e4m3 rows)
+    ws = hybrid.HybridWorkspace(B, T, w.E, dev, snapshots=form == "snapshot", prequant=form != "ring_own_quant")
     x = synth.randn((B * T, 2048), synth.gen(dev, 2), dev)
     # the ring form rolls the GDN conv states in place: every step starts from the same committed
     # states (the copies run inside the timed graph, as the engine's rollback to the accepted window)
-    saved = [c.clone() for c in st.conv_state] if form == "ring" else []
+    saved = [c.clone() for c in st.conv_state] if form != "snapshot" else []
 
     def step():
         for c, c0 in zip(st.conv_state, saved):
@@ -746,6 +798,13 @@ def main():
             "us_proj_graph": round(attn_res["us_proj_graph"], 2), "us_oproj_graph": round(attn_res["us_oproj_graph"], 2),
             "bytes": attn_res["bytes"], "achieved_gbs": round(attn_res["gbs"], 1),
             "frac_hbm": round(attn_res["gbs"] / HBM_PEAK_GBS, 4),
+            # the node's form: activations quantized by their producers (same output bits)
+            "us_proj_prequant_graph": round(attn_res["us_proj_prequant_graph"], 2),
+            "us_oproj_prequant_graph": round(attn_res["us_oproj_prequant_graph"], 2),
+            "frac_hbm_prequant": round(attn_res["gbs_prequant"] / HBM_PEAK_GBS, 4),
+            "prequant_same_bits": attn_res["prequant_same_bits"],
+            "us_add_norm": round(attn_res["us_add_norm"], 2),
+            "us_add_norm_with_codes": round(attn_res["us_add_norm_with_codes"], 2),
             "workload": "128 tokens, e4m3 128x128-block qkv [9216,2048] + o_proj [2048,4096] (eager back-to-back "
                         "launches; *_graph: 10 calls captured in one graph, replayed, per call)"}
     if dec_res:
@@ -760,6 +819,7 @@ def main():
         line["hybrid_node"] = {
             "us_per_step": round(hyb_res["us_per_step"], 1), "us_eager": round(hyb_res["us_eager"], 1),
             "us_per_step_snapshot": round(hyb_res["us_per_step_snapshot"], 1),
+            "us_per_step_own_quant": round(hyb_res["us_per_step_own_quant"], 1),
             "tokens_per_s": round(hyb_res["tokens_per_s"], 1), "rows": hyb_res["rows"],
             "workload": "config 5: 3 GDN + 1 gated attention layer, each + fp8 MoE (512 experts, top-10, Zipf "
                         "router), add-norms, final norm, int8 lm_head [151936, 2048] + argmax; 64 seqs x 4 verify "

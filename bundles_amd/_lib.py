@@ -27,7 +27,8 @@ class MoeArgs(C.Structure):
                 ("w13", P), ("s13", P), ("w2", P), ("s2", P), ("sw13", P), ("ss13", P), ("sw2", P), ("ss2", P),
                 ("gate_w", P), ("out", P), ("workspace", P), ("workspace_bytes", SZ),
                 ("dbg_acc13", P), ("dbg_acc2", P), ("dbg_h", P),
-                ("resid", P), ("norm_w", P), ("norm_eps", C.c_float), ("norm_out", P)]
+                ("resid", P), ("norm_w", P), ("norm_eps", C.c_float), ("norm_out", P),
+                ("norm_q8", P), ("norm_q8s", P), ("norm_q8_frag", I32)]
 
 
 class MoeWsLayout(C.Structure):
@@ -57,12 +58,13 @@ class GdnRingArgs(C.Structure):
 class AttnArgs(C.Structure):
     _fields_ = [("T", I32), ("max_pos", I32), ("x", P), ("wqkv", P), ("sqkv", P), ("q_norm_w", P),
                 ("k_norm_w", P), ("eps", C.c_float), ("cos_sin", P), ("positions", P), ("q", P), ("gate", P),
-                ("k", P), ("v", P), ("k8", P), ("v8", P), ("workspace", P), ("workspace_bytes", SZ)]
+                ("k", P), ("v", P), ("k8", P), ("v8", P), ("workspace", P), ("workspace_bytes", SZ),
+                ("xq", P), ("xqs", P)]
 
 
 class OprojArgs(C.Structure):
     _fields_ = [("T", I32), ("attn", P), ("gate", P), ("wo", P), ("so", P), ("out", P), ("workspace", P),
-                ("workspace_bytes", SZ)]
+                ("workspace_bytes", SZ), ("aq", P), ("aqs", P)]
 
 
 class LmheadArgs(C.Structure):
@@ -77,7 +79,7 @@ class LinearSeg(C.Structure):
 
 class Fp8LinearArgs(C.Structure):
     _fields_ = [("T", I32), ("N", I32), ("K", I32), ("n_out", I32), ("x", P), ("w", P), ("ws", P), ("nseg", I32),
-                ("seg", LinearSeg * 4), ("workspace", P), ("workspace_bytes", SZ)]
+                ("seg", LinearSeg * 4), ("workspace", P), ("workspace_bytes", SZ), ("xq", P), ("xqs", P)]
 
 
 class Dense8LinearArgs(C.Structure):
@@ -86,14 +88,15 @@ class Dense8LinearArgs(C.Structure):
 
 
 class AddNormArgs(C.Structure):
-    _fields_ = [("T", I32), ("H", I32), ("delta", P), ("residual", P), ("norm_w", P), ("eps", C.c_float), ("out", P)]
+    _fields_ = [("T", I32), ("H", I32), ("delta", P), ("residual", P), ("norm_w", P), ("eps", C.c_float), ("out", P),
+                ("q8", P), ("q8s", P), ("q8_frag", I32)]
 
 
 class DecodeArgs(C.Structure):
     _fields_ = [("B", I32), ("NT", I32), ("HQ", I32), ("HKV", I32), ("D", I32), ("splits", I32), ("q", P),
                 ("k_cache", P), ("v_cache", P), ("num_slots", C.c_int64), ("page_table", P), ("pt_stride", I32),
                 ("seqlens", P), ("out_loc", P), ("k_new", P), ("v_new", P), ("scale", C.c_float), ("out", P),
-                ("workspace", P), ("workspace_bytes", SZ)]
+                ("workspace", P), ("workspace_bytes", SZ), ("gate", P), ("oq", P), ("oqs", P)]
 
 
 _lib = None
@@ -112,10 +115,12 @@ SYMBOLS = [
     ("q36_moe_forward_static", I32, [C.POINTER(MoeArgs), P]),
     ("q36_gdn_verify", I32, [C.POINTER(GdnArgs), P]),
     ("q36_gdn_verify_ring", I32, [C.POINTER(GdnRingArgs), P]),
+    ("q36_attn_act_frag", I32, [I32]),
     ("q36_attn_workspace_bytes", SZ, [I32]),
     ("q36_oproj_workspace_bytes", SZ, [I32]),
     ("q36_attn_proj", I32, [C.POINTER(AttnArgs), P]),
     ("q36_attn_oproj", I32, [C.POINTER(OprojArgs), P]),
+    ("q36_fp8_linear_act_frag", I32, [I32, I32]),
     ("q36_fp8_linear_workspace_bytes", SZ, [I32, I32]),
     ("q36_fp8_linear", I32, [C.POINTER(Fp8LinearArgs), P]),
     ("q36_add_rmsnorm", I32, [C.POINTER(AddNormArgs), P]),

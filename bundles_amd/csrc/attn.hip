@@ -41,10 +41,6 @@ __device__ __forceinline__ v4f mfma_e4m3(v8i a, v8i b) {
 // also covers the tokens up to the next multiple of 16, whose codes and scales are zero.
 // gate != nullptr: the value quantized is bf16(x * sigmoid(gate)) (the o_proj input).
 // ------------------------------------------------------------------------------------------
-__device__ __forceinline__ size_t frag_offset(int t, int k, int K) {
-  const int kb = k >> 7, j = k & 127;
-  return ((size_t)(t >> 4) * (K >> 7) + kb) * 2048 + ((j & 31) >> 4) * 1024 + 16 * ((t & 15) + 16 * (j >> 5)) + (j & 15);
-}
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* x, const uint16_t* gate, int T, int K, bool frag,
                                                         uint8_t* q, float* s) {
   const int t = blockIdx.x, tid = threadIdx.x;
@@ -77,10 +73,7 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* x, const
 #pragma unroll
     for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));  // 16 threads = one 128-group
     const float inv = m > 0.f ? 448.f / m : 0.f;
-    uint32_t wd[2] = {0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) wd[i >> 2] |= f2e4m3x2_hw(f[i] * inv, f[i + 1] * inv) << (8 * (i & 3));
-    *reinterpret_cast<uint2*>(q + (frag ? frag_offset(t, 8 * c, K) : (size_t)t * K + 8 * c)) = make_uint2(wd[0], wd[1]);
+    *reinterpret_cast<uint2*>(q + (frag ? frag_offset(t, 8 * c, K) : (size_t)t * K + 8 * c)) = e4m3_run8(f, inv);
     if ((c & 15) == 0) s[(size_t)t * (K >> 7) + c / 16] = m / 448.f;
   }
 }
@@ -784,15 +777,19 @@ __global__ __launch_bounds__(256) void pack_frag_kernel(const uint8_t* q, int64_
 using namespace q36;
 
 extern "C" size_t q36_attn_workspace_bytes(int32_t T) { return attn_ws(T).total; }
+extern "C" int q36_attn_act_frag(int32_t T) { return T >= kKsMinT ? 1 : 0; }
 extern "C" size_t q36_oproj_workspace_bytes(int32_t T) { return oproj_ws(T).total; }
 
 extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
   Q36_REQUIRE(a != nullptr, "q36_attn_proj: null args");
   Q36_REQUIRE(a->T >= 1 && a->T <= 65535, "q36_attn_proj: T=%d out of range", a->T);
   Q36_REQUIRE(a->max_pos >= 1, "q36_attn_proj: max_pos=%d", a->max_pos);
-  Q36_REQUIRE(a->x && a->wqkv && a->sqkv && a->q_norm_w && a->k_norm_w && a->cos_sin && a->positions && a->q &&
-                  a->gate && a->k && a->v && a->k8 && a->v8 && a->workspace,
+  Q36_REQUIRE((a->x || a->xq) && a->wqkv && a->sqkv && a->q_norm_w && a->k_norm_w && a->cos_sin && a->positions &&
+                  a->q && a->gate && a->k && a->v && a->k8 && a->v8 && a->workspace,
               "q36_attn_proj: a required pointer is null");
+  Q36_REQUIRE((a->xq == nullptr) == (a->xqs == nullptr), "q36_attn_proj: xq and xqs go together");
+  Q36_REQUIRE(aligned16(a->xq) && (reinterpret_cast<uintptr_t>(a->xqs) & 3u) == 0,
+              "q36_attn_proj: xq must be 16-byte and xqs 4-byte aligned");
   Q36_REQUIRE(aligned16(a->x) && aligned16(a->wqkv) && aligned16(a->q_norm_w) && aligned16(a->k_norm_w) &&
                   aligned16(a->cos_sin) && aligned16(a->q) && aligned16(a->gate) && aligned16(a->k) &&
                   aligned16(a->v) && (reinterpret_cast<uintptr_t>(a->k8) & 7u) == 0 &&
@@ -805,12 +802,18 @@ extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
               a->workspace_bytes, L.total);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(a->workspace);
-  uint8_t* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
-  float* xs = reinterpret_cast<float*>(ws + L.xs);
+  const uint8_t* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
+  const float* xs = reinterpret_cast<float*>(ws + L.xs);
   uint16_t* qkv = reinterpret_cast<uint16_t*>(ws + L.qkv);
   const bool ks = a->T >= kKsMinT;
   const int Tq = ks ? (a->T + 15) / 16 * 16 : a->T;
-  act_quant_kernel<<<Tq, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr, a->T, 2048, ks, xq, xs);
+  if (a->xq) {  // quantized by the rows' producer, in this entry's layout (q36_attn_act_frag)
+    xq = static_cast<const uint8_t*>(a->xq);
+    xs = a->xqs;
+  } else {
+    act_quant_kernel<<<Tq, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr, a->T, 2048, ks,
+                                         reinterpret_cast<uint8_t*>(ws + L.xq), reinterpret_cast<float*>(ws + L.xs));
+  }
   const GemmDev g = gemm_dev(xq, xs, a->T, 2048, static_cast<const uint8_t*>(a->wqkv), a->sqkv, 9216, qkv);
   // 144-row x 32-token workgroups, 3 row groups x 4 K quarters (12 waves): 256 workgroups at 128
   // tokens, 17.9 us per graph-timed call against 19.2 us for the streaming GEMM (128 x 32 tiles, 288
@@ -833,8 +836,11 @@ extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
 extern "C" int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream) {
   Q36_REQUIRE(a != nullptr, "q36_attn_oproj: null args");
   Q36_REQUIRE(a->T >= 1 && a->T <= 65535, "q36_attn_oproj: T=%d out of range", a->T);
-  Q36_REQUIRE(a->attn && a->gate && a->wo && a->so && a->out && a->workspace,
+  Q36_REQUIRE(((a->attn && a->gate) || a->aq) && a->wo && a->so && a->out && a->workspace,
               "q36_attn_oproj: a required pointer is null");
+  Q36_REQUIRE((a->aq == nullptr) == (a->aqs == nullptr), "q36_attn_oproj: aq and aqs go together");
+  Q36_REQUIRE(aligned16(a->aq) && (reinterpret_cast<uintptr_t>(a->aqs) & 3u) == 0,
+              "q36_attn_oproj: aq must be 16-byte and aqs 4-byte aligned");
   Q36_REQUIRE(aligned16(a->attn) && aligned16(a->gate) && aligned16(a->wo) &&
                   (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0,
               "q36_attn_oproj: attn, gate, wo must be 16-byte and workspace 256-byte aligned");
@@ -843,10 +849,16 @@ extern "C" int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream) {
               a->workspace_bytes, L.total);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(a->workspace);
-  uint8_t* aq = reinterpret_cast<uint8_t*>(ws + L.aq);
-  float* as = reinterpret_cast<float*>(ws + L.as);
-  act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->attn), static_cast<const uint16_t*>(a->gate),
-                                         a->T, 4096, false, aq, as);
+  const uint8_t* aq = reinterpret_cast<uint8_t*>(ws + L.aq);
+  const float* as = reinterpret_cast<float*>(ws + L.as);
+  if (a->aq) {  // quantized by the attention's epilogue (q36_attn_decode's oq / oqs)
+    aq = static_cast<const uint8_t*>(a->aq);
+    as = a->aqs;
+  } else {
+    act_quant_kernel<<<a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->attn),
+                                           static_cast<const uint16_t*>(a->gate), a->T, 4096, false,
+                                           reinterpret_cast<uint8_t*>(ws + L.aq), reinterpret_cast<float*>(ws + L.as));
+  }
   const GemmDev g =
       gemm_dev(aq, as, a->T, 4096, static_cast<const uint8_t*>(a->wo), a->so, 2048, static_cast<uint16_t*>(a->out));
   // 64-row blocks (one 16-row tile per wave), one-tile token groups, 4 stages in flight: 256
@@ -862,6 +874,7 @@ extern "C" int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream) {
 }
 
 extern "C" size_t q36_fp8_linear_workspace_bytes(int32_t T, int32_t K) { return lin_ws(T, K).total; }
+extern "C" int q36_fp8_linear_act_frag(int32_t T, int32_t K) { return T >= kTileMinT && K == 2048 ? 1 : 0; }
 
 extern "C" int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream) {
   Q36_REQUIRE(a != nullptr, "q36_fp8_linear: null args");
@@ -871,7 +884,10 @@ extern "C" int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream)
               a->N);
   Q36_REQUIRE(a->n_out >= 4 && a->n_out <= a->N && a->n_out % 4 == 0, "q36_fp8_linear: n_out=%d (N=%d)", a->n_out,
               a->N);
-  Q36_REQUIRE(a->x && a->w && a->ws && a->workspace, "q36_fp8_linear: a required pointer is null");
+  Q36_REQUIRE((a->x || a->xq) && a->w && a->ws && a->workspace, "q36_fp8_linear: a required pointer is null");
+  Q36_REQUIRE((a->xq == nullptr) == (a->xqs == nullptr), "q36_fp8_linear: xq and xqs go together");
+  Q36_REQUIRE(aligned16(a->xq) && (reinterpret_cast<uintptr_t>(a->xqs) & 3u) == 0,
+              "q36_fp8_linear: xq must be 16-byte and xqs 4-byte aligned");
   Q36_REQUIRE(aligned16(a->x) && aligned16(a->w) && (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0,
               "q36_fp8_linear: x, w must be 16-byte and workspace 256-byte aligned");
   Q36_REQUIRE(a->nseg >= 1 && a->nseg <= 4 && a->seg[0].col0 == 0, "q36_fp8_linear: nseg=%d, first segment at %d",
@@ -890,11 +906,17 @@ extern "C" int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream)
               a->workspace_bytes, L.total);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(a->workspace);
-  uint8_t* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
-  float* xs = reinterpret_cast<float*>(ws + L.xs);
+  const uint8_t* xq = reinterpret_cast<uint8_t*>(ws + L.xq);
+  const float* xs = reinterpret_cast<float*>(ws + L.xs);
   const bool tiled = a->T >= kTileMinT && a->K == 2048;
-  act_quant_kernel<<<tiled ? (a->T + 15) / 16 * 16 : a->T, 256, 0, st>>>(static_cast<const uint16_t*>(a->x), nullptr,
-                                                                         a->T, a->K, tiled, xq, xs);
+  if (a->xq) {  // quantized by the rows' producer, in this entry's layout (q36_fp8_linear_act_frag)
+    xq = static_cast<const uint8_t*>(a->xq);
+    xs = a->xqs;
+  } else {
+    act_quant_kernel<<<tiled ? (a->T + 15) / 16 * 16 : a->T, 256, 0, st>>>(
+        static_cast<const uint16_t*>(a->x), nullptr, a->T, a->K, tiled, reinterpret_cast<uint8_t*>(ws + L.xq),
+        reinterpret_cast<float*>(ws + L.xs));
+  }
   GemmDev g = gemm_dev(xq, xs, a->T, a->K, static_cast<const uint8_t*>(a->w), a->ws, a->N, nullptr);
   g.nseg = a->nseg;
   g.nout = a->n_out;

@@ -67,7 +67,26 @@ struct DecodeDev {
   float* ws_o;              // [B*2*splits][32][256] unnormalised partial outputs
   float* ws_ml;             // [B*2*splits][2][32]: running max (base 2) and weight sum per row
   uint16_t* out;            // bf16 [B*NT, 16, 256]
+  const uint16_t* gate;     // bf16 [B*NT, 16 * 256] or null: with oq, the o_proj's quantized input
+  uint8_t* oq;              // e4m3 [B*NT, 16 * 256] of bf16(out * sigmoid(gate)) per 128-group
+  float* oqs;               // [B*NT, 32] group scales
 };
+
+// The output's 4 values at dims 4c .. 4c + 3 of row (token tok, head) after the bf16 store: the o_proj
+// input bf16(o * sigmoid(gate)) in e4m3 per 128-channel group (32 neighbouring lanes of one wave hold
+// a group), the same arithmetic as the o_proj's own quantization of the bf16 output.
+__device__ __forceinline__ void gated_e4m3(const DecodeDev& d, int tok, int head, int c, uint32_t o01, uint32_t o23) {
+  const size_t at = (size_t)tok * (kQH * kDD) + head * kDD + 4 * c;
+  const uint2 gv = *reinterpret_cast<const uint2*>(d.gate + at);
+  float f[4] = {rbf(bf_lo(o01) * sigmoid_q(bf_lo(gv.x))), rbf(bf_hi(o01) * sigmoid_q(bf_hi(gv.x))),
+                rbf(bf_lo(o23) * sigmoid_q(bf_lo(gv.y))), rbf(bf_hi(o23) * sigmoid_q(bf_hi(gv.y)))};
+  float m = fmaxf(fmaxf(fabsf(f[0]), fabsf(f[1])), fmaxf(fabsf(f[2]), fabsf(f[3])));
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  const float inv = m > 0.f ? 448.f / m : 0.f;
+  *reinterpret_cast<uint32_t*>(d.oq + at) = f2e4m3x2_hw(f[0] * inv, f[1] * inv) | (f2e4m3x2_hw(f[2] * inv, f[3] * inv) << 16);
+  if ((c & 31) == 0) d.oqs[(size_t)tok * (kQH * kDD / 128) + head * 2 + c / 32] = m / 448.f;
+}
 
 __device__ __forceinline__ v4f mfma_e4m3(v8i a, v8i b, v4f c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
@@ -384,7 +403,10 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
       } else {
         const float L = rowL[row], il = L > 0.f ? 1.f / L : 0.f;
         uint16_t* dst = d.out + (((size_t)b * NT + (row >> 3)) * kQH + h * kGQ + (row & 7)) * kDD + 4 * c;
-        *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(a[0] * il, a[1] * il), pack_bf2(a[2] * il, a[3] * il));
+        const uint32_t o01 = pack_bf2(a[0] * il, a[1] * il), o23 = pack_bf2(a[2] * il, a[3] * il);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(o01, o23);
+        // a wave holds one row (rows * 64 threads, whole waves): its two 128-groups are its lane halves
+        if (d.oq) gated_e4m3(d, b * NT + (row >> 3), h * kGQ + (row & 7), c, o01, o23);
       }
     }
   }
@@ -409,8 +431,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeDev d) {
     a += w * *reinterpret_cast<const v4f*>(d.ws_o + ((size_t)(g0 + s) * kDRows + gr) * kDD + 4 * c);
   }
   const float il = L > 0.f ? 1.f / L : 0.f;
-  *reinterpret_cast<uint2*>(d.out + (size_t)qr * kDD + 4 * c) =
-      make_uint2(pack_bf2(a[0] * il, a[1] * il), pack_bf2(a[2] * il, a[3] * il));
+  const uint32_t o01 = pack_bf2(a[0] * il, a[1] * il), o23 = pack_bf2(a[2] * il, a[3] * il);
+  *reinterpret_cast<uint2*>(d.out + (size_t)qr * kDD + 4 * c) = make_uint2(o01, o23);
+  // 64 consecutive threads are one row (the row count is whole waves): lanes 0-31 / 32-63 its groups
+  if (d.oq) gated_e4m3(d, qr / kQH, head, c, o01, o23);
 }
 
 int decode_splits(int B, int splits) {
@@ -448,6 +472,11 @@ extern "C" int q36_attn_decode(const q36_decode_args* a, q36_stream_t stream) {
               "q36_attn_decode: num_slots=%lld out of range", (long long)a->num_slots);
   Q36_REQUIRE(a->pt_stride >= 1, "q36_attn_decode: pt_stride=%d", a->pt_stride);
   Q36_REQUIRE(!a->out_loc || (a->k_new && a->v_new), "q36_attn_decode: out_loc needs k_new and v_new");
+  Q36_REQUIRE((a->gate == nullptr) == (a->oq == nullptr) && (a->oq == nullptr) == (a->oqs == nullptr),
+              "q36_attn_decode: gate, oq and oqs go together");
+  Q36_REQUIRE(!a->oq || ((reinterpret_cast<uintptr_t>(a->gate) & 7u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(a->oq) & 3u) == 0 && (reinterpret_cast<uintptr_t>(a->oqs) & 3u) == 0),
+              "q36_attn_decode: gate must be 8-byte, oq and oqs 4-byte aligned");
   const int S = decode_splits(a->B, a->splits);
   const size_t need = decode_ws_bytes(a->B, S);
   Q36_REQUIRE(a->workspace_bytes >= need, "q36_attn_decode: workspace of %zu bytes < %zu required", a->workspace_bytes,
@@ -465,7 +494,8 @@ extern "C" int q36_attn_decode(const q36_decode_args* a, q36_stream_t stream) {
               static_cast<const uint8_t*>(a->v_cache), (int64_t)a->num_slots * kKVH * kDD, a->page_table, a->seqlens,
               a->scale * 1.44269504088896340736f, reinterpret_cast<float*>(ws),
               reinterpret_cast<float*>(ws + align_up(sizeof(float) * (size_t)a->B * kKVH * S * kDRows * kDD, 256)),
-              static_cast<uint16_t*>(a->out)};
+              static_cast<uint16_t*>(a->out), static_cast<const uint16_t*>(a->gate), static_cast<uint8_t*>(a->oq),
+              a->oqs};
   if (a->NT <= 2)
     decode_split_kernel<1><<<dim3(S, kKVH, a->B), 256, 0, st>>>(d);
   else

@@ -85,6 +85,9 @@ struct MoeDev {
   const uint16_t* norm_w;
   float norm_eps;
   uint16_t* norm_out;
+  uint8_t* norm_q8;       // norm_out's e4m3 codes (fragment order when norm_q8_frag), or null
+  float* norm_q8s;
+  int norm_q8_frag;
 };
 
 __device__ __forceinline__ v4i ldg16_nt(const uint8_t* p) {
@@ -1126,6 +1129,12 @@ constexpr int kCombH = 2048;
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
   const int t = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (t >= d.M) {
+    // the fused add-norm's e4m3 rows in fragment order: the padding tokens up to a multiple of 16
+    *reinterpret_cast<uint2*>(d.norm_q8 + frag_offset(t, 8 * tid, kCombH)) = make_uint2(0u, 0u);
+    if ((tid & 15) == 0) d.norm_q8s[(size_t)t * (kCombH / 128) + tid / 16] = 0.f;
+    return;
+  }
   const bool valid = d.pos == nullptr || d.pos[t] != 0;
   const int S = d.M * d.k;
   __shared__ float rstd_s;
@@ -1205,6 +1214,21 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
     ov[q] = (int)pack_bf2((z[2 * q] * rstd) * (1.f + bf_lo((uint32_t)wv[q])),
                           (z[2 * q + 1] * rstd) * (1.f + bf_hi((uint32_t)wv[q])));
   *reinterpret_cast<v4i*>(d.norm_out + at) = ov;
+  if (d.norm_q8 == nullptr) return;
+  // the normed row's e4m3 codes for the next projection (a 128-group is 16 neighbouring threads)
+  float f[8];
+  float m = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f[2 * q] = bf_lo((uint32_t)ov[q]);
+    f[2 * q + 1] = bf_hi((uint32_t)ov[q]);
+    m = fmaxf(m, fmaxf(fabsf(f[2 * q]), fabsf(f[2 * q + 1])));
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  const float inv = m > 0.f ? 448.f / m : 0.f;
+  *reinterpret_cast<uint2*>(d.norm_q8 + (d.norm_q8_frag ? frag_offset(t, 8 * c, kCombH) : at)) = e4m3_run8(f, inv);
+  if ((c & 15) == 0) d.norm_q8s[(size_t)t * (kCombH / 128) + c / 16] = m / 448.f;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1259,6 +1283,11 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
   Q36_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0, "q36_moe: workspace must be 256-byte aligned");
   Q36_REQUIRE(a->norm_out == nullptr || (a->resid && a->norm_w),
               "q36_moe: the fused add-norm (norm_out) needs resid and norm_w");
+  Q36_REQUIRE((a->norm_q8 == nullptr) == (a->norm_q8s == nullptr) && (a->norm_q8 == nullptr || a->norm_out),
+              "q36_moe: norm_q8 and norm_q8s go together, with norm_out");
+  Q36_REQUIRE(!a->norm_q8 || ((reinterpret_cast<uintptr_t>(a->norm_q8) & 7u) == 0 &&
+                              (reinterpret_cast<uintptr_t>(a->norm_q8s) & 3u) == 0),
+              "q36_moe: norm_q8 must be 8-byte and norm_q8s 4-byte aligned");
   q36_moe_ws_layout L;
   layout(a->M, a->E, a->H, a->I, a->topk, a->dtype, &L);
   Q36_REQUIRE(a->workspace_bytes >= L.total, "q36_moe: workspace of %zu bytes is smaller than the %zu required",
@@ -1281,7 +1310,8 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
               reinterpret_cast<float*>(ws + L.xs), reinterpret_cast<uint16_t*>(ws + L.h),
               reinterpret_cast<uint16_t*>(ws + L.y), a->dbg_acc13, a->dbg_acc2,
               static_cast<uint16_t*>(a->dbg_h), static_cast<uint16_t*>(a->resid),
-              static_cast<const uint16_t*>(a->norm_w), a->norm_eps, static_cast<uint16_t*>(a->norm_out)};
+              static_cast<const uint16_t*>(a->norm_w), a->norm_eps, static_cast<uint16_t*>(a->norm_out),
+              static_cast<uint8_t*>(a->norm_q8), a->norm_q8s, a->norm_q8_frag != 0};
   return Q36_OK;
 }
 
@@ -1331,7 +1361,9 @@ int launch_down(const MoeDev& d, int dtype, hipStream_t st) {
   return dtype == Q36_MOE_FP8 ? launch_down_t<Q36_MOE_FP8>(d, st) : launch_down_t<Q36_MOE_INT8>(d, st);
 }
 int launch_combine(const MoeDev& d, hipStream_t st) {
-  moe_combine_kernel<<<d.M, 256, 0, st>>>(d);
+  // fragment-order e4m3 rows pad the tokens to a multiple of 16 (zero rows)
+  const int grid = d.norm_q8 && d.norm_q8_frag ? (d.M + 15) / 16 * 16 : d.M;
+  moe_combine_kernel<<<grid, 256, 0, st>>>(d);
   return check_launch("q36_moe_combine");
 }
 

@@ -7,6 +7,8 @@
 // same bits, and rsqrt is the correctly rounded 1 / sqrt.
 //
 // Kernel: one wave per row, four rows per workgroup; a row is 2048 bf16 = 4 chunks of 8 per lane.
+// Optionally the normed row also leaves as e4m3 codes per 128-channel group (the next projection's
+// input, so that projection skips its own quantization launch): a group is 16 neighbouring lanes.
 #include "q36_device.h"
 #include "q36_host.h"
 
@@ -22,12 +24,26 @@ struct NormDev {
   const uint16_t* w;
   float eps;
   uint16_t* out;
+  uint8_t* q8;   // e4m3 codes of out (fragment order when frag), or null
+  float* q8s;    // [tokens, 16] group scales
+  int frag;
 };
 
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormDev d) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + wave;
-  if (r >= d.T) return;
+  if (r >= d.T) {
+    // fragment order pads the tokens to a multiple of 16: zero codes and scales
+    if (d.q8 && d.frag && r < (d.T + 15) / 16 * 16) {
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j) {
+        const int c = lane + 64 * j;
+        *reinterpret_cast<uint2*>(d.q8 + frag_offset(r, 8 * c, kNH)) = make_uint2(0u, 0u);
+        if ((c & 15) == 0) d.q8s[(size_t)r * (kNH / 128) + c / 16] = 0.f;
+      }
+    }
+    return;
+  }
   float z[kNJ][8];
 #pragma unroll
   for (int j = 0; j < kNJ; ++j) {
@@ -67,6 +83,24 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormDev d) {
       ov[q] = (int)pack_bf2((z[j][2 * q] * rstd) * (1.f + bf_lo((uint32_t)wv[q])),
                             (z[j][2 * q + 1] * rstd) * (1.f + bf_hi((uint32_t)wv[q])));
     *reinterpret_cast<v4i*>(d.out + (size_t)r * kNH + 8 * (lane + 64 * j)) = ov;
+    if (d.q8) {
+      // the bf16 outputs' e4m3 codes: the same arithmetic as the projections' own quantization
+      const int c = lane + 64 * j;
+      float f[8];
+      float m = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f[2 * q] = bf_lo((uint32_t)ov[q]);
+        f[2 * q + 1] = bf_hi((uint32_t)ov[q]);
+        m = fmaxf(m, fmaxf(fabsf(f[2 * q]), fabsf(f[2 * q + 1])));
+      }
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+      const float inv = m > 0.f ? 448.f / m : 0.f;
+      *reinterpret_cast<uint2*>(d.q8 + (d.frag ? frag_offset(r, 8 * c, kNH) : (size_t)r * kNH + 8 * c)) =
+          e4m3_run8(f, inv);
+      if ((c & 15) == 0) d.q8s[(size_t)r * (kNH / 128) + c / 16] = m / 448.f;
+    }
   }
 }
 
@@ -82,8 +116,13 @@ extern "C" int q36_add_rmsnorm(const q36_add_norm_args* a, q36_stream_t stream) 
   Q36_REQUIRE(a->residual && a->norm_w && a->out, "q36_add_rmsnorm: a required pointer is null");
   Q36_REQUIRE(aligned16(a->residual) && aligned16(a->norm_w) && aligned16(a->out) && (!a->delta || aligned16(a->delta)),
               "q36_add_rmsnorm: pointers must be 16-byte aligned");
+  Q36_REQUIRE((a->q8 == nullptr) == (a->q8s == nullptr), "q36_add_rmsnorm: q8 and q8s go together");
+  Q36_REQUIRE(!a->q8 || ((reinterpret_cast<uintptr_t>(a->q8) & 7u) == 0 && (reinterpret_cast<uintptr_t>(a->q8s) & 3u) == 0),
+              "q36_add_rmsnorm: q8 must be 8-byte and q8s 4-byte aligned");
   NormDev d{a->T, static_cast<const uint16_t*>(a->delta), static_cast<uint16_t*>(a->residual),
-            static_cast<const uint16_t*>(a->norm_w), a->eps, static_cast<uint16_t*>(a->out)};
-  add_rmsnorm_kernel<<<(a->T + 3) / 4, 256, 0, static_cast<hipStream_t>(stream)>>>(d);
+            static_cast<const uint16_t*>(a->norm_w), a->eps, static_cast<uint16_t*>(a->out),
+            static_cast<uint8_t*>(a->q8), a->q8s, a->q8_frag != 0};
+  const int rows = a->q8 && a->q8_frag ? (a->T + 15) / 16 * 16 : a->T;
+  add_rmsnorm_kernel<<<(rows + 3) / 4, 256, 0, static_cast<hipStream_t>(stream)>>>(d);
   return check_launch("q36_add_rmsnorm");
 }

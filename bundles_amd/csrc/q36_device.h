@@ -152,6 +152,25 @@ __device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
   return v;
 }
 
+// Byte offset of element (token t, channel k) of e4m3 activations [T, K] in MFMA fragment order
+// (the operand layout the projection GEMMs read): token tile t / 16 and 128-block kb at
+// ((t / 16) * K / 128 + kb) * 2048, byte j of the block at (j % 32) / 16 * 1024 +
+// 16 * (t % 16 + 16 * (j / 32)) + j % 16 -- the 32 bytes lane t % 16 + 16 (j / 32) feeds the MFMA,
+// as two 16-byte halves 1 KB apart.  8-byte runs k .. k + 7 (k % 8 == 0) stay contiguous.
+__host__ __device__ __forceinline__ size_t frag_offset(int t, int k, int K) {
+  const int kb = k >> 7, j = k & 127;
+  return ((size_t)(t >> 4) * (K >> 7) + kb) * 2048 + ((j & 31) >> 4) * 1024 + 16 * ((t & 15) + 16 * (j >> 5)) + (j & 15);
+}
+
+// e4m3 codes of 8 values (one 8-byte run) of a 128-channel group quantized with inverse scale inv
+// (448 / group amax, 0 for an all-zero group), round to nearest even with saturation.
+__device__ __forceinline__ uint2 e4m3_run8(const float* f, float inv) {
+  uint32_t wd[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) wd[i >> 2] |= f2e4m3x2_hw(f[i] * inv, f[i + 1] * inv) << (8 * (i & 3));
+  return make_uint2(wd[0], wd[1]);
+}
+
 // Round half away from zero and clamp to +-127 (the int8 activation / weight rule).
 __device__ __forceinline__ int round_i8(float v) {
   float r = v >= 0.f ? __builtin_floorf(v + 0.5f) : -__builtin_floorf(0.5f - v);

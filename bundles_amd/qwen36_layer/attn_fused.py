@@ -54,6 +54,33 @@ def rope_cos_sin(max_pos: int, theta: float = 1e7, rot_dim: int = 64, device="cp
     return torch.cat([ang.cos(), ang.sin()], dim=1).to(torch.float32).to(device)
 
 
+@dataclass
+class QuantRows:
+    """e4m3 rows a producer kernel quantized for the next projection: codes per token x 128 channels
+    (fragment order when frag, tokens padded to a multiple of 16) and fp32 scales [tokens, K/128]."""
+    codes: torch.Tensor   # uint8 [tokens, K]
+    scales: torch.Tensor  # fp32 [tokens, K / 128]
+    T: int
+    frag: bool
+
+    @staticmethod
+    def alloc(T: int, K: int, frag: bool, device) -> "QuantRows":
+        n = (T + 15) // 16 * 16 if frag else T
+        return QuantRows(torch.empty((n, K), dtype=torch.uint8, device=device),
+                         torch.empty((n, K // 128), dtype=torch.float32, device=device), T, frag)
+
+
+def proj_rows(T: int, device) -> QuantRows:
+    """Buffers for q36_attn_proj's pre-quantized input of T tokens, in the layout it reads
+    (q36_attn_act_frag); a producer (glue.add_rmsnorm, moe_row_batch's fused add-norm) fills them."""
+    return QuantRows.alloc(T, HIDDEN, bool(_lib.lib().q36_attn_act_frag(T)), device)
+
+
+def oproj_rows(T: int, device) -> QuantRows:
+    """Buffers for q36_attn_oproj's pre-quantized input (row-major), filled by attn_decode(gate=...)."""
+    return QuantRows.alloc(T, N_Q_HEADS * HEAD_DIM, False, device)
+
+
 class Workspace:
     def __init__(self, T_max: int, device):
         L = _lib.lib()
@@ -62,12 +89,17 @@ class Workspace:
         self.oproj = torch.empty(L.q36_oproj_workspace_bytes(T_max), dtype=torch.uint8, device=device)
 
 
-def attn_proj(x, w: AttnWeights, q_norm_w, k_norm_w, eps, cos_sin, positions, ws: Workspace, out=None, stream=None):
-    """Returns dict(q, gate, k, v, k8, v8) for tokens x bf16 [T, 2048]."""
-    T = x.shape[0]
+def attn_proj(x, w: AttnWeights, q_norm_w, k_norm_w, eps, cos_sin, positions, ws: Workspace, out=None, stream=None,
+              xq: QuantRows | None = None):
+    """Returns dict(q, gate, k, v, k8, v8) for tokens x bf16 [T, 2048].  xq: the rows already quantized
+    by their producer (proj_rows); x is then not read (may be None) and the projection skips its own
+    quantization launch, with the same output bits."""
+    T = x.shape[0] if x is not None else xq.T
+    if xq is not None and (xq.T != T or xq.frag != bool(_lib.lib().q36_attn_act_frag(T))):
+        raise ValueError("attn_proj: xq was not made for this token count (proj_rows)")
     if T > ws.T_max:
         raise ValueError(f"attn_proj: {T} tokens exceed the workspace's {ws.T_max}")
-    dev = x.device
+    dev = x.device if x is not None else xq.codes.device
     o = out or dict(q=torch.empty((T, N_Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=dev),
                     gate=torch.empty((T, N_Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=dev),
                     k=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=dev),
@@ -76,16 +108,23 @@ def attn_proj(x, w: AttnWeights, q_norm_w, k_norm_w, eps, cos_sin, positions, ws
                     v8=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.uint8, device=dev))
     a = AttnArgs(T, cos_sin.shape[0], ptr(x), ptr(w.wqkv_p), ptr(w.sqkv), ptr(q_norm_w), ptr(k_norm_w), eps,
                  ptr(cos_sin), ptr(positions), ptr(o["q"]), ptr(o["gate"]), ptr(o["k"]), ptr(o["v"]), ptr(o["k8"]),
-                 ptr(o["v8"]), ptr(ws.proj), ws.proj.numel())
+                 ptr(o["v8"]), ptr(ws.proj), ws.proj.numel(), ptr(None if xq is None else xq.codes),
+                 ptr(None if xq is None else xq.scales))
     check(_lib.lib().q36_attn_proj(C.byref(a), _lib.stream_handle(stream)), "q36_attn_proj")
     return o
 
 
-def attn_oproj(attn, gate, w: AttnWeights, ws: Workspace, out=None, stream=None):
-    """out bf16 [T, 2048] = o_proj(bf16(attn * sigmoid(gate))), attn / gate bf16 [T, 4096]."""
-    T = attn.shape[0]
-    out = torch.empty((T, HIDDEN), dtype=torch.bfloat16, device=attn.device) if out is None else out
-    a = OprojArgs(T, ptr(attn), ptr(gate), ptr(w.wo_p), ptr(w.so), ptr(out), ptr(ws.oproj), ws.oproj.numel())
+def attn_oproj(attn, gate, w: AttnWeights, ws: Workspace, out=None, stream=None, aq: QuantRows | None = None):
+    """out bf16 [T, 2048] = o_proj(bf16(attn * sigmoid(gate))), attn / gate bf16 [T, 4096].  aq: that
+    input already quantized by the attention (attn_decode(gate=..., oq=...)); attn, gate are then
+    not read (may be None)."""
+    T = attn.shape[0] if attn is not None else aq.T
+    if aq is not None and (aq.T != T or aq.frag):
+        raise ValueError("attn_oproj: aq must be row-major rows of this token count (oproj_rows)")
+    dev = attn.device if attn is not None else aq.codes.device
+    out = torch.empty((T, HIDDEN), dtype=torch.bfloat16, device=dev) if out is None else out
+    a = OprojArgs(T, ptr(attn), ptr(gate), ptr(w.wo_p), ptr(w.so), ptr(out), ptr(ws.oproj), ws.oproj.numel(),
+                  ptr(None if aq is None else aq.codes), ptr(None if aq is None else aq.scales))
     check(_lib.lib().q36_attn_oproj(C.byref(a), _lib.stream_handle(stream)), "q36_attn_oproj")
     return out
 
@@ -103,13 +142,15 @@ class DecodeWorkspace:
 
 
 def attn_decode(q, k_cache, v_cache, page_table, seqlens, NT: int, scale: float, ws: DecodeWorkspace,
-                out_loc=None, k_new=None, v_new=None, out=None, stream=None):
+                out_loc=None, k_new=None, v_new=None, out=None, stream=None, gate=None, oq: QuantRows | None = None):
     """Attention of B requests' NT new tokens over the e4m3 KV cache (one-token pages).
 
     q bf16 [B*NT, 16, 256]; k_cache / v_cache e4m3 codes (uint8) [slots, 2, 256]; page_table int32
     [B, >= max seqlens]; seqlens int32 [B] (new tokens included).  With out_loc (int64 [B*NT]) the
     new tokens' k_new / v_new rows are written into the cache first.  Returns bf16 [B*NT, 16, 256]
     = softmax(scale * e4m3(q) k^T) V per query head, causal among the new tokens, not gated.
+    gate (bf16 [B*NT, 4096], attn_proj's gate) with oq (oproj_rows): the o_proj's input
+    bf16(out * sigmoid(gate)) is also written there, quantized as attn_oproj would.
     """
     T = q.shape[0]
     if T % NT:
@@ -123,9 +164,15 @@ def attn_decode(q, k_cache, v_cache, page_table, seqlens, NT: int, scale: float,
             raise ValueError(f"attn_decode: {name} must be a contiguous {dt} tensor")
     if out_loc is not None and (out_loc.dtype != torch.int64 or k_new is None or v_new is None):
         raise ValueError("attn_decode: out_loc must be int64 and comes with k_new and v_new")
+    if (gate is None) != (oq is None):
+        raise ValueError("attn_decode: gate and oq go together")
+    if oq is not None and (oq.T != T or oq.frag or gate.dtype != torch.bfloat16 or not gate.is_contiguous()
+                           or gate.numel() != T * N_Q_HEADS * HEAD_DIM):
+        raise ValueError("attn_decode: gate must be contiguous bf16 [T, 4096] and oq row-major rows (oproj_rows)")
     out = torch.empty_like(q) if out is None else out
     a = DecodeArgs(B, NT, q.shape[1], k_cache.shape[1], q.shape[2], ws.splits, ptr(q), ptr(k_cache), ptr(v_cache),
                    k_cache.shape[0], ptr(page_table), page_table.shape[1], ptr(seqlens), ptr(out_loc), ptr(k_new),
-                   ptr(v_new), scale, ptr(out), ptr(ws.buf), ws.buf.numel())
+                   ptr(v_new), scale, ptr(out), ptr(ws.buf), ws.buf.numel(), ptr(gate),
+                   ptr(None if oq is None else oq.codes), ptr(None if oq is None else oq.scales))
     check(_lib.lib().q36_attn_decode(C.byref(a), _lib.stream_handle(stream)), "q36_attn_decode")
     return out

@@ -62,24 +62,39 @@ class LinearWorkspace:
         self.buf = torch.empty(_lib.lib().q36_fp8_linear_workspace_bytes(T_max, K), dtype=torch.uint8, device=device)
 
 
-def fp8_linear(x: torch.Tensor, w: Fp8Weight, ws: LinearWorkspace, segments=None, stream=None):
+def linear_rows(T: int, K: int, device):
+    """Buffers for fp8_linear's pre-quantized input of T tokens of width K, in the layout it reads
+    (q36_fp8_linear_act_frag); a producer (add_rmsnorm, the MoE's fused add-norm) fills them."""
+    from .attn_fused import QuantRows
+    return QuantRows.alloc(T, K, bool(_lib.lib().q36_fp8_linear_act_frag(T, K)), device)
+
+
+def fp8_linear(x: torch.Tensor, w: Fp8Weight, ws: LinearWorkspace, segments=None, stream=None, xq=None):
     """y = x . W^T (bf16), x bf16 [T, K].
 
     segments: None (returns one [T, n] tensor) or a list of (col0, out) with out a bf16 [T, width]
     view whose rows may be strided (row stride = out.stride(0)); columns col0 .. col0 + width of y
-    land in it.  The segments must tile [0, n) in order.
+    land in it.  The segments must tile [0, n) in order.  xq (linear_rows): x already quantized by its
+    producer; x is then not read (may be None), with the same output bits.
     """
-    T, K = x.shape
+    if x is None:
+        T, K = xq.T, xq.codes.shape[1]
+    else:
+        T, K = x.shape
+    if xq is not None and (xq.T != T or xq.codes.shape[1] != K or
+                           xq.frag != bool(_lib.lib().q36_fp8_linear_act_frag(T, K))):
+        raise ValueError("fp8_linear: xq was not made for this input (linear_rows)")
     if T > ws.T_max or K != ws.K:
         raise ValueError(f"fp8_linear: [{T}, {K}] does not fit the workspace ({ws.T_max}, {ws.K})")
     if segments is None:
-        out = torch.empty((T, w.n), dtype=torch.bfloat16, device=x.device)
+        out = torch.empty((T, w.n), dtype=torch.bfloat16, device=w.qp.device)
         segments, ret = [(0, out)], out
     else:
         ret = None
     segs = _segments("fp8_linear", T, w.n, segments)
     a = Fp8LinearArgs(T, w.qp.shape[0], K, w.n, ptr(x), ptr(w.qp), ptr(w.s), len(segments), segs,
-                      ptr(ws.buf), ws.buf.numel())
+                      ptr(ws.buf), ws.buf.numel(), ptr(None if xq is None else xq.codes),
+                      ptr(None if xq is None else xq.scales))
     check(_lib.lib().q36_fp8_linear(C.byref(a), _lib.stream_handle(stream)), "q36_fp8_linear")
     return ret
 
@@ -121,11 +136,16 @@ def dense8_linear(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, segments=No
     return ret
 
 
-def add_rmsnorm(delta, residual: torch.Tensor, norm_w: torch.Tensor, eps: float, out=None, stream=None):
+def add_rmsnorm(delta, residual: torch.Tensor, norm_w: torch.Tensor, eps: float, out=None, stream=None, q8=None):
     """residual += delta (bf16, in place; delta None: residual unchanged); returns the Gemma-normalised
-    rows bf16((z * rstd) * (1 + w)) of z = delta + residual in fp32."""
+    rows bf16((z * rstd) * (1 + w)) of z = delta + residual in fp32.  q8 (attn_fused.QuantRows of T
+    rows): the rows' e4m3 codes also go there, as the next projection reads them."""
     T, H = residual.shape
     out = torch.empty_like(residual) if out is None else out
-    a = AddNormArgs(T, H, ptr(delta), ptr(residual), ptr(norm_w), eps, ptr(out))
+    if q8 is not None and (q8.T != T or q8.codes.shape[1] != H):
+        raise ValueError("add_rmsnorm: q8 rows do not match the residual")
+    a = AddNormArgs(T, H, ptr(delta), ptr(residual), ptr(norm_w), eps, ptr(out),
+                    ptr(None if q8 is None else q8.codes), ptr(None if q8 is None else q8.scales),
+                    int(q8 is not None and q8.frag))
     check(_lib.lib().q36_add_rmsnorm(C.byref(a), _lib.stream_handle(stream)), "q36_add_rmsnorm")
     return out

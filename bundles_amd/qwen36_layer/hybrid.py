@@ -25,7 +25,7 @@ import torch
 from .. import synth
 from ..qwen36_lmhead8 import lmhead8, node as lm_node
 from . import attn_fused, gdn_fused, moe
-from .glue import Fp8Weight, LinearWorkspace, add_rmsnorm, fp8_linear, prepare_fp8_weight
+from .glue import Fp8Weight, LinearWorkspace, add_rmsnorm, fp8_linear, linear_rows, prepare_fp8_weight
 
 KINDS = ("gdn", "gdn", "gdn", "attn")
 HIDDEN, TOPK = 2048, 10
@@ -166,13 +166,17 @@ def make_state(B: int, T: int, ctx: int, device, seed: int = 0, extra_slots: int
 @dataclass
 class HybridWorkspace:
     """Every intermediate of one step of M = B*T rows (allocated once, reused by every step).  With
-    snapshots=False (the ring form) the per-position GDN state buffers are not allocated."""
+    snapshots=False (the ring form) the per-position GDN state buffers are not allocated.  With
+    prequant (the default) every projection that follows an add-norm or the attention reads e4m3 rows
+    its producer wrote (the add-norm, the MoE's fused add-norm, the attention epilogue) instead of
+    quantizing them in a launch of its own; the outputs are the same bits either way."""
     B: int
     T: int
     E: int
     device: object
     bufs: dict = field(default_factory=dict)
     snapshots: bool = True
+    prequant: bool = True
 
     def __post_init__(self):
         M, dev, bf = self.B * self.T, self.device, torch.bfloat16
@@ -189,6 +193,10 @@ class HybridWorkspace:
             attn=dict(q=e(M, 16, 256), gate=e(M, 16, 256), k=e(M, 2, 256), v=e(M, 2, 256),
                       k8=e(M, 2, 256, dtype=torch.uint8), v8=e(M, 2, 256, dtype=torch.uint8)),
             attn_out=e(M, 16, 256), ids=e(M, dtype=torch.int32))
+        # producer-quantized rows for the layers' first projections (GDN in_proj, attention QKV) and the o_proj
+        self.q8_gdn = linear_rows(M, HIDDEN, dev)
+        self.q8_attn = attn_fused.proj_rows(M, dev)
+        self.q8_o = attn_fused.oproj_rows(M, dev)
         self.lin2048 = LinearWorkspace(M, 2048, dev)
         self.lin4096 = LinearWorkspace(M, 4096, dev)
         self.attn = attn_fused.Workspace(M, dev)
@@ -215,9 +223,14 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
         if trace is not None:
             trace[name] = t.clone() if isinstance(t, torch.Tensor) else t
 
+    def rows_for(i):  # the e4m3 rows layer i's first projection reads (None: it quantizes its own)
+        if not ws.prequant or i >= len(w.layers):
+            return None
+        return ws.q8_gdn if w.layers[i].kind == "gdn" else ws.q8_attn
+
     res, h, h_next = b["residual"], b["h"], b["h2"]
     res.copy_(x)
-    add_rmsnorm(None, res, w.layers[0].input_norm_w, w.eps, out=h, stream=stream)
+    add_rmsnorm(None, res, w.layers[0].input_norm_w, w.eps, out=h, stream=stream, q8=rows_for(0))
     keep("x", x)
     keep("h0", h)
     gi = 0
@@ -227,7 +240,8 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
             g = L.mixer
             fp8_linear(h, g.in_proj, ws.lin2048, segments=[(0, b["mixed"]), (GDN_QKV, b["z"]),
                                                            (GDN_QKV + GDN_Z, b["b"]),
-                                                           (GDN_QKV + GDN_Z + GDN_HV, b["a"])], stream=stream)
+                                                           (GDN_QKV + GDN_Z + GDN_HV, b["a"])], stream=stream,
+                       xq=rows_for(i))
             keep(f"L{i}.mixed", b["mixed"]), keep(f"L{i}.z", b["z"]), keep(f"L{i}.a", b["a"]), keep(f"L{i}.b", b["b"])
             if st.gdn_form == "ring":
                 R = st.ring[gi]
@@ -248,15 +262,16 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
         else:
             a = L.mixer
             p = attn_fused.attn_proj(h, a.w, a.q_norm_w, a.k_norm_w, w.eps, st.cos_sin, st.positions, ws.attn,
-                                     out=b["attn"], stream=stream)
+                                     out=b["attn"], stream=stream, xq=rows_for(i))
+            oq = ws.q8_o if ws.prequant else None
             for k in ("q", "gate", "k8", "v8"):
                 keep(f"L{i}.{k}", p[k])
             attn_fused.attn_decode(p["q"], st.k_cache, st.v_cache, st.page_table, st.seqlens, st.T, ATTN_SCALE,
                                    ws.decode, out_loc=st.out_loc, k_new=p["k8"], v_new=p["v8"], out=b["attn_out"],
-                                   stream=stream)
+                                   stream=stream, gate=p["gate"].view(M, 4096) if oq is not None else None, oq=oq)
             keep(f"L{i}.attn", b["attn_out"])
             attn_fused.attn_oproj(b["attn_out"].view(M, 4096), p["gate"].view(M, 4096), a.w, ws.attn, out=b["o"],
-                                  stream=stream)
+                                  stream=stream, aq=oq)
         keep(f"L{i}.o", b["o"])
         keep(f"L{i}.res_in", res)
         add_rmsnorm(b["o"], res, L.post_norm_w, w.eps, out=h, stream=stream)
@@ -265,7 +280,8 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
         # the next block's input add-norm runs inside the MoE's combine (same bits as add_rmsnorm)
         nxt = w.layers[i + 1].input_norm_w if i + 1 < len(w.layers) else w.final_norm_w
         moe.moe_row_batch(h, None, L.router_w, L.gate_w, L.experts, TOPK, ws.moe, out=b["m"],
-                          router_bias=L.router_bias, stream=stream, norm=(res, nxt, w.eps, h_next))
+                          router_bias=L.router_bias, stream=stream, norm=(res, nxt, w.eps, h_next),
+                          norm_q8=rows_for(i + 1))
         h, h_next = h_next, h
         keep(f"L{i}.moe", b["m"])
         keep(f"L{i}.res_out", res)

@@ -179,7 +179,7 @@ class Workspace:
             y=v(L.y, (S + M) * self.H, torch.bfloat16).view(S + M, self.H))
 
 
-def _args(x, positions, router_w, gate_w, ew, topk, ws: Workspace, out, router_bias, debug, norm=None):
+def _args(x, positions, router_w, gate_w, ew, topk, ws: Workspace, out, router_bias, debug, norm=None, norm_q8=None):
     M, H = x.shape
     if M > ws.max_tokens:
         raise ValueError(f"moe_row_batch: {M} rows exceed the workspace's {ws.max_tokens}")
@@ -204,7 +204,8 @@ def _args(x, positions, router_w, gate_w, ew, topk, ws: Workspace, out, router_b
     return MoeArgs(M, router_w.shape[0], H, ws.I, topk, ws.dtype, ptr(x), ptr(router_w), ptr(router_bias),
                    ptr(positions), *(ptr(t) for t in w), ptr(gate_w), ptr(out), ptr(ws.buf), ws.buf.numel(),
                    ptr(dbg.get("acc13")), ptr(dbg.get("acc2")), ptr(dbg.get("h")), ptr(resid), ptr(norm_w),
-                   float(eps), ptr(norm_out))
+                   float(eps), ptr(norm_out), ptr(None if norm_q8 is None else norm_q8.codes),
+                   ptr(None if norm_q8 is None else norm_q8.scales), int(norm_q8 is not None and norm_q8.frag))
 
 
 def route(x, positions, router_w, topk: int, ws: Workspace, router_bias=None, stream=None):
@@ -215,17 +216,20 @@ def route(x, positions, router_w, topk: int, ws: Workspace, router_bias=None, st
 
 
 def moe_row_batch(x, positions, router_w, gate_w, ew: ExpertWeights, topk: int, ws: Workspace, out=None,
-                  router_bias=None, debug=None, stream=None, norm=None):
+                  router_bias=None, debug=None, stream=None, norm=None, norm_q8=None):
     """out[M, H] = shared_gate * shared_expert(x) + sum_j w_j * expert_{id_j}(x)  (bf16).
 
     norm = (resid, norm_w, eps, norm_out) fuses the next block's input add-norm into the combine:
     resid <- bf16(out + resid) in place and norm_out = its Gemma RMSNorm, the same bits as
-    glue.add_rmsnorm(out, resid, norm_w, eps) after the block (L/qk_route.cu:630-820 combine_norm)."""
+    glue.add_rmsnorm(out, resid, norm_w, eps) after the block (L/qk_route.cu:630-820 combine_norm).
+    norm_q8 (attn_fused.QuantRows, with norm): norm_out's e4m3 codes for the next projection."""
     if ew.E != router_w.shape[0] or ew.I != ws.I or ew.dtype != ws.dtype or ew.E != ws.E:
         raise ValueError("moe_row_batch: expert weights, router and workspace disagree on E / I / dtype")
     if out is None:
         out = torch.empty_like(x)
-    a = _args(x, positions, router_w, gate_w, ew, topk, ws, out, router_bias, debug, norm)
+    if norm_q8 is not None and (norm is None or norm_q8.T != x.shape[0]):
+        raise ValueError("moe_row_batch: norm_q8 needs the fused add-norm and one row per token")
+    a = _args(x, positions, router_w, gate_w, ew, topk, ws, out, router_bias, debug, norm, norm_q8)
     check(_lib.lib().q36_moe_forward(C.byref(a), _lib.stream_handle(stream)), "q36_moe_forward")
     return out
 

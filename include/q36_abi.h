@@ -99,11 +99,15 @@ typedef struct q36_moe_args {
    * L/qk_route.cu:630-820), when norm_out is not NULL: z = out + resid (fp32, out the bf16 combine
    * result), resid <- bf16(z) in place, norm_out = bf16((z * rstd) * (1 + norm_w)) with rstd over z
    * in q36_add_rmsnorm's order: the same bits as q36_add_rmsnorm(out, resid, norm_w) after the block.
-   * resid, norm_out bf16 [M, H]; norm_w bf16 [H]. */
+   * resid, norm_out bf16 [M, H]; norm_w bf16 [H].  norm_q8 / norm_q8s / norm_q8_frag (optional, with
+   * norm_out): also norm_out's e4m3 codes as q36_add_rmsnorm's q8 / q8s / q8_frag. */
   void* resid;
   const void* norm_w;
   float norm_eps;
   void* norm_out;
+  void* norm_q8;
+  float* norm_q8s;
+  int32_t norm_q8_frag;
 } q36_moe_args;
 
 typedef struct q36_moe_ws_layout {
@@ -271,7 +275,18 @@ int q36_gdn_verify_ring(const q36_gdn_ring_args* a, q36_stream_t stream);
  *     (L/qk_attn_verify.cu:730-737).
  * Alignment: x, wqkv, attn, gate, wo, the norm weights, cos_sin and q, gate, k, v 16 bytes; k8, v8
  * 8 bytes.
- * Workspaces: q36_attn_workspace_bytes(T), q36_oproj_workspace_bytes(T), 256-byte aligned. */
+ * Workspaces: q36_attn_workspace_bytes(T), q36_oproj_workspace_bytes(T), 256-byte aligned.
+ * Activations quantized by their producer (no reference counterpart: the quantization folded into the
+ * kernel that writes the rows, so these entries skip their own act_quant launch):
+ *   q36_attn_proj with xq / xqs set (x then unused, may be NULL): the e4m3 codes of x's rows per token
+ *     x 128 channels, in fragment order when q36_attn_act_frag(T) (codes [ceil(T/16)*16, 2048] by
+ *     q36_pack_frag8's order of tokens x channels, the padding tokens' codes and scales zero), else
+ *     row-major [T, 2048]; xqs fp32 [that many tokens, 16] = group amax / 448.  q36_add_rmsnorm
+ *     (q8 / q8s / q8_frag) and q36_moe_forward's fused add-norm (norm_q8 ...) write exactly these.
+ *   q36_attn_oproj with aq / aqs set (attn, gate unused, may be NULL): e4m3 codes row-major [T, 4096]
+ *     of bf16(attn * sigmoid(gate)) and fp32 [T, 32] scales, as q36_attn_decode writes them
+ *     (its gate / oq / oqs).
+ * Either way the projection's outputs are the same bits as from the bf16 inputs. */
 typedef struct q36_attn_args {
   int32_t T, max_pos;
   const void* x;
@@ -290,6 +305,8 @@ typedef struct q36_attn_args {
   void* v8;
   void* workspace;
   size_t workspace_bytes;
+  const void* xq;  /* optional producer-quantized x (see above) */
+  const float* xqs;
 } q36_attn_args;
 typedef struct q36_oproj_args {
   int32_t T;
@@ -300,7 +317,12 @@ typedef struct q36_oproj_args {
   void* out;
   void* workspace;
   size_t workspace_bytes;
+  const void* aq;  /* optional producer-quantized o_proj input (see above) */
+  const float* aqs;
 } q36_oproj_args;
+/* 1 when q36_attn_proj reads T tokens' activations in fragment order (its K-sliced and tiled GEMMs,
+ * T >= 32), 0 when row-major (the streaming GEMM below 32 tokens). */
+int q36_attn_act_frag(int32_t T);
 size_t q36_attn_workspace_bytes(int32_t T);
 size_t q36_oproj_workspace_bytes(int32_t T);
 int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream);
@@ -315,7 +337,9 @@ int q36_attn_oproj(const q36_oproj_args* a, q36_stream_t stream);
  * in fragment order (q36_pack_frag8), N a multiple of 128 (rows past n_out are padding), ws fp32
  * [N/128, K/128].  y[t, n] = bf16(sum over 128-blocks kb in order of fma(blocksum, xs * ws, acc)).
  * Column n < n_out goes to the segment i with seg[i].col0 <= n < seg[i+1].col0 (or n_out), at
- * seg[i].out[t * seg[i].ld + n - seg[i].col0]; col0 and ld multiples of 4, outputs 8-byte aligned. */
+ * seg[i].out[t * seg[i].ld + n - seg[i].col0]; col0 and ld multiples of 4, outputs 8-byte aligned.
+ * xq / xqs (optional, no reference counterpart): x already quantized by its producer (x then unused),
+ * as q36_attn_proj's xq / xqs but in the layout q36_fp8_linear_act_frag(T, K) names. */
 typedef struct q36_linear_seg {
   int32_t col0;
   int32_t ld;
@@ -330,7 +354,12 @@ typedef struct q36_fp8_linear_args {
   q36_linear_seg seg[4];
   void* workspace;
   size_t workspace_bytes;
+  const void* xq;
+  const float* xqs;
 } q36_fp8_linear_args;
+/* 1 when q36_fp8_linear reads T tokens' activations of width K in fragment order (its tiled GEMM,
+ * T >= 129 and K = 2048), 0 when row-major. */
+int q36_fp8_linear_act_frag(int32_t T, int32_t K);
 size_t q36_fp8_linear_workspace_bytes(int32_t T, int32_t K);
 int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream);
 
@@ -358,7 +387,10 @@ int q36_dense8_linear(const q36_dense8_linear_args* a, q36_stream_t stream);
  * z = bf16 delta + residual in fp32 (delta NULL: z = residual); residual <- bf16(z) when delta is
  * given; out = bf16((z * rstd) * (1 + w)), rstd = 1 / sqrt(sum z^2 / H + eps) with the sum in the
  * fixed order lane l of 64 owns the 8-element chunks l + 64 j (fma from zero), then an xor
- * butterfly 32..1.  H = 2048; delta, residual, out and w 16-byte aligned. */
+ * butterfly 32..1.  H = 2048; delta, residual, out and w 16-byte aligned.
+ * q8 (optional, no reference counterpart): also the e4m3 codes of out per token x 128 channels, the
+ * input q36_attn_proj takes as xq / xqs for the next layer's projection: q8 in fragment order when
+ * q8_frag (then ceil(T/16)*16 tokens, padding zero), else row-major [T, 2048]; q8s fp32 [tokens, 16]. */
 typedef struct q36_add_norm_args {
   int32_t T, H;
   const void* delta;
@@ -366,6 +398,9 @@ typedef struct q36_add_norm_args {
   const void* norm_w;
   float eps;
   void* out;
+  void* q8;
+  float* q8s;
+  int32_t q8_frag;
 } q36_add_norm_args;
 int q36_add_rmsnorm(const q36_add_norm_args* a, q36_stream_t stream);
 
@@ -378,6 +413,10 @@ int q36_add_rmsnorm(const q36_add_norm_args* a, q36_stream_t stream);
  * K/V rows (k_new, v_new e4m3 [B*NT, HKV, D], q36_attn_proj's k8 / v8) are written to first.
  * Scores s = (e4m3(q) . k) * scale, softmax weights rounded to f16 for P V, V widened to f16.
  * out bf16 [B*NT, HQ, D] = bf16(o / l), not gated (the o_proj applies the sigmoid gate).
+ * gate / oq / oqs (optional, no reference counterpart: the o_proj's input quantization folded in):
+ * with gate bf16 [B*NT, HQ*D] (q36_attn_proj's gate output), oq receives the e4m3 codes row-major
+ * [B*NT, HQ*D] of bf16(out * sigmoid(gate)) per 128-channel group and oqs fp32 [B*NT, HQ*D/128] the
+ * group scales (amax / 448): q36_attn_oproj's aq / aqs.
  * splits: 0 = min(64, CUs / (B * HKV)).  Constraints: HQ = 16, HKV = 2, D = 256, 1 <= NT <= 4,
  * num_slots * HKV * D < 2^31; q, caches 16-byte aligned. */
 typedef struct q36_decode_args {
@@ -396,6 +435,9 @@ typedef struct q36_decode_args {
   void* out;
   void* workspace;
   size_t workspace_bytes;
+  const void* gate;
+  void* oq;
+  float* oqs;
 } q36_decode_args;
 size_t q36_attn_decode_workspace_bytes(int32_t B, int32_t splits);
 int q36_attn_decode(const q36_decode_args* a, q36_stream_t stream);

@@ -112,3 +112,97 @@ def test_pack_frag_layout(attn, dev):
                     row, col = 16 * r + l % 16, 128 * b + 32 * (l // 16) + 16 * h
                     ref[base + h * 1024 + 16 * l: base + h * 1024 + 16 * l + 16] = src[row, col:col + 16]
     assert np.array_equal(got.reshape(-1), ref)
+
+
+# ---- activations quantized by their producer kernels (the projections skip their own launch) -----------
+def _same(a, b, what):
+    assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                       b.view(torch.int16) if b.dtype == torch.bfloat16 else b), what
+
+
+@pytest.mark.parametrize("T", [1, 37, 128, 256])
+def test_attn_proj_from_add_norm_codes(attn, dev, T):
+    """q36_add_rmsnorm's e4m3 rows (q8) fed to q36_attn_proj (xq) give the same bits as the projection
+    of the add-norm's bf16 output; the codes equal the projection's own quantization in either layout."""
+    from bundles_amd.qwen36_layer import glue
+    print(f"attn_proj from add-norm codes T={T}", flush=True)
+    d, w = _setup(attn, dev, T, seed=300 + T)
+    g = torch.Generator(device=dev).manual_seed(T)
+    resid = torch.randn((T, 2048), generator=g, device=dev).to(torch.bfloat16)
+    delta = torch.randn((T, 2048), generator=g, device=dev).to(torch.bfloat16)
+    nw = (torch.randn(2048, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    r1, r2 = resid.clone(), resid.clone()
+    h = glue.add_rmsnorm(delta, r1, nw, 1e-6)
+    xq = attn.proj_rows(T, dev)
+    xq.codes.fill_(0x7F)  # the padding rows must be written, not left as they were
+    xq.scales.fill_(float("nan"))
+    h2 = glue.add_rmsnorm(delta, r2, nw, 1e-6, q8=xq)
+    ws = attn.Workspace(T, dev)
+    ref = attn.attn_proj(h, w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"], ws)
+    ref = {k: v.clone() for k, v in ref.items()}
+    got = attn.attn_proj(None, w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"], ws, xq=xq)
+    torch.cuda.synchronize()
+    _same(h, h2, "add-norm out")
+    _same(r1, r2, "residual")
+    for k in ref:
+        _same(got[k], ref[k], k)
+    # every byte written (a quantized code is never the NaN pattern 0x7f), padding tokens' scales zero
+    assert (xq.codes != 0x7F).all() and torch.isfinite(xq.scales).all() and (xq.scales[T:] == 0).all()
+
+
+def test_attn_proj_from_moe_combine_codes(attn, dev):
+    """The MoE's fused add-norm with norm_q8: its e4m3 rows drive q36_attn_proj to the same bits as its
+    bf16 norm_out does (64 rows: fragment order)."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import moe
+    M, E = 64, 64
+    print("attn_proj from MoE combine codes", flush=True)
+    md = synth.moe_inputs(M, dev, seed=8, E=E)
+    ew = moe.prepare_experts(md["w13"], md["w2"], md["sw13"], md["sw2"], moe.Q36_MOE_FP8)
+    mws = moe.Workspace(E, 2048, 512, 10, moe.Q36_MOE_FP8, dev)
+    g = torch.Generator(device=dev).manual_seed(9)
+    resid = torch.randn((M, 2048), generator=g, device=dev).to(torch.bfloat16)
+    nw = (torch.randn(2048, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    n1, n2 = torch.empty_like(resid), torch.empty_like(resid)
+    r1, r2 = resid.clone(), resid.clone()
+    moe.moe_row_batch(md["x"], None, md["router_w"], md["gate_w"], ew, 10, mws, norm=(r1, nw, 1e-6, n1))
+    xq = attn.proj_rows(M, dev)
+    moe.moe_row_batch(md["x"], None, md["router_w"], md["gate_w"], ew, 10, mws, norm=(r2, nw, 1e-6, n2), norm_q8=xq)
+    d, w = _setup(attn, dev, M, seed=77)
+    ws = attn.Workspace(M, dev)
+    ref = attn.attn_proj(n1, w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"], ws)
+    ref = {k: v.clone() for k, v in ref.items()}
+    got = attn.attn_proj(None, w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"], ws, xq=xq)
+    torch.cuda.synchronize()
+    _same(n1, n2, "norm_out")
+    for k in ref:
+        _same(got[k], ref[k], k)
+
+
+@pytest.mark.parametrize("B,NT,splits", [(2, 4, 1), (4, 4, 0), (32, 1, 2)])
+def test_oproj_from_decode_codes(attn, dev, B, NT, splits):
+    """q36_attn_decode with the gate writes the o_proj's e4m3 input; q36_attn_oproj on it (aq) gives
+    the same bits as on the bf16 attention output and gate (one split: the split kernel's epilogue;
+    several: the combine's)."""
+    print(f"oproj from decode codes B={B} NT={NT} splits={splits}", flush=True)
+    T = B * NT
+    g = torch.Generator(device=dev).manual_seed(B * 10 + NT)
+    ctx = 300
+    slots = B * ctx + 16
+    q = torch.randn((T, 16, 256), generator=g, device=dev).to(torch.bfloat16)
+    kc = torch.randn((slots, 2, 256), generator=g, device=dev).to(torch.float8_e4m3fn).view(torch.uint8)
+    vc = torch.randn((slots, 2, 256), generator=g, device=dev).to(torch.float8_e4m3fn).view(torch.uint8)
+    pt = torch.randperm(slots, generator=g, device=dev)[:B * ctx].to(torch.int32).view(B, ctx).contiguous()
+    sl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    gate = (torch.randn((T, 4096), generator=g, device=dev) * 2).to(torch.bfloat16)
+    dws = attn.DecodeWorkspace(B, dev, splits=splits)
+    o1 = attn.attn_decode(q, kc, vc, pt, sl, NT, 1.0 / 16, dws)
+    oq = attn.oproj_rows(T, dev)
+    o2 = attn.attn_decode(q, kc, vc, pt, sl, NT, 1.0 / 16, dws, gate=gate, oq=oq)
+    d, w = _setup(attn, dev, T, seed=5)
+    ws = attn.Workspace(T, dev)
+    ref = attn.attn_oproj(o1.view(T, -1), gate, w, ws)
+    got = attn.attn_oproj(None, None, w, ws, aq=oq)
+    torch.cuda.synchronize()
+    _same(o1, o2, "attention out")
+    _same(got, ref, "o_proj out")

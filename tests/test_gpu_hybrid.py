@@ -171,3 +171,20 @@ def test_end_to_end_against_the_free_running_oracle(run, oracle_mod):
     ids, _ = O.lmhead(h, None, w.eps, np_(w.lm_q), np_(w.lm_s), two_term=mode == "two_term", w8a16=mode == "w8a16")
     agree = float(np.mean(ids == np_(run["ids"])))
     print(f"end to end: final hidden row error {wr:.2e}, greedy ids agree on {agree:.2f} of rows", flush=True)
+
+
+def test_producer_quantized_rows_change_no_bit(run, dev):
+    """The step with every projection quantizing its own input (prequant=False) gives the same bits at
+    every stage as the default, where the add-norms, the MoE's fused add-norm and the attention
+    epilogue write the e4m3 rows (the KV cache rows it rewrites are the same values)."""
+    from bundles_amd import synth
+    hybrid, w, st = run["hybrid"], run["w"], run["st"]
+    ws = hybrid.HybridWorkspace(B, T, E, dev, prequant=False)
+    x = synth.randn((B * T, 2048), synth.gen(dev, 5), dev)
+    trace = {}
+    ids = hybrid.forward(x, w, st, ws, trace=trace)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, run["ids"])
+    for k, v in run["trace"].items():
+        if isinstance(v, torch.Tensor):
+            assert torch.equal(trace[k].view(torch.uint8), v.view(torch.uint8)), k
