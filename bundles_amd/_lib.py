@@ -52,7 +52,7 @@ class GdnRingArgs(C.Structure):
                 ("d_ring", P), ("dlo_ring", P), ("d_slot", I64), ("dlo_slot", I64), ("k_ring", P), ("klo_ring", P),
                 ("k_slot", I64), ("klo_slot", I64), ("g_ring", P), ("g_slot", I64), ("qsl", P), ("state_idx", P),
                 ("replay_idx", P), ("win_idx", P), ("idx_i64", I32), ("write_pos", P), ("cache_base", P),
-                ("norm_w", P), ("eps", C.c_float), ("scale", C.c_float), ("out", P)]
+                ("norm_w", P), ("eps", C.c_float), ("scale", C.c_float), ("out", P), ("oq", P), ("oqs", P)]
 
 
 class AttnArgs(C.Structure):

@@ -63,6 +63,8 @@ struct GdnRingDev {
   const uint16_t* norm_w;
   float eps, scale;
   uint16_t* out;
+  uint8_t* oq;   // out's e4m3 codes per value head (the out_proj's input), or null
+  float* oqs;    // [rows, 32] their scales
 };
 
 // Four waves per SIMD (two workgroups per CU): at most 128 VGPRs, of which the 16 x 4 h0 values are 64.
@@ -106,6 +108,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
     if (tid < 64 * T) {
       const int t = tid >> 6, c = (tid & 63) * 4;
       *reinterpret_cast<v2i*>(d.out + (bos + t) * RZ + hk * 2 * RV + c) = v2i{0, 0};
+      if (d.oq) {
+        *reinterpret_cast<uint32_t*>(d.oq + (bos + t) * RZ + hk * 2 * RV + c) = 0u;
+        if (c == 0) {  // the key head's two value heads
+          d.oqs[(bos + t) * RHV + 2 * hk] = 0.f;
+          d.oqs[(bos + t) * RHV + 2 * hk + 1] = 0.f;
+        }
+      }
     }
     return;
   }
@@ -409,8 +418,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void g
       const float rstd = 1.f / sqrtf(ss / (float)RV + d.eps);
       const float z0 = bf2f(zs[t][h * RV + lane]), z1 = bf2f(zs[t][h * RV + lane + 64]);
       uint16_t* op = d.out + (bos + t) * RZ + (2 * hk + h) * RV + lane;
-      op[0] = (uint16_t)f2bf(((o0 * rstd) * nws[lane]) * (z0 * sigmoid_q(z0)));
-      op[64] = (uint16_t)f2bf(((o1 * rstd) * nws[lane + 64]) * (z1 * sigmoid_q(z1)));
+      const uint32_t y0 = f2bf(((o0 * rstd) * nws[lane]) * (z0 * sigmoid_q(z0)));
+      const uint32_t y1 = f2bf(((o1 * rstd) * nws[lane + 64]) * (z1 * sigmoid_q(z1)));
+      op[0] = (uint16_t)y0;
+      op[64] = (uint16_t)y1;
+      if (d.oq) {
+        // the value head's 128 outputs are one e4m3 group of the out_proj's input (the wave's lanes)
+        const float f0 = bf2f(y0), f1 = bf2f(y1);
+        const float m = wave_max(fmaxf(fabsf(f0), fabsf(f1)));
+        const float inv = m > 0.f ? 448.f / m : 0.f;
+        const uint32_t cd = f2e4m3x2_hw(f0 * inv, f1 * inv);
+        uint8_t* qp = d.oq + (bos + t) * RZ + (2 * hk + h) * RV + lane;
+        qp[0] = (uint8_t)(cd & 0xffu);
+        qp[64] = (uint8_t)((cd >> 8) & 0xffu);
+        if (lane == 0) d.oqs[(bos + t) * RHV + 2 * hk + h] = m / 448.f;
+      }
     }
   }
 }
@@ -449,6 +471,9 @@ extern "C" int q36_gdn_verify_ring(const q36_gdn_ring_args* a, q36_stream_t stre
                   aligned16(a->out),
               "q36_gdn_verify_ring: h0, z, conv_state, window, conv_w, the rings and out must be 16-byte aligned");
   Q36_REQUIRE((reinterpret_cast<uintptr_t>(a->dt_bias) & 3) == 0, "q36_gdn_verify_ring: dt_bias must be 4-byte aligned");
+  Q36_REQUIRE((a->oq == nullptr) == (a->oqs == nullptr), "q36_gdn_verify_ring: oq and oqs go together");
+  Q36_REQUIRE(!a->oq || ((reinterpret_cast<uintptr_t>(a->oq) & 3u) == 0 && (reinterpret_cast<uintptr_t>(a->oqs) & 3u) == 0),
+              "q36_gdn_verify_ring: oq and oqs must be 4-byte aligned");
   GdnRingDev d{a->B, a->T, a->rows, a->slots, a->rslots, a->wslots,
                static_cast<const uint16_t*>(a->mixed), static_cast<const uint16_t*>(a->z),
                static_cast<const uint16_t*>(a->a), static_cast<const uint16_t*>(a->b),
@@ -458,7 +483,7 @@ extern "C" int q36_gdn_verify_ring(const q36_gdn_ring_args* a, q36_stream_t stre
                static_cast<uint16_t*>(a->k_ring), static_cast<uint16_t*>(a->klo_ring), a->k_slot, a->klo_slot,
                a->g_ring, a->g_slot, a->qsl, a->state_idx, a->replay_idx, a->win_idx, a->idx_i64 & 7,
                a->write_pos, a->cache_base, static_cast<const uint16_t*>(a->norm_w), a->eps, a->scale,
-               static_cast<uint16_t*>(a->out)};
+               static_cast<uint16_t*>(a->out), static_cast<uint8_t*>(a->oq), a->oqs};
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (a->T <= 4) gdn_ring_kernel<4><<<a->B * RHK, 512, 0, st>>>(d);
   else if (a->T == 5) gdn_ring_kernel<5><<<a->B * RHK, 512, 0, st>>>(d);

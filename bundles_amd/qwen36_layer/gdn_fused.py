@@ -77,7 +77,7 @@ def _idx(t, name, n):
 def gdn_verify_ring(mixed, z, a, b, conv_state, conv_w, window, A_log, dt_bias, h0, d_ring, dlo_ring, k_ring,
                     klo_ring, g_ring, qsl, state_idx, replay_idx, win_idx, write_pos, cache_base, norm_w,
                     eps: float = 1e-6, scale: float = HEAD_K ** -0.5, pf_weight=None, *, T: int = 4, out=None,
-                    stream=None):
+                    stream=None, oq=None):
     """out_proj's input [rows, 4096] for a verify batch over the ReplaySSM ring.
 
     The argument list is the reference kernel's (L/qk_gdn_verify.cu:841-849).  rows = B * T with T the
@@ -85,6 +85,7 @@ def gdn_verify_ring(mixed, z, a, b, conv_state, conv_w, window, A_log, dt_bias, 
     conv_state, window and the five rings are updated in place; h0 is read only.  window is either
     the [wslots, 8192, T + 2] record pool or the reference's deduplicated [wslots, T, 8192, 3] view
     of it.  pf_weight is the reference's L2-prefetch hint (no effect on results) and is ignored.
+    oq (glue.linear_rows(rows, 4096)): out's e4m3 codes also go there, the out_proj's pre-quantized input.
     Raises ValueError on a layout the kernel does not serve, RuntimeError when the library
     rejects the call."""
     rows = mixed.shape[0]
@@ -131,12 +132,15 @@ def gdn_verify_ring(mixed, z, a, b, conv_state, conv_w, window, A_log, dt_bias, 
     _req(norm_w, "norm weight", torch.bfloat16, (HEAD_V,))
     out = torch.empty((rows, N_V_HEADS * HEAD_V), dtype=torch.bfloat16, device=mixed.device) if out is None else out
     _req(out, "out", torch.bfloat16, (rows, N_V_HEADS * HEAD_V))
+    if oq is not None and (oq.T != rows or oq.frag or oq.codes.shape[1] != N_V_HEADS * HEAD_V):
+        raise ValueError("gdn_verify_ring: oq must be row-major rows of the verify batch (glue.linear_rows)")
     args = GdnRingArgs(
         B, T, rows, min(conv_state.shape[0], h0.shape[0]), rslots, window.shape[0],
         ptr(mixed), ptr(z), ptr(a), ptr(b), ptr(conv_state), conv_state.stride(0), ptr(conv_w), ptr(window),
         window.stride(0), ptr(A_log), ptr(dt_bias), int(dt_bias.dtype == torch.float32), ptr(h0),
         ptr(d_ring), ptr(dlo_ring), d_ring.stride(0), dlo_ring.stride(0), ptr(k_ring), ptr(klo_ring),
         k_ring.stride(0), klo_ring.stride(0), ptr(g_ring), g_ring.stride(0), ptr(qsl), ptr(state_idx),
-        ptr(replay_idx), ptr(win_idx), flags, ptr(write_pos), ptr(cache_base), ptr(norm_w), eps, scale, ptr(out))
+        ptr(replay_idx), ptr(win_idx), flags, ptr(write_pos), ptr(cache_base), ptr(norm_w), eps, scale, ptr(out),
+        ptr(None if oq is None else oq.codes), ptr(None if oq is None else oq.scales))
     check(_lib.lib().q36_gdn_verify_ring(C.byref(args), _lib.stream_handle(stream)), "q36_gdn_verify_ring")
     return out

@@ -197,6 +197,7 @@ class HybridWorkspace:
         self.q8_gdn = linear_rows(M, HIDDEN, dev)
         self.q8_attn = attn_fused.proj_rows(M, dev)
         self.q8_o = attn_fused.oproj_rows(M, dev)
+        self.q8_gout = linear_rows(M, 4096, dev)  # the ring verify's output codes for the out_proj
         self.lin2048 = LinearWorkspace(M, 2048, dev)
         self.lin4096 = LinearWorkspace(M, 4096, dev)
         self.attn = attn_fused.Workspace(M, dev)
@@ -251,13 +252,16 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
                 gdn_fused.gdn_verify_ring(b["mixed"], b["z"], b["a"], b["b"], st.conv_state[gi], g.conv_w, R["window"],
                                           g.A_log, g.dt_bias, st.S[gi], R["d"], R["dlo"], R["k"], R["klo"], R["g"],
                                           R["qsl"], R["idx"], R["idx"], R["idx"], R["wp"], R["cb"], g.norm_w, w.eps,
-                                          128 ** -0.5, T=st.T, out=b["gout"], stream=stream)
+                                          128 ** -0.5, T=st.T, out=b["gout"], stream=stream,
+                                          oq=ws.q8_gout if ws.prequant else None)
+                gq = ws.q8_gout if ws.prequant else None
             else:
                 gdn_fused.gdn_verify_fused(b["mixed"], b["z"], b["a"], b["b"], st.conv_state[gi], g.conv_w, g.A_log,
                                            g.dt_bias, st.S[gi], g.norm_w, w.eps, T=st.T, out=b["gout"],
                                            snaps=b["snaps"][gi], conv_state_out=b["conv_out"][gi], stream=stream)
+                gq = None
             keep(f"L{i}.gout", b["gout"])
-            fp8_linear(b["gout"], g.out_proj, ws.lin4096, segments=[(0, b["o"])], stream=stream)
+            fp8_linear(b["gout"], g.out_proj, ws.lin4096, segments=[(0, b["o"])], stream=stream, xq=gq)
             gi += 1
         else:
             a = L.mixer

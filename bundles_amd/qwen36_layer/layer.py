@@ -33,7 +33,7 @@ import torch
 from . import attn_fused, gdn_fused, moe
 from .engine import EngineView, SglangView
 from .formats import quant_dense8
-from .glue import LinearWorkspace, dense8_linear, fp8_linear, prepare_fp8_weight
+from .glue import LinearWorkspace, dense8_linear, fp8_linear, linear_rows, prepare_fp8_weight
 
 HIDDEN, EXPERTS, INTERMEDIATE, TOPK = 2048, 512, 512, 10
 MAX_TOKENS = moe.MAX_TOKENS
@@ -230,15 +230,17 @@ class _GdnMixer:
         else:
             fp8_linear(x, self.in_proj, sc.lin2048, segments=segs)
         p = pools
+        # the e4m3 out_proj input comes from the verify kernel's epilogue (same bits as quantizing core)
+        oq = None if dense8 else linear_rows(rows, PROJ_IN, x.device)
         core = gdn_fused.gdn_verify_ring(mixed, z, a, b, p.conv_state, self.conv_w, p.window, self.A_log,
                                          self.dt_bias, p.h0, p.d, p.dlo, p.k, p.klo, p.g, p.qsl, p.state_idx,
                                          p.replay_idx, p.win_idx, p.write_pos, p.cache_base, self.norm_w, self.eps,
-                                         self.scale, T=p.draft)
+                                         self.scale, T=p.draft, oq=oq)
         out = torch.empty((rows, HIDDEN), **e)
         if dense8:
             dense8_linear(core, *self.out8, segments=[(0, out)])
         else:
-            fp8_linear(core, self.out_proj, sc.lin4096, segments=[(0, out)])
+            fp8_linear(core, self.out_proj, sc.lin4096, segments=[(0, out)], xq=oq)
         return out
 
 
@@ -320,9 +322,12 @@ class _AttnMixer:
         pos = positions.to(torch.int32).contiguous()
         p = attn_fused.attn_proj(x.contiguous(), self.w, self.q_norm_w, self.k_norm_w, self.eps, self.cos_sin, pos,
                                  sc.attn)
+        # the o_proj's e4m3 input comes from the attention's epilogue (same bits as quantizing o * sigmoid(gate))
+        aq = attn_fused.oproj_rows(rows, x.device)
+        gate = p["gate"].view(rows, -1)
         o = attn_fused.attn_decode(p["q"], kv.k_cache, kv.v_cache, kv.page_table, kv.seqlens, kv.draft, self.scale,
-                                   sc.decode, out_loc=kv.out_loc, k_new=p["k8"], v_new=p["v8"])
-        return attn_fused.attn_oproj(o.view(rows, -1), p["gate"].view(rows, -1), self.w, sc.attn)
+                                   sc.decode, out_loc=kv.out_loc, k_new=p["k8"], v_new=p["v8"], gate=gate, oq=aq)
+        return attn_fused.attn_oproj(o.view(rows, -1), gate, self.w, sc.attn, aq=aq)
 
 
 def _install_attention(module, replica, engine, max_tokens):

@@ -256,6 +256,11 @@ typedef struct q36_gdn_ring_args {
   const void* norm_w;
   float eps, scale;
   void* out;
+  /* optional (no reference counterpart): out's e4m3 codes row-major [rows, 4096] per 128 channels (one
+   * value head) and fp32 scales [rows, 32], the input q36_fp8_linear takes as xq / xqs for the
+   * out_proj (K = 4096 reads row-major); a padded request's rows get zero codes and scales */
+  void* oq;
+  float* oqs;
 } q36_gdn_ring_args;
 int q36_gdn_verify_ring(const q36_gdn_ring_args* a, q36_stream_t stream);
 

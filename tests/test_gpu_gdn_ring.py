@@ -143,3 +143,41 @@ def test_ring_rejects_bad_layouts(gdn, dev):
     bad[10] = d["d_ring"][:, :, :8]  # an 8-entry ring is not the served layout
     with pytest.raises(ValueError, match="d ring"):
         gdn.gdn_verify_ring(*bad, T=4)
+
+
+@pytest.mark.parametrize("padded", [(), (1,)])
+def test_ring_out_proj_codes(gdn, dev, padded):
+    """The verify kernel's e4m3 codes of its output (oq) drive the out_proj (q36_fp8_linear, K = 4096)
+    to the same bits as the bf16 output does; a padded request's rows get zero codes and scales."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import glue
+    B, T = 4, 5
+    print(f"gdn ring out_proj codes padded={padded}", flush=True)
+    d = synth.gdn_ring_inputs(B, T, dev, seed=41, padded=padded)
+    pools = {k: d[k].clone() for k in POOLS}
+
+    def run(oq):
+        for k in POOLS:
+            d[k].copy_(pools[k])
+        return gdn.gdn_verify_ring(d["mixed"], d["z"], d["a"], d["b"], d["conv_state"], d["conv_w"], d["window"],
+                                   d["A_log"], d["dt_bias"], d["h0"], d["d_ring"], d["dlo_ring"], d["k_ring"],
+                                   d["klo_ring"], d["g_ring"], d["qsl"], d["state_idx"], d["replay_idx"],
+                                   d["win_idx"], d["write_pos"], d["cache_base"], d["norm_w"], 1e-6, d["scale"],
+                                   T=T, oq=oq)
+    out1 = run(None).clone()
+    oq = glue.linear_rows(B * T, 4096, dev)
+    oq.codes.fill_(0x7F)
+    oq.scales.fill_(float("nan"))
+    out2 = run(oq)
+    g = torch.Generator(device=dev).manual_seed(3)
+    w = glue.prepare_fp8_weight((torch.randn((2048, 4096), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+    ws = glue.LinearWorkspace(B * T, 4096, dev)
+    y1 = glue.fp8_linear(out1, w, ws)
+    y2 = glue.fp8_linear(None, w, ws, xq=oq)
+    torch.cuda.synchronize()
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert (oq.codes != 0x7F).all() and torch.isfinite(oq.scales).all()
+    for r in padded:
+        rows = slice(int(d["qsl"][r]), int(d["qsl"][r]) + T)
+        assert not oq.codes[rows].any() and not oq.scales[rows].any()
