@@ -205,17 +205,21 @@ def bench_small(args, torch, dev):
         ws_ = []
         for _ in range(copies):
             w = (torch.randn((N, K), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
-            ws_.append(formats.quant_dense8(w))
+            q, s = formats.quant_dense8(w)
+            ws_.append((q, formats.tile_w16(q), s))
             del w
         pts = {}
         for T in (1, 4, 16, 32):
             x = torch.randn((T, K), generator=gen, device=dev).to(torch.bfloat16)
             y = torch.empty((T, N), dtype=torch.bfloat16, device=dev)
-            calls = [lambda q=q, s=s: glue.dense8_linear(x, q, s, segments=[(0, y)]) for q, s in ws_]
+            # the layer node's form: the copy's rows in the kernel's tile order; beside it the row-major copy
+            calls = [lambda q=qt, s=s: glue.dense8_linear(x, q, s, segments=[(0, y)], tiled=True) for _, qt, s in ws_]
             ms = graph_time(calls)
+            ms_rm = graph_time([lambda q=q, s=s: glue.dense8_linear(x, q, s, segments=[(0, y)]) for q, _, s in ws_])
             algo = N * K + (K // 128) * N * 2 + T * K * 2 + T * N * 2
             pts[f"t{T}"] = dict(us=round(ms * 1e3, 2), bytes=algo, gbs=round(algo / (ms * 1e-3) / 1e9, 1),
-                                frac_hbm=round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+                                frac_hbm=round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                us_row_major=round(ms_rm * 1e3, 2))
         res[name] = dict(rows=N, k=K, copies_cycled=copies, **pts)
         print(f"bench: {name} done", file=sys.stderr, flush=True)
         del ws_

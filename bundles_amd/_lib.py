@@ -84,7 +84,7 @@ class Fp8LinearArgs(C.Structure):
 
 class Dense8LinearArgs(C.Structure):
     _fields_ = [("T", I32), ("N", I32), ("K", I32), ("n_out", I32), ("x", P), ("q", P), ("s", P),
-                ("s_ld", C.c_int64), ("nseg", I32), ("seg", LinearSeg * 4)]
+                ("s_ld", C.c_int64), ("nseg", I32), ("seg", LinearSeg * 4), ("tiled", I32)]
 
 
 class AddNormArgs(C.Structure):
@@ -125,6 +125,7 @@ SYMBOLS = [
     ("q36_fp8_linear", I32, [C.POINTER(Fp8LinearArgs), P]),
     ("q36_add_rmsnorm", I32, [C.POINTER(AddNormArgs), P]),
     ("q36_dense8_linear", I32, [C.POINTER(Dense8LinearArgs), P]),
+    ("q36_tile_w16", I32, [P, C.c_int64, I32, P, P]),
     ("q36_attn_decode_workspace_bytes", SZ, [I32, I32]),
     ("q36_attn_decode", I32, [C.POINTER(DecodeArgs), P]),
     ("q36_lmhead_workspace_bytes", SZ, [I32]),

@@ -9,7 +9,8 @@ namespace q36 {
 struct W16Dev {
   int T, N, K;
   const uint16_t* x;      // bf16 [T, K]
-  const int8_t* q;        // int8 [N, K]
+  const int8_t* q;        // int8 [N, K], row-major or (tiled) in the tile order of q36_tile_w16
+  int tiled;
   // mode 0
   const float* ws;        // fp32 [N]
   uint16_t* logits;       // bf16 [T, N] or null

@@ -80,9 +80,13 @@ __global__ __launch_bounds__(64 * WAVES) void w8a16_kernel(W16Dev d) {
   const int8_t* wrow = d.q + (size_t)(active ? r0 : 0) * K;
   const __amdgpu_buffer_rsrc_t wrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)wrow, (short)0, active ? RW * K : 0, 0x00020000);
+  // row-major: lane (lr, lg) reads row lr at columns 64 s + 16 lg (an instruction spans 16 rows); tiled:
+  // the same 16 bytes at 16 lane of the step's 1 KB piece (an instruction reads 1 KB contiguous)
+  const int tiled = d.tiled, sstep = tiled ? 1024 : 64;
   int wv[RT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) wv[rt] = (16 * rt + lr) * K + k0 + 16 * lg;
+  for (int rt = 0; rt < RT; ++rt)
+    wv[rt] = tiled ? 16 * rt * K + (k0 >> 6) * 1024 + 16 * lane : (16 * rt + lr) * K + k0 + 16 * lg;
   // activations: token 16 tt + lr (tokens past T read as zero), elements k0 + 64 s + 16 lg .. + 15
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)d.x, (short)0, d.T * K * 2, 0x00020000);
@@ -107,7 +111,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8a16_kernel(W16Dev d) {
     // (nsteps is a compile-time constant and the step loop unrolls, so `in` folds away per step.)
     auto issue = [&](int u, int s) {
       const bool in = s < nsteps;
-      const int wo = in ? 64 * s : 0, xo = in ? 128 * s : 0, oob = in ? 0 : (1 << 30);
+      const int wo = in ? sstep * s : 0, xo = in ? 128 * s : 0, oob = in ? 0 : (1 << 30);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) wq[u][rt] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wv[rt] + oob, wo, 2);
 #pragma unroll
@@ -326,6 +330,34 @@ int launch_w8a16(const W16Dev& d, int mode, hipStream_t st) {
 
 using namespace q36;
 
+namespace q36 {
+namespace {
+// Row-major int8 [N, K] -> the tile order: one thread per 16-byte piece of the output.
+__global__ __launch_bounds__(256) void tile_w16_kernel(const int8_t* q, int64_t N, int K, int8_t* out) {
+  const int64_t o = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16;
+  if (o >= N * K) return;
+  const int64_t piece = o >> 10;            // (row tile, column step)
+  const int l = (int)((o & 1023) >> 4);     // 16-byte lane of the piece
+  const int64_t tile = piece / (K >> 6);
+  const int step = (int)(piece % (K >> 6));
+  const int64_t row = tile * 16 + (l & 15);
+  const int col = step * 64 + 16 * (l >> 4);
+  *reinterpret_cast<v4i*>(out + o) = *reinterpret_cast<const v4i*>(q + row * K + col);
+}
+}  // namespace
+}  // namespace q36
+
+extern "C" int q36_tile_w16(const void* q, int64_t N, int32_t K, void* tiled, q36_stream_t stream) {
+  Q36_REQUIRE(q && tiled, "q36_tile_w16: null pointer");
+  Q36_REQUIRE(N >= 16 && N % 16 == 0 && K >= 64 && K % 64 == 0 && N * (int64_t)K < ((int64_t)1 << 40),
+              "q36_tile_w16: N=%lld K=%d must be multiples of 16 and 64", (long long)N, K);
+  Q36_REQUIRE(aligned16(q) && aligned16(tiled) && q != tiled, "q36_tile_w16: 16-byte aligned, distinct buffers");
+  const int64_t pieces = N * K / 16;
+  tile_w16_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const int8_t*>(q), N, K, static_cast<int8_t*>(tiled));
+  return check_launch("q36_tile_w16");
+}
+
 extern "C" int q36_dense8_linear(const q36_dense8_linear_args* a, q36_stream_t stream) {
   Q36_REQUIRE(a != nullptr, "q36_dense8_linear: null args");
   Q36_REQUIRE(a->T >= 1 && a->T <= 64, "q36_dense8_linear: T=%d must be in [1, 64]", a->T);
@@ -357,6 +389,7 @@ extern "C" int q36_dense8_linear(const q36_dense8_linear_args* a, q36_stream_t s
   d.K = a->K;
   d.x = static_cast<const uint16_t*>(a->x);
   d.q = static_cast<const int8_t*>(a->q);
+  d.tiled = a->tiled != 0;
   d.s16 = static_cast<const uint16_t*>(a->s);
   d.s_ld = a->s_ld;
   d.nseg = a->nseg;

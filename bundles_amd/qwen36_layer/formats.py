@@ -79,3 +79,15 @@ def quant_dense8(w: torch.Tensor, q=None, s=None, stream=None):
     check(_lib.lib().q36_quant_dense8(ptr(w), N, K, ptr(q), ptr(s), s.stride(0), _lib.stream_handle(stream)),
           "q36_quant_dense8")
     return q, s
+
+
+def tile_w16(q: torch.Tensor, stream=None) -> torch.Tensor:
+    """A DENSE8 copy's int8 rows [N, K] reordered into the W8A16 kernel's tile order (q36_tile_w16):
+    each 16-row x 64-column piece the kernel loads at once becomes 1 KB contiguous.  The scales keep
+    their group-major layout; glue.dense8_linear(..., tiled=True) reads the result."""
+    N, K = q.shape
+    if q.dtype != torch.int8 or not q.is_contiguous():
+        raise ValueError("tile_w16: q must be contiguous int8 [N, K]")
+    out = torch.empty_like(q)
+    check(_lib.lib().q36_tile_w16(ptr(q), N, K, ptr(out), _lib.stream_handle(stream)), "q36_tile_w16")
+    return out

@@ -114,10 +114,11 @@ def _segments(fn: str, T: int, n: int, segments):
     return segs
 
 
-def dense8_linear(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, segments=None, stream=None):
+def dense8_linear(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, segments=None, stream=None, tiled=False):
     """y = x . dequant(q, s)^T (bf16) on a DENSE8 copy (formats.quant_dense8: q int8 [N, K], s fp16
     [K/128, >= N] group-major, possibly a column block of a wider buffer), x bf16 [T, K], T <= 64.
-    segments as fp8_linear's.  The reference's decode W8A16 projections (L/dense8.py:229-265)."""
+    segments as fp8_linear's.  The reference's decode W8A16 projections (L/dense8.py:229-265).
+    tiled: q is formats.tile_w16's reordering of the copy (same bits out, 1 KB contiguous loads)."""
     T, K = x.shape
     N = q.shape[0]
     if x.dtype != torch.bfloat16 or not x.is_contiguous():
@@ -131,7 +132,7 @@ def dense8_linear(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, segments=No
     else:
         ret = None
     segs = _segments("dense8_linear", T, N, segments)
-    a = Dense8LinearArgs(T, N, K, N, ptr(x), ptr(q), ptr(s), s.stride(0), len(segments), segs)
+    a = Dense8LinearArgs(T, N, K, N, ptr(x), ptr(q), ptr(s), s.stride(0), len(segments), segs, int(bool(tiled)))
     check(_lib.lib().q36_dense8_linear(C.byref(a), _lib.stream_handle(stream)), "q36_dense8_linear")
     return ret
 

@@ -32,7 +32,7 @@ import torch
 
 from . import attn_fused, gdn_fused, moe
 from .engine import EngineView, SglangView
-from .formats import quant_dense8
+from .formats import quant_dense8, tile_w16
 from .glue import LinearWorkspace, dense8_linear, fp8_linear, linear_rows, prepare_fp8_weight
 
 HIDDEN, EXPERTS, INTERMEDIATE, TOPK = 2048, 512, 512, 10
@@ -162,6 +162,12 @@ def _install_moe(module, replica, dtype, topk, max_tokens):
 
 
 # ---- GDN mixer -----------------------------------------------------------------------------------------
+def _tiled_dense8(w: torch.Tensor):
+    """The reference's DENSE8 copy of w (L/dense8.py:168-188) with its rows tiled for the W8A16 kernel."""
+    q, s = quant_dense8(w)
+    return tile_w16(q), s
+
+
 def gdn_layer_refusal(core, norm) -> str | None:
     """Why the ring verify cannot serve this recurrent layer (None: it can): the layer half of the
     reference's served-layout check (L/gdn_fused.py:30-34), a bias-free SiLU conv and the swish-gated
@@ -206,9 +212,10 @@ class _GdnMixer:
             w_in = torch.cat([w_qkvz, w_ba], dim=0)
             self.in_proj = prepare_fp8_weight(w_in)
             self.out_proj = prepare_fp8_weight(w_out)
-            # the DENSE8 copies (int8 rows, fp16 scales per 128 columns) for the narrow batches
-            self.in8 = quant_dense8(w_in) if self.dense8_rows > 0 else None
-            self.out8 = quant_dense8(w_out.contiguous()) if self.dense8_rows > 0 else None
+            # the DENSE8 copies (int8 rows, fp16 scales per 128 columns) for the narrow batches, their rows
+            # in the W8A16 kernel's tile order (1 KB contiguous loads; the same results)
+            self.in8 = _tiled_dense8(w_in) if self.dense8_rows > 0 else None
+            self.out8 = _tiled_dense8(w_out.contiguous()) if self.dense8_rows > 0 else None
 
     def __call__(self, hidden_states, forward_batch):
         x = hidden_states
@@ -226,7 +233,7 @@ class _GdnMixer:
         segs = [(0, mixed), (GDN_QKV, z), (GDN_QKV + GDN_Z, b), (GDN_QKV + GDN_Z + GDN_HV, a)]
         dense8 = rows <= self.dense8_rows
         if dense8:
-            dense8_linear(x, *self.in8, segments=segs)
+            dense8_linear(x, *self.in8, segments=segs, tiled=True)
         else:
             fp8_linear(x, self.in_proj, sc.lin2048, segments=segs)
         p = pools
@@ -238,7 +245,7 @@ class _GdnMixer:
                                          self.scale, T=p.draft, oq=oq)
         out = torch.empty((rows, HIDDEN), **e)
         if dense8:
-            dense8_linear(core, *self.out8, segments=[(0, out)])
+            dense8_linear(core, *self.out8, segments=[(0, out)], tiled=True)
         else:
             fp8_linear(core, self.out_proj, sc.lin4096, segments=[(0, out)], xq=oq)
         return out

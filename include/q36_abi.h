@@ -375,7 +375,10 @@ int q36_fp8_linear(const q36_fp8_linear_args* a, q36_stream_t stream);
  * acc_c = fma(sum over the group's 128 columns of x * q (exact products, fp32 accumulation), s[g][n], acc_c)
  * over the chunk's groups in order; acc = the chunk sums added in chunk order.  Column
  * segments as q36_fp8_linear's (col0, ld multiples of 4, outputs 8-byte aligned).  N % 32 == 0,
- * K is 2048 or 4096 (the model's projection widths).  No workspace. */
+ * K is 2048 or 4096 (the model's projection widths).  No workspace.
+ * tiled (no reference counterpart): q is in the tile order q36_tile_w16 writes instead of row-major
+ * (the same bytes reordered so that each 16-row x 64-column piece the kernel loads is 1 KB
+ * contiguous); the results are the same bits. */
 typedef struct q36_dense8_linear_args {
   int32_t T, N, K, n_out;
   const void* x;
@@ -384,8 +387,13 @@ typedef struct q36_dense8_linear_args {
   int64_t s_ld;
   int32_t nseg;
   q36_linear_seg seg[4];
+  int32_t tiled;
 } q36_dense8_linear_args;
 int q36_dense8_linear(const q36_dense8_linear_args* a, q36_stream_t stream);
+/* Row-major int8 q [N, K] -> the W8A16 tile order (prepare time; N % 16 == 0, K % 64 == 0): the 16-row x
+ * 64-column piece (row tile i, column step j) at byte (i * K / 64 + j) * 1024, row r and columns
+ * 16 g .. 16 g + 15 of it at byte 16 (r + 16 g) of the piece. */
+int q36_tile_w16(const void* q, int64_t N, int32_t K, void* tiled, q36_stream_t stream);
 
 /* ---- Fused residual add + Gemma RMSNorm between the hybrid layer's blocks: replaces the add-norm
  * of L/proj.py:60-81 (_add_norm_kernel) and the stock fused add-RMSNorm it reproduces ----

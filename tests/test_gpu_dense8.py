@@ -100,3 +100,23 @@ def test_lmhead_w8a16_vs_oracle(mods, oracle_mod, dev, R, V, norm):
     assert np.all(rmax - picked <= np.abs(rmax) * 2 ** -7 + 1e-6), "an id's logit is below the oracle maximum"
     agree = np.mean(np_(ids) == rid)
     assert agree >= 0.9, f"ids agree on {agree:.2f} of the rows"
+
+
+@pytest.mark.parametrize("T,N,K", [(1, 12352, 2048), (16, 2048, 4096), (37, 384, 2048)])
+def test_dense8_tiled_copy_same_bits(dev, T, N, K):
+    """formats.tile_w16 is the stated permutation of the rows (checked against a torch reshape of the
+    same definition), and the linear on the tiled copy gives the row-major copy's bits."""
+    from bundles_amd.qwen36_layer import formats, glue
+    print(f"dense8 tiled T={T} N={N} K={K}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(N + T)
+    w = (torch.randn((N, K), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x = torch.randn((T, K), generator=g, device=dev).to(torch.bfloat16)
+    q, s = formats.quant_dense8(w)
+    qt = formats.tile_w16(q)
+    # piece (row tile i, column step j) at (i * K/64 + j) KB; row r, columns 16 g .. of it at 16 (r + 16 g)
+    want = q.view(N // 16, 16, K // 64, 4, 16).permute(0, 2, 3, 1, 4).contiguous().view(N, K)
+    y0 = glue.dense8_linear(x, q, s)
+    y1 = glue.dense8_linear(x, qt, s, tiled=True)
+    torch.cuda.synchronize()
+    assert torch.equal(qt, want)
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
