@@ -63,9 +63,10 @@ __host__ __device__ __forceinline__ int act_row(int r, int term, int x2) {
 }
 __host__ __device__ __forceinline__ int act_rows(int R, int x2) { return x2 ? 64 * ((R + 31) >> 5) : R; }
 
-__global__ __launch_bounds__(256) void lmh_prep_kernel(LmhDev d) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + wave;
+// one wave (and workgroup) per row: a batch's rows spread over as many CUs
+__global__ __launch_bounds__(64) void lmh_prep_kernel(LmhDev d) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x;
   if (r >= d.R) return;
   constexpr int NJ = kLH / 512;
   float y[NJ][8];
@@ -552,7 +553,7 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
            f32 ? static_cast<float*>(a->logits) : nullptr, reinterpret_cast<int8_t*>(ws + L.xq), reinterpret_cast<float*>(ws + L.xs),
            reinterpret_cast<unsigned long long*>(ws + L.keys)};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  lmh_prep_kernel<<<(a->R + 3) / 4, 256, 0, st>>>(d);
+  lmh_prep_kernel<<<a->R, 64, 0, st>>>(d);
   if (w16) {
     W16Dev g{};
     g.T = a->R;

@@ -335,9 +335,9 @@ __device__ __forceinline__ void sort_desc(uint32_t* key) {
 // winning lane.  The weights keep the oracle's arithmetic: p_j = exp(v_j - v_0) / sum in lane j,
 // their total added in pick order.
 template <int NM>
-__global__ __launch_bounds__(256) void route_topk_kernel(MoeDev d) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + wave;
+__global__ __launch_bounds__(64) void route_topk_kernel(MoeDev d) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x;  // one wave (and workgroup) per token: a batch's tokens on as many CUs
   if (t >= d.M) return;
   const int E = d.E, k = d.k, nm = E / 64;
   const bool valid = d.pos == nullptr || d.pos[t] != 0;
@@ -1324,9 +1324,9 @@ int launch_route(const MoeDev& d, int dtype, hipStream_t st) {
   else
     route_logits_kernel<Q36_MOE_INT8><<<n_router + d.M, 256, 0, st>>>(d, n_router);
   if (d.E <= 512)
-    route_topk_kernel<8><<<(d.M + 3) / 4, 256, 0, st>>>(d);
+    route_topk_kernel<8><<<d.M, 64, 0, st>>>(d);
   else
-    route_topk_kernel<16><<<(d.M + 3) / 4, 256, 0, st>>>(d);
+    route_topk_kernel<16><<<d.M, 64, 0, st>>>(d);
   return check_launch("q36_moe_route");
 }
 int launch_lists(const MoeDev& d, hipStream_t st) {

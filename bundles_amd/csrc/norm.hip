@@ -6,7 +6,8 @@
 // chunks l + 64 j, fma from zero, then an xor butterfly 32..1) so that the CPU oracle gives the
 // same bits, and rsqrt is the correctly rounded 1 / sqrt.
 //
-// Kernel: one wave per row, four rows per workgroup; a row is 2048 bf16 = 4 chunks of 8 per lane.
+// Kernel: one wave per row, one row per workgroup (a workgroup per row spreads a decode batch's
+// few hundred rows over as many CUs); a row is 2048 bf16 = 4 chunks of 8 per lane.
 // Optionally the normed row also leaves as e4m3 codes per 128-channel group (the next projection's
 // input, so that projection skips its own quantization launch): a group is 16 neighbouring lanes.
 #include "q36_device.h"
@@ -29,9 +30,9 @@ struct NormDev {
   int frag;
 };
 
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormDev d) {
+__global__ __launch_bounds__(64) void add_rmsnorm_kernel(NormDev d) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + wave;
+  const int r = blockIdx.x * (blockDim.x >> 6) + wave;
   if (r >= d.T) {
     // fragment order pads the tokens to a multiple of 16: zero codes and scales
     if (d.q8 && d.frag && r < (d.T + 15) / 16 * 16) {
@@ -123,6 +124,6 @@ extern "C" int q36_add_rmsnorm(const q36_add_norm_args* a, q36_stream_t stream) 
             static_cast<const uint16_t*>(a->norm_w), a->eps, static_cast<uint16_t*>(a->out),
             static_cast<uint8_t*>(a->q8), a->q8s, a->q8_frag != 0};
   const int rows = a->q8 && a->q8_frag ? (a->T + 15) / 16 * 16 : a->T;
-  add_rmsnorm_kernel<<<(rows + 3) / 4, 256, 0, static_cast<hipStream_t>(stream)>>>(d);
+  add_rmsnorm_kernel<<<rows, 64, 0, static_cast<hipStream_t>(stream)>>>(d);
   return check_launch("q36_add_rmsnorm");
 }
