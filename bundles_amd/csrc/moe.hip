@@ -110,12 +110,14 @@ __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
 // ------------------------------------------------------------------------------------------
 // 1. router logits + activation quantization
 // ------------------------------------------------------------------------------------------
-// Router workgroup = 8 tokens x 8 experts; wave w owns experts e0, e0 + 1.  The x tile is staged in
-// LDS; lane l keeps the 8-element chunks c = l + 64 j (j < H/512) of its 2 expert rows in registers
-// and accumulates every (token, expert) dot with fma in (j, i) order.  The 64 lane partials of each
-// output then meet in a recursive-halving reduce-scatter (xor 32 .. 4, then xor-2 and xor-1 adds):
-// every sum pairs the same two operands as the xor butterfly (offsets 32 .. 1) of q36o_dot_canon,
-// so the logits are bit-identical to the oracle's.
+// Router workgroup = TT tokens x 4 EPW experts; wave w owns experts e0 .. e0 + EPW - 1.  The x tile
+// is staged in LDS as fp32 (each bf16 unpacked once, when the tile is filled, instead of once per
+// wave and expert group); lane l keeps the 8-element chunks c = l + 64 j (j < H/512) of its EPW expert
+// rows in registers and accumulates every (token, expert) dot with fma in (j, i) order.  The 64 lane
+// partials of each output then meet in a recursive-halving reduce-scatter (xor 32, 16, ... over the
+// NO = TT EPW outputs), then the xor butterfly's remaining stages: every sum pairs the same two
+// operands as the xor butterfly (offsets 32 .. 1) of q36o_dot_canon, so the logits are
+// bit-identical to the oracle's.
 // One reduce-scatter stage over N values: lanes whose bit O is set keep the upper half.
 template <int N, int O>
 __device__ __forceinline__ void rs_stage(float* v, int lane) {
@@ -127,77 +129,85 @@ __device__ __forceinline__ void rs_stage(float* v, int lane) {
     v[i] = keep + __shfl_xor(send, O);
   }
 }
-constexpr int kRouteTT = 8;   // tokens per router workgroup
-constexpr int kRouteEPW = 2;  // experts per wave: each unpacked activation serves both
-constexpr int kRouteEW = 4 * kRouteEPW;  // experts per router workgroup
+// Stages xor O, O / 2, ... until one value is left: lane l then holds output (l / (64 / N)) % N
+// (its bits above log2(64 / N)), summed over the lanes that share those bits.
+template <int N, int O>
+__device__ __forceinline__ void rs_all(float* v, int lane) {
+  if constexpr (N > 1) {
+    rs_stage<N, O>(v, lane);
+    rs_all<N / 2, O / 2>(v, lane);
+  }
+}
 constexpr int kRouteH = 2048;
-template <int DT>
+// Router shapes (tokens x experts a wave): TT = 8, EPW = 4 from 5 tokens on (one workgroup a CU at
+// batch 64: each unpacked activation feeds 4 experts); fewer tokens use TT = 1, 2 or 4 with EPW = 2
+// (64 workgroups a token group: the GEMV spread over more CUs, and no wave computes a padding
+// token's copy of another token).
+__host__ __device__ constexpr int route_tt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+__host__ __device__ constexpr int route_epw(int tt) { return tt == 8 ? 4 : 2; }
+template <int DT, int TT, int EPW>
 __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_router_wg) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int bid = blockIdx.x;
+  constexpr int EW = 4 * EPW;  // experts a workgroup
+  __shared__ float4 xlo[TT][kRouteH / 8], xhi[TT][kRouteH / 8];  // elements 0-3 / 4-7 of each chunk
   if (bid < n_router_wg) {
-    // Router workgroup = 8 tokens x 8 experts, two per wave: the router GEMV is VALU work in the
-    // canonical order (the bf16 unpacking of the activations its largest part), so each unpacked
-    // element feeds two experts, and the work is still spread over every SIMD of the chip
     constexpr int NJ = kRouteH / 512;
-    constexpr int NO = kRouteTT * kRouteEPW;  // outputs per wave: (expert, token) pairs
-    __shared__ v4i xt[kRouteTT][kRouteH / 8];
-    const int neg = d.E / kRouteEW;
+    constexpr int NO = TT * EPW;  // outputs per wave: (expert, token) pairs
+    static_assert(NO >= 2 && NO <= 64 && (NO & (NO - 1)) == 0, "outputs per wave: a power of two, 2 .. 64");
+    constexpr int S = __builtin_ctz(NO);  // reduce-scatter stages
+    const int neg = d.E / EW;
     const int eg = bid % neg, tg = bid / neg;
-    const int e0 = eg * kRouteEW + wave * kRouteEPW;
-    const int t0 = tg * kRouteTT;
-    v4i w[kRouteEPW][NJ];
+    const int e0 = eg * EW + wave * EPW;
+    const int t0 = tg * TT;
+    v4i w[EPW][NJ];
 #pragma unroll
-    for (int x = 0; x < kRouteEPW; ++x)
+    for (int x = 0; x < EPW; ++x)
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
         w[x][j] = ldg16(reinterpret_cast<const uint8_t*>(d.wr + (size_t)(e0 + x) * kRouteH + 8 * (lane + 64 * j)));
 #pragma unroll
-    for (int r = 0; r < kRouteTT * kRouteH / 8 / 256; ++r) {
-      const int c = threadIdx.x + 256 * r;
-      const int t = c / (kRouteH / 8), cc = c % (kRouteH / 8);
+    for (int t = 0; t < TT; ++t) {
       const int tok = min(t0 + t, d.M - 1);
-      xt[t][cc] = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)tok * kRouteH + 8 * cc));
+      const v4i xv = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)tok * kRouteH + 8 * threadIdx.x));
+      xlo[t][threadIdx.x] = make_float4(bf_lo((uint32_t)xv[0]), bf_hi((uint32_t)xv[0]), bf_lo((uint32_t)xv[1]),
+                                        bf_hi((uint32_t)xv[1]));
+      xhi[t][threadIdx.x] = make_float4(bf_lo((uint32_t)xv[2]), bf_hi((uint32_t)xv[2]), bf_lo((uint32_t)xv[3]),
+                                        bf_hi((uint32_t)xv[3]));
     }
     __syncthreads();
-    float v[NO];  // output o = x * kRouteTT + t
+    float v[NO];  // output o = x * TT + t
 #pragma unroll
     for (int i = 0; i < NO; ++i) v[i] = 0.f;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
+    for (int j = 0; j < NJ; ++j) {
+      float wf[EPW][8];
 #pragma unroll
-      for (int t = 0; t < kRouteTT; ++t) {
-        const v4i xv = xt[t][lane + 64 * j];
-        float xf[8];
+      for (int x = 0; x < EPW; ++x)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          xf[2 * q] = bf_lo((uint32_t)xv[q]);
-          xf[2 * q + 1] = bf_hi((uint32_t)xv[q]);
+          wf[x][2 * q] = bf_lo((uint32_t)w[x][j][q]);
+          wf[x][2 * q + 1] = bf_hi((uint32_t)w[x][j][q]);
         }
 #pragma unroll
-        for (int x = 0; x < kRouteEPW; ++x) {
-          float a = v[x * kRouteTT + t];
+      for (int t = 0; t < TT; ++t) {
+        const float4 lo = xlo[t][lane + 64 * j], hi = xhi[t][lane + 64 * j];
+        const float xf[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            a = __builtin_fmaf(xf[2 * q], bf_lo((uint32_t)w[x][j][q]), a);
-            a = __builtin_fmaf(xf[2 * q + 1], bf_hi((uint32_t)w[x][j][q]), a);
-          }
-          v[x * kRouteTT + t] = a;
+        for (int x = 0; x < EPW; ++x) {
+          float a = v[x * TT + t];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) a = __builtin_fmaf(xf[i], wf[x][i], a);
+          v[x * TT + t] = a;
         }
       }
-    // reduce-scatter over xor 32, 16, 8, 4 (a lane keeps the half of its outputs whose index bit
-    // matches its lane bit: output (lane >> 2) & 15 after four stages), then the butterfly's last
-    // two stages (xor 2, 1) among the four lanes that hold the output
-    static_assert(NO == 16, "the stage list below assumes 16 outputs per wave");
-    rs_stage<16, 32>(v, lane);
-    rs_stage<8, 16>(v, lane);
-    rs_stage<4, 8>(v, lane);
-    rs_stage<2, 4>(v, lane);
+    }
+    rs_all<NO, 32>(v, lane);
     float tot = v[0];
-    tot = tot + __shfl_xor(tot, 2);
-    tot = tot + __shfl_xor(tot, 1);
-    const int o = (lane >> 2) & 15, t = o % kRouteTT, e = e0 + o / kRouteTT;
-    if ((lane & 3) == 0 && t0 + t < d.M) {
+#pragma unroll
+    for (int o = 32 >> S; o >= 1; o >>= 1) tot = tot + __shfl_xor(tot, o);
+    const int o = (lane >> (6 - S)) & (NO - 1), t = o % TT, e = e0 + o / TT;
+    if ((lane & ((64 >> S) - 1)) == 0 && t0 + t < d.M) {
       if (d.bias) tot = tot + d.bias[e];
       d.logits[(size_t)(t0 + t) * d.E + e] = rbf(tot);
     }
@@ -1318,11 +1328,19 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
 // Raise a kernel's dynamic-LDS limit (once per device and kernel) when a launch needs more than
 // the 64 KiB default; gfx950 has 160 KiB per CU.
 int launch_route(const MoeDev& d, int dtype, hipStream_t st) {
-  const int n_router = (d.E / kRouteEW) * ((d.M + kRouteTT - 1) / kRouteTT);
-  if (dtype == Q36_MOE_FP8)
-    route_logits_kernel<Q36_MOE_FP8><<<n_router + d.M, 256, 0, st>>>(d, n_router);
-  else
-    route_logits_kernel<Q36_MOE_INT8><<<n_router + d.M, 256, 0, st>>>(d, n_router);
+  const int tt = route_tt(d.M), n_router = (d.E / (4 * route_epw(tt))) * ((d.M + tt - 1) / tt);
+  auto go = [&](auto dt, auto tt_c) {
+    constexpr int DT = decltype(dt)::value, TT = decltype(tt_c)::value;
+    route_logits_kernel<DT, TT, route_epw(TT)><<<n_router + d.M, 256, 0, st>>>(d, n_router);
+  };
+  auto go_tt = [&](auto dt) {
+    if (tt == 1) go(dt, std::integral_constant<int, 1>{});
+    else if (tt == 2) go(dt, std::integral_constant<int, 2>{});
+    else if (tt == 4) go(dt, std::integral_constant<int, 4>{});
+    else go(dt, std::integral_constant<int, 8>{});
+  };
+  if (dtype == Q36_MOE_FP8) go_tt(std::integral_constant<int, Q36_MOE_FP8>{});
+  else go_tt(std::integral_constant<int, Q36_MOE_INT8>{});
   if (d.E <= 512)
     route_topk_kernel<8><<<d.M, 64, 0, st>>>(d);
   else
@@ -1338,11 +1356,13 @@ int launch_lists(const MoeDev& d, hipStream_t st) {
 }
 
 // Expert-kernel grid: 8 workgroups per work item: the shared expert's 1 + nsh blocks, and room for
-// every routed block (one per active expert, at most E, and the further ones: an expert past 64
-// tokens only when M > 64, at most M k / 64 of them, fewer than E, so the list holds 2E)
+// every routed block (one per active expert, at most min(E, M k) of them, and the further ones: an
+// expert past 64 tokens only when M > 64, at most M k / 64 of them, fewer than E, so the list holds
+// 2E).  A decode batch of a few rows launches only as many workgroups as its picks can keep busy.
 int expert_grid(const MoeDev& d) {
   const int nrb = d.M > kTokBlock ? d.M * d.k / kTokBlock : 0;
-  return 8 * (d.E + 1 + d.nsh + nrb);
+  const int picks = d.M * d.k < d.E ? d.M * d.k : d.E;
+  return 8 * (picks + 1 + d.nsh + nrb);
 }
 template <int DT>
 int launch_up_t(const MoeDev& d, hipStream_t st) {
