@@ -818,7 +818,10 @@ extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
   // 144-row x 32-token workgroups, 3 row groups x 4 K quarters (12 waves): 256 workgroups at 128
   // tokens, 17.9 us per graph-timed call against 19.2 us for the streaming GEMM (128 x 32 tiles, 288
   // workgroups).  Both move about 90 MB through L2 per call (the token groups re-read the weights, the
-  // row blocks the activations), which at ~18 TB/s across the chip is what bounds them.
+  // row blocks the activations), which at ~18 TB/s across the chip is what bounds them.  (norm_rope
+  // fused into the K-sliced GEMM's epilogue, which needs one 256-row head per workgroup: 144
+  // workgroups of 256 rows x 32 tokens, or 288 of 16 tokens, measured 14.1-22.1 us for the fused call
+  // against 13.4 us for the GEMM and norm_rope at 128 tokens with prequantized rows.)
   if (a->T >= kTileMinT)
     launch_tile<16>(g, st);
   else if (ks)
