@@ -139,12 +139,13 @@ __device__ __forceinline__ void rs_all(float* v, int lane) {
   }
 }
 constexpr int kRouteH = 2048;
-// Router shapes (tokens x experts a wave): TT = 8, EPW = 4 from 5 tokens on (one workgroup a CU at
-// batch 64: each unpacked activation feeds 4 experts); fewer tokens use TT = 1, 2 or 4 with EPW = 2
-// (64 workgroups a token group: the GEMV spread over more CUs, and no wave computes a padding
-// token's copy of another token).
-__host__ __device__ constexpr int route_tt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
-__host__ __device__ constexpr int route_epw(int tt) { return tt == 8 ? 4 : 2; }
+// Router shapes, TT tokens x EPW experts a wave, by batch: one token group per 1 or 2 tokens, groups
+// of 4 up to 16 tokens and of 8 up to 32 with EPW = 2 (64 workgroups a token group: the GEMV spread
+// over many CUs, no wave computing a padding token's copy of another token), and from 33 tokens on
+// TT = 8, EPW = 4 (each unpacked activation feeds 4 experts; one workgroup a CU at batch 64).
+constexpr int kRouteT4Max = 16, kRouteE2Max = 32;
+__host__ __device__ constexpr int route_tt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= kRouteT4Max ? 4 : 8; }
+__host__ __device__ constexpr int route_epw(int M) { return M <= kRouteE2Max ? 2 : 4; }
 template <int DT, int TT, int EPW>
 __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_router_wg) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1328,16 +1329,21 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
 // Raise a kernel's dynamic-LDS limit (once per device and kernel) when a launch needs more than
 // the 64 KiB default; gfx950 has 160 KiB per CU.
 int launch_route(const MoeDev& d, int dtype, hipStream_t st) {
-  const int tt = route_tt(d.M), n_router = (d.E / (4 * route_epw(tt))) * ((d.M + tt - 1) / tt);
-  auto go = [&](auto dt, auto tt_c) {
-    constexpr int DT = decltype(dt)::value, TT = decltype(tt_c)::value;
-    route_logits_kernel<DT, TT, route_epw(TT)><<<n_router + d.M, 256, 0, st>>>(d, n_router);
+  const int tt = route_tt(d.M), epw = route_epw(d.M), n_router = (d.E / (4 * epw)) * ((d.M + tt - 1) / tt);
+  auto go = [&](auto dt, auto tt_c, auto epw_c) {
+    constexpr int DT = decltype(dt)::value, TT = decltype(tt_c)::value, EPW = decltype(epw_c)::value;
+    route_logits_kernel<DT, TT, EPW><<<n_router + d.M, 256, 0, st>>>(d, n_router);
   };
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I4 = std::integral_constant<int, 4>;
+  using I8 = std::integral_constant<int, 8>;
   auto go_tt = [&](auto dt) {
-    if (tt == 1) go(dt, std::integral_constant<int, 1>{});
-    else if (tt == 2) go(dt, std::integral_constant<int, 2>{});
-    else if (tt == 4) go(dt, std::integral_constant<int, 4>{});
-    else go(dt, std::integral_constant<int, 8>{});
+    if (tt == 1) go(dt, I1{}, I2{});
+    else if (tt == 2) go(dt, I2{}, I2{});
+    else if (tt == 4) go(dt, I4{}, I2{});
+    else if (epw == 2) go(dt, I8{}, I2{});
+    else go(dt, I8{}, I4{});
   };
   if (dtype == Q36_MOE_FP8) go_tt(std::integral_constant<int, Q36_MOE_FP8>{});
   else go_tt(std::integral_constant<int, Q36_MOE_INT8>{});
