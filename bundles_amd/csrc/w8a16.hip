@@ -272,7 +272,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8a16_kernel(W16Dev d) {
 
 // The launch shape: token tiles NTT (T <= 16 NTT), row tiles per wave RT, K split KS, waves per
 // workgroup WAVES.  Every shape the policy can pick is instantiated here.
-#define Q36_W16_SHAPES_0(X) X(1, 2, 1, 4) X(2, 2, 1, 4) X(4, 2, 1, 4)
+#define Q36_W16_SHAPES_0(X) X(1, 2, 1, 4) X(1, 4, 1, 2) X(2, 4, 1, 2) X(4, 2, 1, 4)
 #define Q36_W16_SHAPES_1(X) \
   X(1, 2, 4, 8) X(2, 2, 4, 8) X(4, 2, 4, 8) \
   X(1, 1, 8, 8) X(2, 1, 8, 8) X(4, 1, 8, 8)
@@ -281,12 +281,16 @@ struct W16Shape {
   int ntt, rt, ks, waves;
 };
 
-// Measured on MI355X over T = 4..64: the lm_head (N in the 100 000s) streams whole rows, 32 a wave;
-// the projections split K so that every CU has waves: in quarters for the 9216- and 12352-row
+// Measured on MI355X over T = 4..64: the lm_head (N in the 100 000s) streams whole rows, 32 a wave in
+// four-wave workgroups up to 8 tokens; from 9 tokens on 64 a wave in two-wave workgroups, so each
+// activation fragment a wave reads from L2 serves twice the weight rows (16 tokens 95 -> 90 us, 32
+// tokens 125 -> 115 us; at 1-4 tokens the wider waves leave too few loads in flight: 77 -> 84 us).
+// The projections split K so that every CU has waves: in quarters for the 9216- and 12352-row
 // in_proj / qkv, in eighths for the 2048-row o_proj / out_proj.
 W16Shape w16_shape(const W16Dev& d, int mode) {
   const int ntt = d.T <= 16 ? 1 : d.T <= 32 ? 2 : 4;
-  if (mode == 0) return {ntt, 2, 1, 4};
+  // (the wider waves need N % 64 == 0: a wave's rows are all in or all out)
+  if (mode == 0) return ntt == 4 || d.T <= 8 || d.N % 64 != 0 ? W16Shape{ntt, 2, 1, 4} : W16Shape{ntt, 4, 1, 2};
   return d.N >= 8192 ? W16Shape{ntt, 2, 4, 8} : W16Shape{ntt, 1, 8, 8};
 }
 
