@@ -59,7 +59,7 @@ class AttnArgs(C.Structure):
     _fields_ = [("T", I32), ("max_pos", I32), ("x", P), ("wqkv", P), ("sqkv", P), ("q_norm_w", P),
                 ("k_norm_w", P), ("eps", C.c_float), ("cos_sin", P), ("positions", P), ("q", P), ("gate", P),
                 ("k", P), ("v", P), ("k8", P), ("v8", P), ("workspace", P), ("workspace_bytes", SZ),
-                ("xq", P), ("xqs", P)]
+                ("xq", P), ("xqs", P), ("out_loc", P), ("k_cache", P), ("v_cache", P), ("num_slots", C.c_int64)]
 
 
 class OprojArgs(C.Structure):

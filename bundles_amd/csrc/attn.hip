@@ -598,6 +598,10 @@ struct RopeDev {
   uint16_t* v;
   uint8_t* k8;
   uint8_t* v8;
+  const int64_t* out_loc;  // the cache append (optional): row out_loc[t] of kc / vc
+  uint8_t* kc;
+  uint8_t* vc;
+  int64_t num_slots;
 };
 constexpr int kRopeItems = 18;  // waves per token
 __global__ __launch_bounds__(256) void norm_rope_kernel(RopeDev d) {
@@ -667,6 +671,11 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(RopeDev d) {
     e8.x = f2e4m3x2_hw(x[0], x[1]) | (f2e4m3x2_hw(x[2], x[3]) << 16);
     e8.y = f2e4m3x2_hw(x[4], x[5]) | (f2e4m3x2_hw(x[6], x[7]) << 16);
     *reinterpret_cast<uint2*>((normed ? d.k8 : d.v8) + o) = e8;
+    if (d.out_loc) {
+      const int64_t slot = d.out_loc[t];
+      if (slot >= 0 && slot < d.num_slots)
+        *reinterpret_cast<uint2*>((normed ? d.kc : d.vc) + ((size_t)slot * 2 + hh) * 256 + 8 * j) = e8;
+    }
   }
 }
 
@@ -797,6 +806,12 @@ extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
                   (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0,
               "q36_attn_proj: x, wqkv, the norm weights, cos_sin, q, gate, k, v must be 16-byte, k8 and v8 8-byte "
               "and workspace 256-byte aligned");
+  Q36_REQUIRE(!a->out_loc || (a->k_cache && a->v_cache && a->num_slots >= 1 &&
+                               a->num_slots * 2 * 256 < ((int64_t)1 << 40) &&
+                               (reinterpret_cast<uintptr_t>(a->k_cache) & 7u) == 0 &&
+                               (reinterpret_cast<uintptr_t>(a->v_cache) & 7u) == 0),
+              "q36_attn_proj: out_loc needs k_cache and v_cache (8-byte aligned) and num_slots >= 1 (got %lld)",
+              (long long)a->num_slots);
   const AttnWs L = attn_ws(a->T);
   Q36_REQUIRE(a->workspace_bytes >= L.total, "q36_attn_proj: workspace of %zu bytes < %zu required",
               a->workspace_bytes, L.total);
@@ -831,7 +846,8 @@ extern "C" int q36_attn_proj(const q36_attn_args* a, q36_stream_t stream) {
   RopeDev r{a->T, a->max_pos, qkv, static_cast<const uint16_t*>(a->q_norm_w),
             static_cast<const uint16_t*>(a->k_norm_w), a->eps, a->cos_sin, a->positions,
             static_cast<uint16_t*>(a->q), static_cast<uint16_t*>(a->gate), static_cast<uint16_t*>(a->k),
-            static_cast<uint16_t*>(a->v), static_cast<uint8_t*>(a->k8), static_cast<uint8_t*>(a->v8)};
+            static_cast<uint16_t*>(a->v), static_cast<uint8_t*>(a->k8), static_cast<uint8_t*>(a->v8),
+            a->out_loc, static_cast<uint8_t*>(a->k_cache), static_cast<uint8_t*>(a->v_cache), a->num_slots};
   norm_rope_kernel<<<(a->T * kRopeItems + 3) / 4, 256, 0, st>>>(r);
   return check_launch("q36_attn_proj");
 }

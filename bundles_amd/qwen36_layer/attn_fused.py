@@ -90,10 +90,13 @@ class Workspace:
 
 
 def attn_proj(x, w: AttnWeights, q_norm_w, k_norm_w, eps, cos_sin, positions, ws: Workspace, out=None, stream=None,
-              xq: QuantRows | None = None):
+              xq: QuantRows | None = None, cache=None):
     """Returns dict(q, gate, k, v, k8, v8) for tokens x bf16 [T, 2048].  xq: the rows already quantized
     by their producer (proj_rows); x is then not read (may be None) and the projection skips its own
-    quantization launch, with the same output bits."""
+    quantization launch, with the same output bits.  cache = (k_cache, v_cache, out_loc): the new
+    tokens' e4m3 K / V rows also go into the cache (e4m3 codes, uint8 [slots, 2, 256]) at slots out_loc
+    (int64 [T]; slots outside the cache are skipped), as the reference's verify step writes them
+    (L/qk_attn_verify.cu:431-465); attn_decode then needs no out_loc."""
     T = x.shape[0] if x is not None else xq.T
     if xq is not None and (xq.T != T or xq.frag != bool(_lib.lib().q36_attn_act_frag(T))):
         raise ValueError("attn_proj: xq was not made for this token count (proj_rows)")
@@ -106,10 +109,23 @@ def attn_proj(x, w: AttnWeights, q_norm_w, k_norm_w, eps, cos_sin, positions, ws
                     v=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=dev),
                     k8=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.uint8, device=dev),
                     v8=torch.empty((T, N_KV_HEADS, HEAD_DIM), dtype=torch.uint8, device=dev))
+    kc = vc = loc = None
+    slots = 0
+    if cache is not None:
+        kc, vc, loc = cache
+        for name, t in (("k_cache", kc), ("v_cache", vc)):
+            if t.dtype != torch.uint8 or not t.is_contiguous() or t.dim() != 3 or tuple(t.shape[1:]) != (N_KV_HEADS,
+                                                                                                      HEAD_DIM):
+                raise ValueError(f"attn_proj: {name} must be contiguous uint8 [slots, {N_KV_HEADS}, {HEAD_DIM}]")
+        if kc.shape != vc.shape:
+            raise ValueError("attn_proj: k_cache and v_cache differ in shape")
+        if loc.dtype != torch.int64 or not loc.is_contiguous() or loc.numel() < T:
+            raise ValueError(f"attn_proj: out_loc must be contiguous int64 with at least {T} entries")
+        slots = kc.shape[0]
     a = AttnArgs(T, cos_sin.shape[0], ptr(x), ptr(w.wqkv_p), ptr(w.sqkv), ptr(q_norm_w), ptr(k_norm_w), eps,
                  ptr(cos_sin), ptr(positions), ptr(o["q"]), ptr(o["gate"]), ptr(o["k"]), ptr(o["v"]), ptr(o["k8"]),
                  ptr(o["v8"]), ptr(ws.proj), ws.proj.numel(), ptr(None if xq is None else xq.codes),
-                 ptr(None if xq is None else xq.scales))
+                 ptr(None if xq is None else xq.scales), ptr(loc), ptr(kc), ptr(vc), slots)
     check(_lib.lib().q36_attn_proj(C.byref(a), _lib.stream_handle(stream)), "q36_attn_proj")
     return o
 

@@ -265,14 +265,16 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
             gi += 1
         else:
             a = L.mixer
+            # the new tokens' K / V rows go into the cache in the projection's norm / RoPE step
             p = attn_fused.attn_proj(h, a.w, a.q_norm_w, a.k_norm_w, w.eps, st.cos_sin, st.positions, ws.attn,
-                                     out=b["attn"], stream=stream, xq=rows_for(i))
+                                     out=b["attn"], stream=stream, xq=rows_for(i),
+                                     cache=(st.k_cache, st.v_cache, st.out_loc))
             oq = ws.q8_o if ws.prequant else None
             for k in ("q", "gate", "k8", "v8"):
                 keep(f"L{i}.{k}", p[k])
             attn_fused.attn_decode(p["q"], st.k_cache, st.v_cache, st.page_table, st.seqlens, st.T, ATTN_SCALE,
-                                   ws.decode, out_loc=st.out_loc, k_new=p["k8"], v_new=p["v8"], out=b["attn_out"],
-                                   stream=stream, gate=p["gate"].view(M, 4096) if oq is not None else None, oq=oq)
+                                   ws.decode, out=b["attn_out"], stream=stream,
+                                   gate=p["gate"].view(M, 4096) if oq is not None else None, oq=oq)
             keep(f"L{i}.attn", b["attn_out"])
             attn_fused.attn_oproj(b["attn_out"].view(M, 4096), p["gate"].view(M, 4096), a.w, ws.attn, out=b["o"],
                                   stream=stream, aq=oq)

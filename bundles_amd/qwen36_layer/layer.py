@@ -286,8 +286,8 @@ def attn_layer_refusal(module) -> str | None:
 
 class _AttnMixer:
     """The gated attention mixer's target-verify step: q36_attn_proj (q/gate/k/v, q/k norm, partial
-    RoPE, e4m3 K/V rows), q36_attn_decode over the engine's KV cache (the new rows written first), and
-    q36_attn_oproj (sigmoid gate, o_proj)."""
+    RoPE, the new e4m3 K/V rows written into the engine's KV cache at out_cache_loc), q36_attn_decode
+    over that cache, and q36_attn_oproj (sigmoid gate, o_proj)."""
 
     def __init__(self, module, replica, engine: EngineView, max_tokens: int):
         w_qkv, w_o = module.qkv_proj.weight, module.o_proj.weight
@@ -328,12 +328,12 @@ class _AttnMixer:
         sc = _Scratch.get(x.device, rows)
         pos = positions.to(torch.int32).contiguous()
         p = attn_fused.attn_proj(x.contiguous(), self.w, self.q_norm_w, self.k_norm_w, self.eps, self.cos_sin, pos,
-                                 sc.attn)
+                                 sc.attn, cache=(kv.k_cache, kv.v_cache, kv.out_loc.to(torch.int64).contiguous()))
         # the o_proj's e4m3 input comes from the attention's epilogue (same bits as quantizing o * sigmoid(gate))
         aq = attn_fused.oproj_rows(rows, x.device)
         gate = p["gate"].view(rows, -1)
         o = attn_fused.attn_decode(p["q"], kv.k_cache, kv.v_cache, kv.page_table, kv.seqlens, kv.draft, self.scale,
-                                   sc.decode, out_loc=kv.out_loc, k_new=p["k8"], v_new=p["v8"], gate=gate, oq=aq)
+                                   sc.decode, gate=gate, oq=aq)
         return attn_fused.attn_oproj(o.view(rows, -1), gate, self.w, sc.attn, aq=aq)
 
 

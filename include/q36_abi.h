@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define Q36_ABI_VERSION 4
+#define Q36_ABI_VERSION 5
 #define Q36_OK 0
 #define Q36_EINVAL 1
 #define Q36_ELAUNCH 2
@@ -278,8 +278,8 @@ int q36_gdn_verify_ring(const q36_gdn_ring_args* a, q36_stream_t stream);
  *   q36_attn_oproj: out bf16 [T, 2048] = (bf16(attn * sigmoid(gate)) in e4m3) . wo^T with
  *     attn, gate bf16 [T, 4096], wo e4m3 [2048, 4096] in fragment order, so fp32 [16, 32]
  *     (L/qk_attn_verify.cu:730-737).
- * Alignment: x, wqkv, attn, gate, wo, the norm weights, cos_sin and q, gate, k, v 16 bytes; k8, v8
- * 8 bytes.
+ * Alignment: x, wqkv, attn, gate, wo, the norm weights, cos_sin and q, gate, k, v 16 bytes; k8, v8,
+ * k_cache, v_cache 8 bytes.
  * Workspaces: q36_attn_workspace_bytes(T), q36_oproj_workspace_bytes(T), 256-byte aligned.
  * Activations quantized by their producer (no reference counterpart: the quantization folded into the
  * kernel that writes the rows, so these entries skip their own act_quant launch):
@@ -312,6 +312,14 @@ typedef struct q36_attn_args {
   size_t workspace_bytes;
   const void* xq;  /* optional producer-quantized x (see above) */
   const float* xqs;
+  /* optional cache append: with out_loc set, the new tokens' e4m3 K and V rows (k8 / v8's bytes) are
+   * also written to row out_loc[t] (int64 [T]) of k_cache / v_cache e4m3 [num_slots, 2, 256]; a slot
+   * outside [0, num_slots) is skipped.  The reference writes the cache in the same step
+   * (L/qk_attn_verify.cu:431-465, :774-797); q36_attn_decode's out_loc then is not needed. */
+  const int64_t* out_loc;
+  void* k_cache;
+  void* v_cache;
+  int64_t num_slots;
 } q36_attn_args;
 typedef struct q36_oproj_args {
   int32_t T;

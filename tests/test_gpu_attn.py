@@ -34,6 +34,40 @@ def _oracle_weights(w):
     return dict(wqg=q[:8192], sqg=s[:64], wk=q[8192:8704], sk=s[64:68], wv=q[8704:], sv=s[68:72])
 
 
+@pytest.mark.parametrize("T", [1, 37, 128])
+def test_attn_proj_cache_append(attn, dev, T):
+    """cache=(k_cache, v_cache, out_loc): the new tokens' K / V codes land in their slots, the same bytes
+    as k8 / v8 (and as q36_attn_decode's out_loc would write); slots outside the cache are skipped and
+    every other row is untouched; q, gate, k, v are the same bits as without the cache."""
+    print(f"attn_proj cache append T={T}", flush=True)
+    d, w = _setup(attn, dev, T, seed=40 + T)
+    ws = attn.Workspace(T, dev)
+    slots = 3 * T + 5
+    g = torch.Generator(device="cpu").manual_seed(T)
+    kc = torch.randint(0, 256, (slots, 2, 256), generator=g, dtype=torch.uint8).to(dev)
+    vc = torch.randint(0, 256, (slots, 2, 256), generator=g, dtype=torch.uint8).to(dev)
+    kc0, vc0 = kc.clone(), vc.clone()
+    loc = torch.randperm(slots, generator=g)[:T].to(torch.int64)
+    if T > 1:
+        loc[1] = slots      # past the cache: skipped
+        loc[-1] = -1        # padding: skipped
+    ref = attn.attn_proj(d["x"], w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"], ws)
+    ref = {k: v.clone() for k, v in ref.items()}
+    o = attn.attn_proj(d["x"], w, d["q_norm_w"], d["k_norm_w"], 1e-6, d["cos_sin"], d["positions"], ws,
+                       cache=(kc, vc, loc.to(dev)))
+    torch.cuda.synchronize()
+    for key in ("q", "gate", "k", "v", "k8", "v8"):
+        assert torch.equal(o[key], ref[key]), f"{key} changed with the cache append"
+    ek, ev = kc0.clone(), vc0.clone()
+    for t in range(T):
+        s_ = int(loc[t])
+        if 0 <= s_ < slots:
+            ek[s_] = ref["k8"][t]
+            ev[s_] = ref["v8"][t]
+    assert torch.equal(kc, ek), "k_cache differs from the expected rows"
+    assert torch.equal(vc, ev), "v_cache differs from the expected rows"
+
+
 @pytest.mark.parametrize("T", [1, 37, 128, 256])
 def test_attn_proj_parity(attn, oracle_mod, dev, T):
     O = oracle_mod
