@@ -70,8 +70,9 @@ struct MoeDev {
   int32_t* active;
   int32_t* ctl;
   int32_t* ecount;  // tokens per expert, counted by route_topk (zeroed by route_logits)
-  int32_t* eact;    // [2E] routed work items e | j << 16 (token block j of expert e), in the order
-                    // route_topk opened them; ctl[2] counts them
+  int32_t* eact;    // routed work items e | j << 16 (token block j of expert e), in the order
+                    // route_topk opened them: [0, E) experts' first blocks (ctl[2] counts them),
+                    // [E, 2E) their further blocks, past 64 tokens (ctl[3])
   int32_t* elist;   // [E][M] slots of each expert, in the order route_topk met them
   int nsh;          // the shared expert's token blocks past its first: ceil(M / kTokBlock) - 1
   uint8_t* xq;
@@ -243,6 +244,7 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
     for (int e = tid; e < d.E; e += 256) d.ecount[e] = 0;  // route_topk counts into them next
     if (tid == 0) {
       d.ctl[2] = 0;
+      d.ctl[3] = 0;
     }
   }
   const int nr = d.H / 2048 > 0 ? d.H / 2048 : 1;
@@ -398,8 +400,13 @@ __global__ __launch_bounds__(64) void route_topk_kernel(MoeDev d) {
     const int pos = atomicAdd(&d.ecount[my_id], 1);
     d.elist[(size_t)my_id * d.M + pos] = t * k + lane;
     // an expert's first token, and every 64th after it, opens a token block: one work item of the
-    // expert kernels, appended to the one compact list they read
-    if ((pos & (kTokBlock - 1)) == 0) d.eact[atomicAdd(&d.ctl[2], 1)] = my_id | ((pos >> kTokBlockShift) << 16);
+    // expert kernels.  First blocks go to one compact list, further blocks (a hot expert's, past 64
+    // tokens, four-tile work) to another that the expert kernels' grid takes first, so that with
+    // more items than a round of workgroups the heavy ones are not left for the second round.
+    if (pos == 0)
+      d.eact[atomicAdd(&d.ctl[2], 1)] = my_id;
+    else if ((pos & (kTokBlock - 1)) == 0)
+      d.eact[d.E + atomicAdd(&d.ctl[3], 1)] = my_id | ((pos >> kTokBlockShift) << 16);
   }
 }
 
@@ -610,9 +617,6 @@ __device__ __forceinline__ WorkItem work_item(const MoeDev& d) {
   const int b = blockIdx.x, x = b >> 3, r = x - 1 - d.nsh;
   WorkItem it;
   it.grp = b & 7;
-  const int n = d.ctl[2];
-  const int ent = d.eact[min(max(r, 0), 2 * d.E - 1)];
-  asm volatile("" ::"s"(n), "s"(ent));  // both loads issued before either is tested
   if (r < 0) {
     it.unit = 0;
     it.e = -1;
@@ -620,7 +624,21 @@ __device__ __forceinline__ WorkItem work_item(const MoeDev& d) {
     return it;
   }
   it.unit = 1;
-  it.e = r < n ? (ent & 0xffff) : -2;
+  if (d.M <= kTokBlock) {
+    // no further blocks: the first-block list alone, its count and entry in one round trip
+    const int n = d.ctl[2];
+    const int ent = d.eact[min(r, d.E - 1)];
+    asm volatile("" ::"s"(n), "s"(ent));  // both loads issued before either is tested
+    it.e = r < n ? ent : -2;
+    it.tb = 0;
+    return it;
+  }
+  // further blocks first, then the first blocks (the entry's index depends on the further count: a
+  // second round trip, past 64 tokens only)
+  const int nx = d.ctl[3], n = d.ctl[2];
+  const int i = r < nx ? d.E + r : r - nx;
+  const int ent = d.eact[min(i, 2 * d.E - 1)];
+  it.e = r < nx + n ? (ent & 0xffff) : -2;
   it.tb = ent >> 16;
   return it;
 }

@@ -126,8 +126,9 @@ typedef struct q36_moe_ws_layout {
   size_t h;        /* bf16 [M*topk+M, I] by slot (t*topk + j; shared M*topk + t) */
   size_t y;        /* bf16 [M*topk+M, H] by slot, routing weight applied */
   size_t ecount;   /* int32 [E] tokens per expert (route-internal) */
-  size_t eact;     /* int32 [2E] work items of the expert kernels, e | j << 16 (token block j of expert e),
-                    * unordered (route-internal; ctl[2] counts them) */
+  size_t eact;     /* int32 [2E] work items of the expert kernels, e | j << 16 (token block j of expert e):
+                    * [0, E) first blocks (ctl[2] counts them), [E, 2E) further blocks (ctl[3]); unordered
+                    * (route-internal) */
   size_t elist;    /* int32 [E, M] slots of each expert, unordered (route-internal) */
   size_t total;
 } q36_moe_ws_layout;
