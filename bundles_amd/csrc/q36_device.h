@@ -110,15 +110,28 @@ __device__ __forceinline__ float xor_swz(float v) {
   static_assert(M > 0 && M < 32, "xor mask within 32 lanes");
   return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (M << 10)));
 }
-__device__ __forceinline__ float wave_sum_bfly(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o);
+// The xor butterfly over the 64 lanes without LDS round trips: stage o combines v(l) with v(l ^ o),
+// o = 32, 16, 8, 4, 2, 1, exactly as a __shfl_xor butterfly does (the same pairs in the same stage
+// order, so the same bits for a commutative op), through v_permlane32_swap / v_permlane16_swap (the
+// swapped pair's two halves are v(l) and v(l ^ o) in some order), DPP row_ror:8 (within a 16-lane
+// row, lane i + 8 mod 16 is lane i ^ 8), ds_swizzle xor 4 and DPP quad_perm xor 2 / xor 1.
+template <typename Op>
+__device__ __forceinline__ float wave_bfly(float v, Op op) {
+  const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = op(__uint_as_float(p32[0]), __uint_as_float(p32[1]));
+  const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = op(__uint_as_float(p16[0]), __uint_as_float(p16[1]));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false)));  // xor 8
+  v = op(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (4 << 10))));         // xor 4
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false)));   // xor 2
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false)));   // xor 1
   return v;
 }
+__device__ __forceinline__ float wave_sum_bfly(float v) {
+  return wave_bfly(v, [](float a, float b) { return a + b; });
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  return wave_bfly(v, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
