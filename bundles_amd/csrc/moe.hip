@@ -347,12 +347,13 @@ __device__ __forceinline__ void sort_desc(uint32_t* key) {
 // in the lane, so each of the k picks is one wave max over the lanes' heads and a shift in the
 // winning lane.  The weights keep the oracle's arithmetic: p_j = exp(v_j - v_0) / sum in lane j,
 // their total added in pick order.
-template <int NM>
+// EXACT: E == 64 NM (every key of a lane is an expert; no per-key bounds test)
+template <int NM, bool EXACT>
 __global__ __launch_bounds__(64) void route_topk_kernel(MoeDev d) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x;  // one wave (and workgroup) per token: a batch's tokens on as many CUs
   if (t >= d.M) return;
-  const int E = d.E, k = d.k, nm = E / 64;
+  const int E = d.E, k = d.k, nm = EXACT ? NM : E / 64;
   const bool valid = d.pos == nullptr || d.pos[t] != 0;
   if (!valid) {
     if (lane < k) {
@@ -1365,10 +1366,14 @@ int launch_route(const MoeDev& d, int dtype, hipStream_t st) {
   };
   if (dtype == Q36_MOE_FP8) go_tt(std::integral_constant<int, Q36_MOE_FP8>{});
   else go_tt(std::integral_constant<int, Q36_MOE_INT8>{});
-  if (d.E <= 512)
-    route_topk_kernel<8><<<d.M, 64, 0, st>>>(d);
+  if (d.E == 512)
+    route_topk_kernel<8, true><<<d.M, 64, 0, st>>>(d);
+  else if (d.E < 512)
+    route_topk_kernel<8, false><<<d.M, 64, 0, st>>>(d);
+  else if (d.E == 1024)
+    route_topk_kernel<16, true><<<d.M, 64, 0, st>>>(d);
   else
-    route_topk_kernel<16><<<d.M, 64, 0, st>>>(d);
+    route_topk_kernel<16, false><<<d.M, 64, 0, st>>>(d);
   return check_launch("q36_moe_route");
 }
 int launch_lists(const MoeDev& d, hipStream_t st) {

@@ -145,15 +145,17 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
 // Unsigned max over the wave: xor 1, xor 2 (quad_perm), half-row and row mirrors (the mirrors pair
-// lanes holding already-reduced quads / half-rows), then the four row values through readlane.
+// lanes holding already-reduced quads / half-rows), then the rows through v_permlane16_swap and
+// v_permlane32_swap (VALU only: no readlane, whose SGPR results the next VALU use waits for).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
   v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
   v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
   v = max(v, dpp_u32<0x140>(v));  // row_mirror
-  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-  return max(max(a, b), max(c, d));
+  const auto p16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max((uint32_t)p16[0], (uint32_t)p16[1]);
+  const auto p32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max((uint32_t)p32[0], (uint32_t)p32[1]);
 }
 
 // Unsigned max over each row of 16 lanes (every lane of the row gets the row's maximum).
