@@ -1170,6 +1170,14 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
   __shared__ float rstd_s;
   __shared__ float zs[kCombH / 8][8];
   const int c = tid;  // the thread's 8-element chunk (H = 2048: one per thread)
+  const size_t at = (size_t)t * kCombH + 8 * c;
+  // the fused add-norm's residual chunk and norm weights are requested with the y rows (one round
+  // trip for every operand; out and resid do not overlap, checked on the host)
+  v4i rv = {0, 0, 0, 0}, wv = {0, 0, 0, 0};
+  if (d.norm_out != nullptr) {
+    rv = *reinterpret_cast<const v4i*>(d.resid + at);
+    wv = *reinterpret_cast<const v4i*>(d.norm_w + 8 * c);
+  }
   uint4 o = make_uint4(0u, 0u, 0u, 0u);
   if (valid) {
     // every y row of the token and its gate in one round trip (rows past k repeat the shared row)
@@ -1205,11 +1213,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
                       __builtin_fmaf(g, bf_hi((uint32_t)sv[q]), acc[2 * q + 1]));
     o = make_uint4(w[0], w[1], w[2], w[3]);
   }
-  const size_t at = (size_t)t * kCombH + 8 * c;
   *reinterpret_cast<uint4*>(d.out + at) = o;
   if (d.norm_out == nullptr) return;
   // the fused add-norm
-  const v4i rv = *reinterpret_cast<const v4i*>(d.resid + at);
   const uint32_t ow[4] = {o.x, o.y, o.z, o.w};
   float z[8];
   v4i nv;
@@ -1237,7 +1243,6 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
   }
   __syncthreads();
   const float rstd = rstd_s;
-  const v4i wv = *reinterpret_cast<const v4i*>(d.norm_w + 8 * c);
   v4i ov;
 #pragma unroll
   for (int q = 0; q < 4; ++q)
@@ -1254,8 +1259,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeDev d) {
     f[2 * q + 1] = bf_hi((uint32_t)ov[q]);
     m = fmaxf(m, fmaxf(fabsf(f[2 * q]), fabsf(f[2 * q + 1])));
   }
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  m = __uint_as_float(row16_max_u32(__float_as_uint(m)));  // non-negative: integer order; the 16 lanes of a group
   const float inv = m > 0.f ? 448.f / m : 0.f;
   *reinterpret_cast<uint2*>(d.norm_q8 + (d.norm_q8_frag ? frag_offset(t, 8 * c, kCombH) : at)) = e4m3_run8(f, inv);
   if ((c & 15) == 0) d.norm_q8s[(size_t)t * (kCombH / 128) + c / 16] = m / 448.f;
@@ -1313,6 +1317,12 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
   Q36_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0, "q36_moe: workspace must be 256-byte aligned");
   Q36_REQUIRE(a->norm_out == nullptr || (a->resid && a->norm_w),
               "q36_moe: the fused add-norm (norm_out) needs resid and norm_w");
+  {
+    const uintptr_t o0 = reinterpret_cast<uintptr_t>(a->out), r0 = reinterpret_cast<uintptr_t>(a->resid);
+    const uintptr_t nb = (uintptr_t)a->M * (uintptr_t)a->H * 2u;
+    Q36_REQUIRE(a->norm_out == nullptr || a->out == nullptr || o0 + nb <= r0 || r0 + nb <= o0,
+                "q36_moe: out and resid must not overlap");
+  }
   Q36_REQUIRE((a->norm_q8 == nullptr) == (a->norm_q8s == nullptr) && (a->norm_q8 == nullptr || a->norm_out),
               "q36_moe: norm_q8 and norm_q8s go together, with norm_out");
   Q36_REQUIRE(!a->norm_q8 || ((reinterpret_cast<uintptr_t>(a->norm_q8) & 7u) == 0 &&
