@@ -28,7 +28,8 @@ class MoeArgs(C.Structure):
                 ("gate_w", P), ("out", P), ("workspace", P), ("workspace_bytes", SZ),
                 ("dbg_acc13", P), ("dbg_acc2", P), ("dbg_h", P),
                 ("resid", P), ("norm_w", P), ("norm_eps", C.c_float), ("norm_out", P),
-                ("norm_q8", P), ("norm_q8s", P), ("norm_q8_frag", I32)]
+                ("norm_q8", P), ("norm_q8s", P), ("norm_q8_frag", I32),
+                ("in_delta", P), ("in_resid", P), ("in_resid_out", P), ("in_norm_w", P), ("in_norm_eps", C.c_float)]
 
 
 class MoeWsLayout(C.Structure):

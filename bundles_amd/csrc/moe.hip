@@ -89,6 +89,14 @@ struct MoeDev {
   uint8_t* norm_q8;       // norm_out's e4m3 codes (fragment order when norm_q8_frag), or null
   float* norm_q8s;
   int norm_q8_frag;
+  // this block's own input add-norm, run by the route kernel (in_norm_w != nullptr): x is formed
+  // there from in_delta + in_resid, in_resid_out receives the bf16 sum, xn (optional) the normed rows
+  const uint16_t* in_delta;
+  const uint16_t* in_resid;
+  uint16_t* in_resid_out;
+  const uint16_t* in_norm_w;
+  float in_eps;
+  uint16_t* xn;
 };
 
 __device__ __forceinline__ v4i ldg16_nt(const uint8_t* p) {
@@ -145,6 +153,72 @@ constexpr int kRouteH = 2048;
 // over many CUs, no wave computing a padding token's copy of another token), and from 33 tokens on
 // TT = 8, EPW = 4 (each unpacked activation feeds 4 experts; one workgroup a CU at batch 64).
 constexpr int kRouteT4Max = 16, kRouteE2Max = 32;
+// The block's input add-norm into a route workgroup's fp32 tile (256 threads, H = 2048: thread c owns
+// the 8-element chunk c of each of the TT rows): z = delta + resid, then the sum of squares of each
+// row in q36_add_rmsnorm's order (lane l of one wave takes chunks l + 64 j, fma from zero in (j,
+// element) order, then the xor butterfly) and the normed row, bf16-rounded, in place of z.  Ends with
+// the tile holding the rows x of the block; the caller's barrier publishes it.  ROW_OUT (one row, the
+// row's quantization workgroup): also in_resid_out <- bf16(z) and, when xn is set, xn <- x.
+template <int TT, bool ROW_OUT = false>
+__device__ __forceinline__ void in_norm_tile(const MoeDev& d, int t0, float4 (*xlo)[kRouteH / 8],
+                                             float4 (*xhi)[kRouteH / 8]) {
+  static_assert(!ROW_OUT || TT == 1, "one row per quantization workgroup");
+  const int c = threadIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __shared__ float rstd_s[TT];
+  float z[TT][8];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const size_t at = (size_t)min(t0 + t, d.M - 1) * kRouteH + 8 * c;
+    const v4i dv = ldg16(reinterpret_cast<const uint8_t*>(d.in_delta + at));
+    const v4i rv = ldg16(reinterpret_cast<const uint8_t*>(d.in_resid + at));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      z[t][2 * q] = bf_lo((uint32_t)dv[q]) + bf_lo((uint32_t)rv[q]);
+      z[t][2 * q + 1] = bf_hi((uint32_t)dv[q]) + bf_hi((uint32_t)rv[q]);
+    }
+    xlo[t][c] = make_float4(z[t][0], z[t][1], z[t][2], z[t][3]);
+    xhi[t][c] = make_float4(z[t][4], z[t][5], z[t][6], z[t][7]);
+    if constexpr (ROW_OUT) {
+      v4i nv;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) nv[q] = (int)pack_bf2(z[t][2 * q], z[t][2 * q + 1]);
+      *reinterpret_cast<v4i*>(d.in_resid_out + at) = nv;
+    }
+  }
+  const v4i wv = ldg16(reinterpret_cast<const uint8_t*>(d.in_norm_w + 8 * c));
+  __syncthreads();
+  for (int t = wave; t < TT; t += 4) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRouteH / 512; ++j) {
+      const float4 lo = xlo[t][lane + 64 * j], hi = xhi[t][lane + 64 * j];
+      const float e[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = __builtin_fmaf(e[i], e[i], acc);
+    }
+    const float ss = wave_sum_bfly(acc);
+    if (lane == 0) rstd_s[t] = 1.f / sqrtf(ss / (float)kRouteH + d.in_eps);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const float rstd = rstd_s[t];
+    float y[8];
+    v4i yv;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t p = pack_bf2((z[t][2 * q] * rstd) * (1.f + bf_lo((uint32_t)wv[q])),
+                                  (z[t][2 * q + 1] * rstd) * (1.f + bf_hi((uint32_t)wv[q])));
+      yv[q] = (int)p;
+      y[2 * q] = bf_lo(p);
+      y[2 * q + 1] = bf_hi(p);
+    }
+    xlo[t][c] = make_float4(y[0], y[1], y[2], y[3]);
+    xhi[t][c] = make_float4(y[4], y[5], y[6], y[7]);
+    if constexpr (ROW_OUT)
+      if (d.xn) *reinterpret_cast<v4i*>(d.xn + (size_t)t0 * kRouteH + 8 * c) = yv;
+  }
+}
 __host__ __device__ constexpr int route_tt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= kRouteT4Max ? 4 : 8; }
 __host__ __device__ constexpr int route_epw(int M) { return M <= kRouteE2Max ? 2 : 4; }
 template <int DT, int TT, int EPW>
@@ -168,14 +242,18 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
         w[x][j] = ldg16(reinterpret_cast<const uint8_t*>(d.wr + (size_t)(e0 + x) * kRouteH + 8 * (lane + 64 * j)));
+    if (d.in_norm_w) {
+      in_norm_tile<TT>(d, t0, xlo, xhi);
+    } else {
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      const int tok = min(t0 + t, d.M - 1);
-      const v4i xv = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)tok * kRouteH + 8 * threadIdx.x));
-      xlo[t][threadIdx.x] = make_float4(bf_lo((uint32_t)xv[0]), bf_hi((uint32_t)xv[0]), bf_lo((uint32_t)xv[1]),
-                                        bf_hi((uint32_t)xv[1]));
-      xhi[t][threadIdx.x] = make_float4(bf_lo((uint32_t)xv[2]), bf_hi((uint32_t)xv[2]), bf_lo((uint32_t)xv[3]),
-                                        bf_hi((uint32_t)xv[3]));
+      for (int t = 0; t < TT; ++t) {
+        const int tok = min(t0 + t, d.M - 1);
+        const v4i xv = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)tok * kRouteH + 8 * threadIdx.x));
+        xlo[t][threadIdx.x] = make_float4(bf_lo((uint32_t)xv[0]), bf_hi((uint32_t)xv[0]), bf_lo((uint32_t)xv[1]),
+                                          bf_hi((uint32_t)xv[1]));
+        xhi[t][threadIdx.x] = make_float4(bf_lo((uint32_t)xv[2]), bf_hi((uint32_t)xv[2]), bf_lo((uint32_t)xv[3]),
+                                          bf_hi((uint32_t)xv[3]));
+      }
     }
     __syncthreads();
     float v[NO];  // output o = x * TT + t
@@ -221,21 +299,39 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
   // combine reads one value instead of a dot product.
   const int t = bid - n_router_wg;
   const int tid = threadIdx.x;
+  // with the input add-norm, the row x is formed here (H = 2048: thread tid owns chunk tid) and
+  // stays in the LDS tile for the gate's canonical order
+  if (d.in_norm_w) {
+    in_norm_tile<1, true>(d, t, xlo, xhi);
+    __syncthreads();
+  }
   if (wave == 0 && d.gate_w != nullptr) {
-    v4i xg[kRouteH / 512], gg[kRouteH / 512];
+    float xe[kRouteH / 512][8];
+    v4i gg[kRouteH / 512];
 #pragma unroll
     for (int j = 0; j < kRouteH / 512; ++j) {
       const int c = lane + 64 * j;
-      xg[j] = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)t * kRouteH + 8 * c));
       gg[j] = ldg16(reinterpret_cast<const uint8_t*>(d.gate_w + 8 * c));
+      if (d.in_norm_w) {
+        const float4 lo = xlo[0][c], hi = xhi[0][c];
+        xe[j][0] = lo.x, xe[j][1] = lo.y, xe[j][2] = lo.z, xe[j][3] = lo.w;
+        xe[j][4] = hi.x, xe[j][5] = hi.y, xe[j][6] = hi.z, xe[j][7] = hi.w;
+      } else {
+        const v4i xg = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)t * kRouteH + 8 * c));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          xe[j][2 * q] = bf_lo((uint32_t)xg[q]);
+          xe[j][2 * q + 1] = bf_hi((uint32_t)xg[q]);
+        }
+      }
     }
     float acc = 0.f;
 #pragma unroll
     for (int j = 0; j < kRouteH / 512; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        acc = __builtin_fmaf(bf_lo((uint32_t)xg[j][q]), bf_lo((uint32_t)gg[j][q]), acc);
-        acc = __builtin_fmaf(bf_hi((uint32_t)xg[j][q]), bf_hi((uint32_t)gg[j][q]), acc);
+        acc = __builtin_fmaf(xe[j][2 * q], bf_lo((uint32_t)gg[j][q]), acc);
+        acc = __builtin_fmaf(xe[j][2 * q + 1], bf_hi((uint32_t)gg[j][q]), acc);
       }
     acc = wave_sum_bfly(acc);
     if (lane == 0) d.gate[t] = sigmoid_q(acc);
@@ -253,7 +349,11 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
   float amax_t = 0.f;
   for (int r = 0; r < nr; ++r) {
     const int c = tid + 256 * r;
-    if (8 * c < d.H) {
+    if (d.in_norm_w) {  // this thread's own chunk of the tile
+      const float4 lo = xlo[0][c], hi = xhi[0][c];
+      xf[r][0] = lo.x, xf[r][1] = lo.y, xf[r][2] = lo.z, xf[r][3] = lo.w;
+      xf[r][4] = hi.x, xf[r][5] = hi.y, xf[r][6] = hi.z, xf[r][7] = hi.w;
+    } else if (8 * c < d.H) {
       v4i xv = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)t * d.H + 8 * c));
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -1307,13 +1407,28 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
   Q36_REQUIRE(a->topk >= 1 && a->topk <= 16 && a->topk <= a->E, "q36_moe: topk=%d must be in [1, min(16, E)]",
               a->topk);
   Q36_REQUIRE(a->M >= 1 && a->M <= kMaxM, "q36_moe: M=%d must be in [1,%d]", a->M, kMaxM);
-  Q36_REQUIRE(a->x && a->router_w && a->workspace, "q36_moe: x, router_w and workspace are required");
+  Q36_REQUIRE((a->x || a->in_norm_w) && a->router_w && a->workspace,
+              "q36_moe: x (or the input add-norm), router_w and workspace are required");
+  Q36_REQUIRE(!a->in_norm_w || (a->in_delta && a->in_resid && a->in_resid_out),
+              "q36_moe: the input add-norm (in_norm_w) needs in_delta, in_resid and in_resid_out");
   Q36_REQUIRE(!need_experts || (a->w13 && a->s13 && a->w2 && a->s2 && a->sw13 && a->ss13 && a->sw2 && a->ss2 &&
                                 a->gate_w && a->out),
               "q36_moe_forward: an expert weight, scale, gate_w or out pointer is null");
   const void* ptrs[] = {a->x, a->router_w, a->w13, a->w2, a->sw13, a->sw2, a->gate_w, a->out, a->workspace,
-                        a->dbg_acc13, a->dbg_acc2, a->dbg_h, a->resid, a->norm_w, a->norm_out};
+                        a->dbg_acc13, a->dbg_acc2, a->dbg_h, a->resid, a->norm_w, a->norm_out,
+                        a->in_delta, a->in_resid, a->in_resid_out, a->in_norm_w};
   for (const void* p : ptrs) Q36_REQUIRE(aligned16(p), "q36_moe: pointer %p is not 16-byte aligned", p);
+  if (a->in_norm_w) {
+    // the route reads in_delta and in_resid while its row workgroups write in_resid_out and x
+    const uintptr_t nb = (uintptr_t)a->M * (uintptr_t)a->H * 2u;
+    auto apart = [&](const void* p, const void* q) {
+      const uintptr_t u = reinterpret_cast<uintptr_t>(p), v = reinterpret_cast<uintptr_t>(q);
+      return p == nullptr || q == nullptr || u + nb <= v || v + nb <= u;
+    };
+    Q36_REQUIRE(apart(a->in_resid_out, a->in_delta) && apart(a->in_resid_out, a->in_resid) &&
+                    apart(a->x, a->in_delta) && apart(a->x, a->in_resid) && apart(a->x, a->in_resid_out),
+                "q36_moe: in_resid_out and x must overlap neither in_delta, in_resid nor each other");
+  }
   Q36_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0, "q36_moe: workspace must be 256-byte aligned");
   Q36_REQUIRE(a->norm_out == nullptr || (a->resid && a->norm_w),
               "q36_moe: the fused add-norm (norm_out) needs resid and norm_w");
@@ -1352,6 +1467,15 @@ int validate(const q36_moe_args* a, MoeDev* d, bool need_experts) {
               static_cast<uint16_t*>(a->dbg_h), static_cast<uint16_t*>(a->resid),
               static_cast<const uint16_t*>(a->norm_w), a->norm_eps, static_cast<uint16_t*>(a->norm_out),
               static_cast<uint8_t*>(a->norm_q8), a->norm_q8s, a->norm_q8_frag != 0};
+  if (a->in_norm_w) {
+    d->x = nullptr;  // formed by the route kernel
+    d->in_delta = static_cast<const uint16_t*>(a->in_delta);
+    d->in_resid = static_cast<const uint16_t*>(a->in_resid);
+    d->in_resid_out = static_cast<uint16_t*>(a->in_resid_out);
+    d->in_norm_w = static_cast<const uint16_t*>(a->in_norm_w);
+    d->in_eps = a->in_norm_eps;
+    d->xn = static_cast<uint16_t*>(const_cast<void*>(a->x));
+  }
   return Q36_OK;
 }
 

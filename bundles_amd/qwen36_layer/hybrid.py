@@ -185,7 +185,7 @@ class HybridWorkspace:
             return torch.empty(shape, dtype=dtype, device=dev)
         n_gdn = KINDS.count("gdn")
         self.bufs = dict(
-            residual=e(M, HIDDEN), h=e(M, HIDDEN), h2=e(M, HIDDEN), o=e(M, HIDDEN), m=e(M, HIDDEN),
+            residual=e(M, HIDDEN), residual2=e(M, HIDDEN), h=e(M, HIDDEN), h2=e(M, HIDDEN), o=e(M, HIDDEN), m=e(M, HIDDEN),
             mixed=e(M, GDN_QKV), z=e(M, GDN_Z), b=e(M, GDN_HV), a=e(M, GDN_HV), gout=e(M, GDN_Z),
             snaps=[e(self.B, self.T, GDN_HV, 128, 128, dtype=torch.float32) for _ in range(n_gdn)] if self.snapshots
             else None,
@@ -229,7 +229,7 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
             return None
         return ws.q8_gdn if w.layers[i].kind == "gdn" else ws.q8_attn
 
-    res, h, h_next = b["residual"], b["h"], b["h2"]
+    res, res_alt, h, h_next = b["residual"], b["residual2"], b["h"], b["h2"]
     res.copy_(x)
     add_rmsnorm(None, res, w.layers[0].input_norm_w, w.eps, out=h, stream=stream, q8=rows_for(0))
     keep("x", x)
@@ -280,14 +280,16 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
                                   stream=stream, aq=oq)
         keep(f"L{i}.o", b["o"])
         keep(f"L{i}.res_in", res)
-        add_rmsnorm(b["o"], res, L.post_norm_w, w.eps, out=h, stream=stream)
-        keep(f"L{i}.post", h)
-        keep(f"L{i}.res_mid", res)
-        # the next block's input add-norm runs inside the MoE's combine (same bits as add_rmsnorm)
+        # the MoE block's input add-norm runs in its route kernel, the next block's in its combine
+        # (the same bits as add_rmsnorm before and after the block); the residual moves to the other
+        # buffer (the route reads the old one while it writes the new one)
         nxt = w.layers[i + 1].input_norm_w if i + 1 < len(w.layers) else w.final_norm_w
-        moe.moe_row_batch(h, None, L.router_w, L.gate_w, L.experts, TOPK, ws.moe, out=b["m"],
-                          router_bias=L.router_bias, stream=stream, norm=(res, nxt, w.eps, h_next),
-                          norm_q8=rows_for(i + 1))
+        moe.moe_row_batch(h if trace is not None else None, None, L.router_w, L.gate_w, L.experts, TOPK, ws.moe,
+                          out=b["m"], router_bias=L.router_bias, stream=stream,
+                          norm=(res_alt, nxt, w.eps, h_next), norm_q8=rows_for(i + 1),
+                          pre_norm=(b["o"], res, res_alt, L.post_norm_w, w.eps))
+        keep(f"L{i}.post", h)
+        res, res_alt = res_alt, res
         h, h_next = h_next, h
         keep(f"L{i}.moe", b["m"])
         keep(f"L{i}.res_out", res)

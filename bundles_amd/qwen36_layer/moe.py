@@ -179,8 +179,9 @@ class Workspace:
             y=v(L.y, (S + M) * self.H, torch.bfloat16).view(S + M, self.H))
 
 
-def _args(x, positions, router_w, gate_w, ew, topk, ws: Workspace, out, router_bias, debug, norm=None, norm_q8=None):
-    M, H = x.shape
+def _args(x, positions, router_w, gate_w, ew, topk, ws: Workspace, out, router_bias, debug, norm=None, norm_q8=None,
+          pre_norm=None):
+    M, H = (x if x is not None else pre_norm[0]).shape
     if M > ws.max_tokens:
         raise ValueError(f"moe_row_batch: {M} rows exceed the workspace's {ws.max_tokens}")
     for name, t in (("x", x), ("router_w", router_w), ("gate_w", gate_w)):
@@ -197,15 +198,25 @@ def _args(x, positions, router_w, gate_w, ew, topk, ws: Workspace, out, router_b
     if norm is not None:
         resid, norm_w, eps, norm_out = norm
         for name, t in (("resid", resid), ("norm_out", norm_out)):
-            if t.dtype != torch.bfloat16 or not t.is_contiguous() or tuple(t.shape) != tuple(x.shape):
-                raise ValueError(f"moe_row_batch: {name} must be contiguous bfloat16 {tuple(x.shape)}")
+            if t.dtype != torch.bfloat16 or not t.is_contiguous() or tuple(t.shape) != (M, H):
+                raise ValueError(f"moe_row_batch: {name} must be contiguous bfloat16 {(M, H)}")
         if norm_w.dtype != torch.bfloat16 or not norm_w.is_contiguous() or norm_w.numel() != H:
             raise ValueError(f"moe_row_batch: norm_w must be contiguous bfloat16 [{H}]")
+    delta = r_in = r_out = in_w = None
+    in_eps = 0.0
+    if pre_norm is not None:
+        delta, r_in, r_out, in_w, in_eps = pre_norm
+        for name, t in (("delta", delta), ("resid_in", r_in), ("resid_out", r_out)):
+            if t.dtype != torch.bfloat16 or not t.is_contiguous() or tuple(t.shape) != (M, H):
+                raise ValueError(f"moe_row_batch: pre_norm {name} must be contiguous bfloat16 {(M, H)}")
+        if in_w.dtype != torch.bfloat16 or not in_w.is_contiguous() or in_w.numel() != H:
+            raise ValueError(f"moe_row_batch: pre_norm norm_w must be contiguous bfloat16 [{H}]")
     return MoeArgs(M, router_w.shape[0], H, ws.I, topk, ws.dtype, ptr(x), ptr(router_w), ptr(router_bias),
                    ptr(positions), *(ptr(t) for t in w), ptr(gate_w), ptr(out), ptr(ws.buf), ws.buf.numel(),
                    ptr(dbg.get("acc13")), ptr(dbg.get("acc2")), ptr(dbg.get("h")), ptr(resid), ptr(norm_w),
                    float(eps), ptr(norm_out), ptr(None if norm_q8 is None else norm_q8.codes),
-                   ptr(None if norm_q8 is None else norm_q8.scales), int(norm_q8 is not None and norm_q8.frag))
+                   ptr(None if norm_q8 is None else norm_q8.scales), int(norm_q8 is not None and norm_q8.frag),
+                   ptr(delta), ptr(r_in), ptr(r_out), ptr(in_w), float(in_eps))
 
 
 def route(x, positions, router_w, topk: int, ws: Workspace, router_bias=None, stream=None):
@@ -216,20 +227,28 @@ def route(x, positions, router_w, topk: int, ws: Workspace, router_bias=None, st
 
 
 def moe_row_batch(x, positions, router_w, gate_w, ew: ExpertWeights, topk: int, ws: Workspace, out=None,
-                  router_bias=None, debug=None, stream=None, norm=None, norm_q8=None):
+                  router_bias=None, debug=None, stream=None, norm=None, norm_q8=None, pre_norm=None):
     """out[M, H] = shared_gate * shared_expert(x) + sum_j w_j * expert_{id_j}(x)  (bf16).
 
     norm = (resid, norm_w, eps, norm_out) fuses the next block's input add-norm into the combine:
     resid <- bf16(out + resid) in place and norm_out = its Gemma RMSNorm, the same bits as
     glue.add_rmsnorm(out, resid, norm_w, eps) after the block (L/qk_route.cu:630-820 combine_norm).
-    norm_q8 (attn_fused.QuantRows, with norm): norm_out's e4m3 codes for the next projection."""
+    norm_q8 (attn_fused.QuantRows, with norm): norm_out's e4m3 codes for the next projection.
+    pre_norm = (delta, resid_in, resid_out, norm_w, eps) runs this block's own input add-norm in the
+    route kernel: resid_out <- bf16(delta + resid_in) and x = its Gemma RMSNorm, the same bits as
+    glue.add_rmsnorm(delta, resid, norm_w, eps, out=x) before the block; x is then an optional
+    output (None, or a tensor that receives those rows).  resid_out must be another buffer than
+    resid_in and delta (the route reads them while it writes)."""
     if ew.E != router_w.shape[0] or ew.I != ws.I or ew.dtype != ws.dtype or ew.E != ws.E:
         raise ValueError("moe_row_batch: expert weights, router and workspace disagree on E / I / dtype")
+    if x is None and pre_norm is None:
+        raise ValueError("moe_row_batch: x is required without pre_norm")
+    shape_src = x if x is not None else pre_norm[0]
     if out is None:
-        out = torch.empty_like(x)
-    if norm_q8 is not None and (norm is None or norm_q8.T != x.shape[0]):
+        out = torch.empty_like(shape_src)
+    if norm_q8 is not None and (norm is None or norm_q8.T != shape_src.shape[0]):
         raise ValueError("moe_row_batch: norm_q8 needs the fused add-norm and one row per token")
-    a = _args(x, positions, router_w, gate_w, ew, topk, ws, out, router_bias, debug, norm, norm_q8)
+    a = _args(x, positions, router_w, gate_w, ew, topk, ws, out, router_bias, debug, norm, norm_q8, pre_norm)
     check(_lib.lib().q36_moe_forward(C.byref(a), _lib.stream_handle(stream)), "q36_moe_forward")
     return out
 

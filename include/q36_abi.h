@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define Q36_ABI_VERSION 5
+#define Q36_ABI_VERSION 6
 #define Q36_OK 0
 #define Q36_EINVAL 1
 #define Q36_ELAUNCH 2
@@ -108,6 +108,18 @@ typedef struct q36_moe_args {
   void* norm_q8;
   float* norm_q8s;
   int32_t norm_q8_frag;
+  /* Optional (no reference counterpart as one launch; the arithmetic is q36_add_rmsnorm's): this
+   * block's own input add-norm run by the route kernel, when in_norm_w is not NULL.  z = in_delta +
+   * in_resid (fp32), in_resid_out <- bf16(z), and the block runs on x = bf16((z * rstd) *
+   * (1 + in_norm_w)) with rstd over z in q36_add_rmsnorm's order: the same bits as q36_add_rmsnorm
+   * (in_delta, residual, in_norm_w, out = x) followed by the block.  x is then an optional output
+   * (those rows, or NULL).  in_delta, in_resid, in_resid_out bf16 [M, H], in_norm_w bf16 [H];
+   * in_resid_out and x overlap neither in_delta nor in_resid (the route reads those while it writes). */
+  const void* in_delta;
+  const void* in_resid;
+  void* in_resid_out;
+  const void* in_norm_w;
+  float in_norm_eps;
 } q36_moe_args;
 
 typedef struct q36_moe_ws_layout {

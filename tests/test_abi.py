@@ -35,7 +35,7 @@ def test_every_declared_symbol_is_exported(L):
         assert hasattr(L, n), f"{n} declared in q36_abi.h but not exported"
     bound = {s[0] for s in _lib.SYMBOLS}
     assert set(names) <= bound, f"not bound in _lib.SYMBOLS: {set(names) - bound}"
-    assert L.q36_abi_version() == 5
+    assert L.q36_abi_version() == 6
 
 
 def test_struct_layouts_match_header(tmp_path):
@@ -80,6 +80,17 @@ def test_invalid_arguments_are_rejected(L):
     assert L.q36_moe_forward(C.byref(a), None) == _lib.Q36_EINVAL
     a.dtype = 1
     assert L.q36_moe_forward(C.byref(a), None) == _lib.Q36_EINVAL  # null pointers
+    # the route's input add-norm: its three row buffers are required, and what the route writes
+    # (in_resid_out, x) must not overlap what it reads (host addresses: nothing is launched)
+    a.router_w, a.workspace, a.in_norm_w = 0x10000, 0x20000, 0x30000
+    assert L.q36_moe_route(C.byref(a), None) == _lib.Q36_EINVAL
+    assert b"in_delta" in L.q36_last_error()
+    a.in_delta, a.in_resid, a.in_resid_out = 0x100000, 0x200000, 0x100000 + 8 * 2048 * 2 - 16
+    assert L.q36_moe_route(C.byref(a), None) == _lib.Q36_EINVAL
+    assert b"overlap" in L.q36_last_error()
+    a.in_resid_out, a.x = 0x300000, 0x200000 + 4096
+    assert L.q36_moe_route(C.byref(a), None) == _lib.Q36_EINVAL
+    assert b"overlap" in L.q36_last_error()
     g = _lib.GdnArgs()
     g.B, g.T = 2, 9
     assert L.q36_gdn_verify(C.byref(g), None) == _lib.Q36_EINVAL

@@ -45,7 +45,9 @@ def test_add_norms_are_bit_exact(run, oracle_mod):
     for i, L in enumerate(w.layers):
         post, res_mid = O.add_rmsnorm(bits16(tr[f"L{i}.o"]), bits16(tr[f"L{i}.res_in"]), bits16(L.post_norm_w), w.eps)
         assert np.array_equal(post, bits16(tr[f"L{i}.post"])), f"layer {i} post norm"
-        assert np.array_equal(res_mid, bits16(tr[f"L{i}.res_mid"])), f"layer {i} residual after the mixer"
+        # the residual after the mixer lives only inside the MoE call (its route writes it, its combine
+        # adds to it in place): checked through the residual after the MoE, formed from the oracle's
+        # res_mid below, and directly by test_moe_input_add_norm
         nxt = w.layers[i + 1].input_norm_w if i + 1 < len(w.layers) else w.final_norm_w
         hn, res_out = O.add_rmsnorm(bits16(tr[f"L{i}.moe"]), res_mid, bits16(nxt), w.eps)
         want = tr[f"L{i + 1}.in"] if i + 1 < len(w.layers) else tr["final"]

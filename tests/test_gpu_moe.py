@@ -312,6 +312,68 @@ def test_moe_fused_add_norm(q36, oracle_mod, dev, dtype):
     assert np.array_equal(bits16(y_got), hn) and np.array_equal(bits16(r_got), res)
 
 
+@pytest.mark.parametrize("dtype,M", [(1, 1), (1, 2), (0, 5), (1, 24), (1, 40), (0, 64), (1, 256)])
+def test_moe_input_add_norm(q36, oracle_mod, dev, dtype, M):
+    """This block's own input add-norm run by the route kernel (pre_norm) gives the same bits as
+    q36_add_rmsnorm followed by the block: the normed rows, the new residual, the block output (padding
+    rows included), and with the next block's add-norm fused into the combine too, the hybrid node's
+    form; the old residual is left as it was, and the oracle's add-norm agrees.  M covers every router
+    shape (1, 2, 4 and 8 tokens a workgroup, two and four experts a wave)."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import glue
+    O = oracle_mod
+    E = 512 if M in (1, 256) else 64
+    d = synth.moe_inputs(M, dev, seed=31 + M, E=E, zipf=1.1)
+    ew = q36.prepare_experts(d["w13"], d["w2"], d["sw13"], d["sw2"], dtype)
+    ws = q36.Workspace(E, 2048, 512, 10, dtype, dev)
+    pos = torch.arange(1, M + 1, dtype=torch.int32, device=dev)
+    pos[2::5] = 0
+    g = synth.gen(dev, 91 + M)
+    delta, resid0 = synth.randn((M, 2048), g, dev), synth.randn((M, 2048), g, dev)
+    nw, nw2 = synth.randn((2048,), g, dev, 0.1), synth.randn((2048,), g, dev, 0.1)
+    kw = dict(router_bias=d["router_bias"])
+    r_ref = resid0.clone()
+    x_ref = glue.add_rmsnorm(delta, r_ref, nw, 1e-6)
+    ref = q36.moe_row_batch(x_ref, pos, d["router_w"], d["gate_w"], ew, 10, ws, **kw)
+    r_in, r_out, x_got = resid0.clone(), torch.empty_like(resid0), torch.empty_like(resid0)
+    got = q36.moe_row_batch(x_got, pos, d["router_w"], d["gate_w"], ew, 10, ws, **kw,
+                            pre_norm=(delta, r_in, r_out, nw, 1e-6))
+    r_out2 = torch.empty_like(resid0)
+    got2 = q36.moe_row_batch(None, pos, d["router_w"], d["gate_w"], ew, 10, ws, **kw,
+                             pre_norm=(delta, r_in, r_out2, nw, 1e-6))
+    # both norms fused (the hybrid node's layer): then the next block's add-norm on the new residual
+    r_ref2 = r_ref.clone()
+    y_ref = glue.add_rmsnorm(ref, r_ref2, nw2, 1e-6)
+    r_out3, y_got = torch.empty_like(resid0), torch.empty_like(resid0)
+    got3 = q36.moe_row_batch(None, pos, d["router_w"], d["gate_w"], ew, 10, ws, **kw,
+                             pre_norm=(delta, r_in, r_out3, nw, 1e-6), norm=(r_out3, nw2, 1e-6, y_got))
+    torch.cuda.synchronize()
+    eq = lambda a, b: torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert eq(x_got, x_ref), "normed rows"
+    assert eq(r_out, r_ref) and eq(r_out2, r_ref), "new residual"
+    assert eq(r_in, resid0), "the old residual is read only"
+    assert eq(got, ref) and eq(got2, ref) and eq(got3, ref), "block output"
+    assert eq(r_out3, r_ref2) and eq(y_got, y_ref), "the next block's add-norm after the fused one"
+    hn, res = O.add_rmsnorm(bits16(delta), bits16(resid0), bits16(nw), 1e-6)
+    assert np.array_equal(bits16(x_got), hn) and np.array_equal(bits16(r_out), res)
+
+
+def test_moe_input_add_norm_rejects_overlap(q36, dev):
+    """The route reads in_delta and in_resid while it writes in_resid_out and x: overlapping buffers
+    are refused before anything is launched."""
+    from bundles_amd import synth
+    d = synth.moe_inputs(8, dev, seed=5, E=64, zipf=1.1)
+    ew = q36.prepare_experts(d["w13"], d["w2"], d["sw13"], d["sw2"], 1)
+    ws = q36.Workspace(64, 2048, 512, 10, 1, dev)
+    delta, resid = torch.zeros((8, 2048), dtype=torch.bfloat16, device=dev), torch.zeros((8, 2048), dtype=torch.bfloat16, device=dev)
+    nw = torch.zeros(2048, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(RuntimeError, match="overlap"):
+        q36.moe_row_batch(None, None, d["router_w"], d["gate_w"], ew, 10, ws, pre_norm=(delta, resid, resid, nw, 1e-6))
+    with pytest.raises(RuntimeError, match="overlap"):
+        q36.moe_row_batch(delta, None, d["router_w"], d["gate_w"], ew, 10, ws,
+                          pre_norm=(delta, resid, torch.empty_like(resid), nw, 1e-6))
+
+
 def test_moe_repeat_deterministic(q36, dev):
     """Two calls on one workspace give identical bits (the self-resetting ticket, no races)."""
     from bundles_amd import synth
