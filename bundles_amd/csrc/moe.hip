@@ -447,13 +447,15 @@ __device__ __forceinline__ void sort_desc(uint32_t* key) {
 // in the lane, so each of the k picks is one wave max over the lanes' heads and a shift in the
 // winning lane.  The weights keep the oracle's arithmetic: p_j = exp(v_j - v_0) / sum in lane j,
 // their total added in pick order.
-// EXACT: E == 64 NM (every key of a lane is an expert; no per-key bounds test)
-template <int NM, bool EXACT>
+// EXACT: E == 64 NM (every key of a lane is an expert; no per-key bounds test).  KF: k fixed at
+// compile time (0: d.k), so the picks unroll and the softmax's exponentials, which need only the
+// first pick (the maximum), interleave with the later picks' cross-lane maxima.
+template <int NM, bool EXACT, int KF>
 __global__ __launch_bounds__(64) void route_topk_kernel(MoeDev d) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x;  // one wave (and workgroup) per token: a batch's tokens on as many CUs
   if (t >= d.M) return;
-  const int E = d.E, k = d.k, nm = EXACT ? NM : E / 64;
+  const int E = d.E, k = KF ? KF : d.k, nm = EXACT ? NM : E / 64;
   const bool valid = d.pos == nullptr || d.pos[t] != 0;
   if (!valid) {
     if (lane < k) {
@@ -469,24 +471,39 @@ __global__ __launch_bounds__(64) void route_topk_kernel(MoeDev d) {
 #pragma unroll
   for (int m = 0; m < NM; ++m) key[m] = m < nm ? logit_key(lg[m], lane + 64 * m) : 0u;
   sort_desc<NM>(key);
-  float mx = 0.f, my_v = 0.f;
+  float my_v = 0.f;
   int my_id = -1;
-  for (int j = 0; j < k; ++j) {  // k is uniform
+  // pick j: one wave max over the lanes' heads; keys are distinct, so one lane pops its head (a bit
+  // select per key, no index arithmetic)
+  auto pick = [&](int j) {
     const uint32_t win = wave_max_u32(key[0]);
     const float v = key_logit(win);
-    if (j == 0) mx = v;
     my_v = lane == j ? v : my_v;
     my_id = lane == j ? (int)(0xffffu - (win & 0xffffu)) : my_id;
-    // keys are distinct: one lane pops its head (a bit select per key, no index arithmetic)
     const uint32_t pop = key[0] == win ? 0xffffffffu : 0u;
 #pragma unroll
     for (int i = 0; i + 1 < NM; ++i) key[i] = (key[i + 1] & pop) | (key[i] & ~pop);
     key[NM - 1] &= ~pop;
-  }
+    return v;
+  };
+  const float mx = pick(0);
   float part = 0.f;
+  if constexpr (KF > 0) {
+    // exponential m goes between picks m + 1 and m + 2 (the sum keeps its order m = 0, 1, ...)
 #pragma unroll
-  for (int m = 0; m < NM; ++m)
-    if (m < nm) part = part + expf_q(lg[m] - mx);
+    for (int j = 1; j < KF; ++j) {
+      pick(j);
+      if (j - 1 < NM && j - 1 < nm) part = part + expf_q(lg[j - 1] - mx);
+    }
+#pragma unroll
+    for (int m = KF - 1; m < NM; ++m)
+      if (m < nm) part = part + expf_q(lg[m] - mx);
+  } else {
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+      if (m < nm) part = part + expf_q(lg[m] - mx);
+    for (int j = 1; j < k; ++j) pick(j);  // k is uniform
+  }
   const float sum = wave_sum_bfly(part);
   const float my_p = lane < k ? expf_q(my_v - mx) / sum : 0.f;
   float wsum = 0.f;
@@ -1500,14 +1517,16 @@ int launch_route(const MoeDev& d, int dtype, hipStream_t st) {
   };
   if (dtype == Q36_MOE_FP8) go_tt(std::integral_constant<int, Q36_MOE_FP8>{});
   else go_tt(std::integral_constant<int, Q36_MOE_INT8>{});
-  if (d.E == 512)
-    route_topk_kernel<8, true><<<d.M, 64, 0, st>>>(d);
+  if (d.E == 512 && d.k == 10)
+    route_topk_kernel<8, true, 10><<<d.M, 64, 0, st>>>(d);
+  else if (d.E == 512)
+    route_topk_kernel<8, true, 0><<<d.M, 64, 0, st>>>(d);
   else if (d.E < 512)
-    route_topk_kernel<8, false><<<d.M, 64, 0, st>>>(d);
+    route_topk_kernel<8, false, 0><<<d.M, 64, 0, st>>>(d);
   else if (d.E == 1024)
-    route_topk_kernel<16, true><<<d.M, 64, 0, st>>>(d);
+    route_topk_kernel<16, true, 0><<<d.M, 64, 0, st>>>(d);
   else
-    route_topk_kernel<16, false><<<d.M, 64, 0, st>>>(d);
+    route_topk_kernel<16, false, 0><<<d.M, 64, 0, st>>>(d);
   return check_launch("q36_moe_route");
 }
 int launch_lists(const MoeDev& d, hipStream_t st) {
