@@ -127,15 +127,57 @@ __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
 // NO = TT EPW outputs), then the xor butterfly's remaining stages: every sum pairs the same two
 // operands as the xor butterfly (offsets 32 .. 1) of q36o_dot_canon, so the logits are
 // bit-identical to the oracle's.
-// One reduce-scatter stage over N values: lanes whose bit O is set keep the upper half.
+// v of lane l ^ O, O < 16, without LDS: DPP row_ror:8 (within a 16-lane row lane i + 8 mod 16 is
+// lane i ^ 8), ds_swizzle xor 4, DPP quad_perm xor 2 / xor 1
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(O == 8 || O == 4 || O == 2 || O == 1, "xor offset below 16");
+  if constexpr (O == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+  else if constexpr (O == 4) return xor_swz<4>(v);
+  else if constexpr (O == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+  else return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+}
+// One reduce-scatter stage over N values: lanes whose bit O is set keep the upper half, and add the
+// partner's (lane l ^ O) copy of it.  O = 32 / 16: v_permlane32_swap / v_permlane16_swap of the
+// halves (v[i], v[i + N / 2]) leaves, in every lane, the kept value and the partner's in its two
+// results (no select); below 16 a select per half and a DPP / swizzle move.  Every sum pairs the same
+// two operands as a __shfl_xor stage.
 template <int N, int O>
 __device__ __forceinline__ void rs_stage(float* v, int lane) {
-  const bool hi = (lane & O) != 0;
+  if constexpr (O == 32 || O == 16) {
 #pragma unroll
-  for (int i = 0; i < N / 2; ++i) {
-    const float send = hi ? v[i] : v[i + N / 2];
-    const float keep = hi ? v[i + N / 2] : v[i];
-    v[i] = keep + __shfl_xor(send, O);
+    for (int i = 0; i < N / 2; ++i) {
+      const uint32_t a = __float_as_uint(v[i]), b = __float_as_uint(v[i + N / 2]);
+      uint32_t r0, r1;
+      if constexpr (O == 32) {
+        const auto p = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+        r0 = p[0], r1 = p[1];
+      } else {
+        const auto p = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+        r0 = p[0], r1 = p[1];
+      }
+      v[i] = __uint_as_float(r0) + __uint_as_float(r1);
+    }
+  } else {
+    const bool hi = (lane & O) != 0;
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      const float send = hi ? v[i] : v[i + N / 2];
+      const float keep = hi ? v[i + N / 2] : v[i];
+      v[i] = keep + lane_xor<O>(send);
+    }
+  }
+}
+// The xor butterfly's stages O, O / 2, .. 1 on one value (O <= 16; O = 0: none)
+template <int O>
+__device__ __forceinline__ float bfly_from(float v) {
+  if constexpr (O == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return bfly_from<8>(__uint_as_float(p[0]) + __uint_as_float(p[1]));
+  } else if constexpr (O >= 1) {
+    return bfly_from<O / 2>(v + lane_xor<O>(v));
+  } else {
+    return v;
   }
 }
 // Stages xor O, O / 2, ... until one value is left: lane l then holds output (l / (64 / N)) % N
@@ -283,9 +325,8 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
       }
     }
     rs_all<NO, 32>(v, lane);
-    float tot = v[0];
-#pragma unroll
-    for (int o = 32 >> S; o >= 1; o >>= 1) tot = tot + __shfl_xor(tot, o);
+    const float tot0 = bfly_from<(32 >> S)>(v[0]);
+    float tot = tot0;
     const int o = (lane >> (6 - S)) & (NO - 1), t = o % TT, e = e0 + o / TT;
     if ((lane & ((64 >> S) - 1)) == 0 && t0 + t < d.M) {
       if (d.bias) tot = tot + d.bias[e];
