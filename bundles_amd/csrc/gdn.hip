@@ -170,9 +170,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     float u[2], ov[2] = {0.f, 0.f};
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      kv[h] = kv[h] + __shfl_xor(kv[h], 1);
-      kv[h] = kv[h] + __shfl_xor(kv[h], 2);
-      kv[h] = kv[h] + __shfl_xor(kv[h], 4);
+      kv[h] = kv[h] + lane_xor<1>(kv[h]);  // DPP / swizzle moves: the __shfl_xor pairs without LDS
+      kv[h] = kv[h] + lane_xor<2>(kv[h]);
+      kv[h] = kv[h] + lane_xor<4>(kv[h]);
       u[h] = beta * (vs[t][r0 + 64 * h] - eg * kv[h]);
     }
 #pragma unroll
@@ -190,9 +190,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      ov[h] = ov[h] + __shfl_xor(ov[h], 1);
-      ov[h] = ov[h] + __shfl_xor(ov[h], 2);
-      ov[h] = ov[h] + __shfl_xor(ov[h], 4);
+      ov[h] = ov[h] + lane_xor<1>(ov[h]);
+      ov[h] = ov[h] + lane_xor<2>(ov[h]);
+      ov[h] = ov[h] + lane_xor<4>(ov[h]);
       if (c8 == 0) os[t][r0 + 64 * h] = rbf(ov[h]);  // the core output is bf16
     }
   }

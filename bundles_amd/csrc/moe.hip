@@ -127,16 +127,6 @@ __device__ __forceinline__ v4i mfma_i8(v4i a, v4i b, v4i c) {
 // NO = TT EPW outputs), then the xor butterfly's remaining stages: every sum pairs the same two
 // operands as the xor butterfly (offsets 32 .. 1) of q36o_dot_canon, so the logits are
 // bit-identical to the oracle's.
-// v of lane l ^ O, O < 16, without LDS: DPP row_ror:8 (within a 16-lane row lane i + 8 mod 16 is
-// lane i ^ 8), ds_swizzle xor 4, DPP quad_perm xor 2 / xor 1
-template <int O>
-__device__ __forceinline__ float lane_xor(float v) {
-  static_assert(O == 8 || O == 4 || O == 2 || O == 1, "xor offset below 16");
-  if constexpr (O == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
-  else if constexpr (O == 4) return xor_swz<4>(v);
-  else if constexpr (O == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
-  else return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
-}
 // One reduce-scatter stage over N values: lanes whose bit O is set keep the upper half, and add the
 // partner's (lane l ^ O) copy of it.  O = 32 / 16: v_permlane32_swap / v_permlane16_swap of the
 // halves (v[i], v[i + N / 2]) leaves, in every lane, the kept value and the partner's in its two
@@ -433,8 +423,7 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
       float m = 0.f;
 #pragma unroll
       for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(xf[r][q]));
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+      m = __uint_as_float(row16_max_u32(__float_as_uint(m)));  // m >= 0: the bits order as the values
       if (8 * c < d.H) {
         const float s = m / 448.f, inv = m > 0.f ? 448.f / m : 0.f;
         uint32_t wd[2] = {0u, 0u};
@@ -1190,8 +1179,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int v = 0; v < 32; ++v) m = fmaxf(m, fabsf(hval(v)));
         uint32_t wd[8];
         if constexpr (DT == Q36_MOE_FP8) {
-          m = fmaxf(m, __shfl_xor(m, 1));
-          m = fmaxf(m, __shfl_xor(m, 2));
+          m = fmaxf(m, lane_xor<1>(m));
+          m = fmaxf(m, lane_xor<2>(m));
           const float inv = m > 0.f ? 448.f / m : 0.f;
 #pragma unroll
           for (int v = 0; v < 8; ++v)
@@ -1199,8 +1188,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     (f2e4m3x2_hw(hval(4 * v + 2) * inv, hval(4 * v + 3) * inv) << 16);
           if ((q16 & 3) == 0) hs[row][q16 >> 2] = m / 448.f;
         } else {
-#pragma unroll
-          for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+          m = fmaxf(m, lane_xor<1>(m));
+          m = fmaxf(m, lane_xor<2>(m));
+          m = fmaxf(m, lane_xor<4>(m));
+          m = fmaxf(m, lane_xor<8>(m));
           const float sc = m / 127.f, safe = m > 0.f ? sc : 1.f;
 #pragma unroll
           for (int v = 0; v < 8; ++v) {

@@ -110,6 +110,16 @@ __device__ __forceinline__ float xor_swz(float v) {
   static_assert(M > 0 && M < 32, "xor mask within 32 lanes");
   return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (M << 10)));
 }
+// v of lane l ^ O, O < 16, without LDS: DPP row_ror:8 (within a 16-lane row lane i + 8 mod 16 is
+// lane i ^ 8), ds_swizzle xor 4, DPP quad_perm xor 2 / xor 1
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(O == 8 || O == 4 || O == 2 || O == 1, "xor offset below 16");
+  if constexpr (O == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+  else if constexpr (O == 4) return xor_swz<4>(v);
+  else if constexpr (O == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+  else return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+}
 // The xor butterfly over the 64 lanes without LDS round trips: stage o combines v(l) with v(l ^ o),
 // o = 32, 16, 8, 4, 2, 1, exactly as a __shfl_xor butterfly does (the same pairs in the same stage
 // order, so the same bits for a commutative op), through v_permlane32_swap / v_permlane16_swap (the
