@@ -182,9 +182,12 @@ __device__ __forceinline__ void rs_all(float* v, int lane) {
 constexpr int kRouteH = 2048;
 // Router shapes, TT tokens x EPW experts a wave, by batch: one token group per 1 or 2 tokens, groups
 // of 4 up to 16 tokens and of 8 up to 32 with EPW = 2 (64 workgroups a token group: the GEMV spread
-// over many CUs, no wave computing a padding token's copy of another token), and from 33 tokens on
-// TT = 8, EPW = 4 (each unpacked activation feeds 4 experts; one workgroup a CU at batch 64).
-constexpr int kRouteT4Max = 16, kRouteE2Max = 32;
+// over many CUs, no wave computing a padding token's copy of another token), from 33 tokens on
+// TT = 8, EPW = 4 (each unpacked activation feeds 4 experts; one workgroup a CU at batch 64), and past
+// 128 tokens EPW = 8 (32 experts a workgroup: half the workgroups, so half the re-reads of each
+// token group's rows and, with the input add-norm, half the redundant norms; measured at 256 rows:
+// the layer 92.0 -> 90.9 us, the hybrid step with the add-norm in the route 938-946 -> 924-927 us).
+constexpr int kRouteT4Max = 16, kRouteE2Max = 32, kRouteE4Max = 128;
 // The block's input add-norm into a route workgroup's fp32 tile (256 threads, H = 2048: thread c owns
 // the 8-element chunk c of each of the TT rows): z = delta + resid, then the sum of squares of each
 // row in q36_add_rmsnorm's order (lane l of one wave takes chunks l + 64 j, fma from zero in (j,
@@ -252,7 +255,7 @@ __device__ __forceinline__ void in_norm_tile(const MoeDev& d, int t0, float4 (*x
   }
 }
 __host__ __device__ constexpr int route_tt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= kRouteT4Max ? 4 : 8; }
-__host__ __device__ constexpr int route_epw(int M) { return M <= kRouteE2Max ? 2 : 4; }
+__host__ __device__ constexpr int route_epw(int M) { return M <= kRouteE2Max ? 2 : M <= kRouteE4Max ? 4 : 8; }
 template <int DT, int TT, int EPW>
 __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_router_wg) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1545,7 +1548,8 @@ int launch_route(const MoeDev& d, int dtype, hipStream_t st) {
     else if (tt == 2) go(dt, I2{}, I2{});
     else if (tt == 4) go(dt, I4{}, I2{});
     else if (epw == 2) go(dt, I8{}, I2{});
-    else go(dt, I8{}, I4{});
+    else if (epw == 4) go(dt, I8{}, I4{});
+    else go(dt, I8{}, std::integral_constant<int, 8>{});
   };
   if (dtype == Q36_MOE_FP8) go_tt(std::integral_constant<int, Q36_MOE_FP8>{});
   else go_tt(std::integral_constant<int, Q36_MOE_INT8>{});
