@@ -14,10 +14,11 @@
 //              and the row's argmax key reset to 0.
 //   lmh_gemm   persistent, one 512-thread workgroup per CU walking 256 x 256 output tiles (8 waves,
 //              two a SIMD, each 128 vocab rows x 64 tokens, 32x32x32 int8 MFMAs with the weights as
-//              operand A, int32 accumulators); K in 64-byte steps through a 4-stage LDS ring
-//              filled by buffer loads straight into LDS four steps ahead, fragments
-//              double-buffered in registers, and the next tile's first steps requested before the
-//              epilogue.  Epilogue: bf16 logits, the
+//              operand A, int32 accumulators); K in 64-byte steps through LDS rings filled by
+//              buffer loads straight into LDS (weights 6 stages, loaded by four waves six steps
+//              ahead; activations 3 stages, loaded by the other four), fragments double-buffered
+//              in registers, and the next tile's first steps requested before the epilogue.
+//              Epilogue: bf16 logits, the
 //              first column of each row's largest value folded into an order-preserving key, and one
 //              64-bit atomic max per row and tile: the result does not depend on the order the
 //              workgroups finish in.  lmh_gemm_logits: the same, writing the bf16 logits too.
@@ -36,6 +37,7 @@ namespace {
 constexpr int kLH = 2048;       // hidden (K)
 constexpr int kBM = 256, kBN = 256, kBK = 64, kNK = kLH / kBK;  // 32 K steps
 constexpr int kLmhWaves = 8;  // waves of the GEMM workgroup: two a SIMD
+constexpr int kNSA = 3, kNSB = 6;  // LDS ring stages of the activations and of the weights
 
 struct LmhDev {
   int R, V;
@@ -143,6 +145,11 @@ __device__ __forceinline__ int bswz(int c, int kc) { return c * kBK + ((kc ^ ((c
 
 template <int N>
 using ic = std::integral_constant<int, N>;
+// f(ic<0>{}), f(ic<1>{}), ... in order, each index a compile-time constant
+template <typename F, int... KS>
+__device__ __forceinline__ void for_steps(F&& f, std::integer_sequence<int, KS...>) {
+  (f(ic<KS>{}), ...);
+}
 
 // threadIdx.x through an empty asm: values derived from it are recomputed where they are used
 // instead of being kept (or spilled) across the K loop
@@ -169,44 +176,47 @@ __device__ __forceinline__ void wait_vm() {
 // XCD's activations (rpg row tiles, 2 MB at 2048 rows) stay resident in its L2 while the weights
 // stream through.
 //
-// Per tile, 32 K steps of 64 bytes through a 4-stage LDS ring filled by buffer loads straight into
-// LDS (no register staging).  Each wave owns a 128 x 128 block (32x32x32 int8 MFMAs, weights as
-// operand A, int32 accumulators in AGPRs) and keeps two register sets of fragments: while the 32
-// MFMAs of step ks run on one set, the 16 LDS reads of step ks + 1 fill the other and the loads of
-// step ks + 4 go out, so the matrix pipe never waits on LDS.  One barrier per step: before it, each
-// wave waits for its own loads of step ks + 1 and its LDS reads of step ks (the stage the loads of
-// step ks + 4 then overwrite).  The last step of a tile first issues the next tile's scales and its
-// first four K steps, so the epilogue runs while they land.
+// Per tile, 32 K steps of 64 bytes through two LDS rings filled by buffer loads straight into LDS
+// (no register staging): the weights' 6 stages, loaded by waves 0-3 six steps ahead, and the
+// activations' 3 stages (L2-resident), loaded by waves 4-7 three steps ahead.  Vector-memory loads
+// complete in order per wave, so a wave that loaded both operands could give neither a deeper
+// lookahead than the other; with one operand a wave, each ring has its own depth.  Each wave owns a
+// 128 x 64 block (32x32x32 int8 MFMAs, weights as operand A, int32 accumulators) and keeps two
+// register sets of fragments: while the 16 MFMAs of step ks run on one set, the 12 LDS reads of step
+// ks + 1 fill the other and the wave's loads of step ks + (6 or 3) go out.  One barrier per step:
+// before it, each wave waits for its own loads of step ks + 1 and its LDS reads of step ks (the
+// stages the loads issued after the barrier overwrite).  The next tile's scales and first steps go
+// out before the epilogue, so it runs while they land.  The LDS reads, 96 KB a step besides the
+// 32 KB the loads write, keep the matrix cores below full rate: the ring depth changes little.
 // row groups of XCDs (see lmh_gemm_body): two when there are at least 4 row tiles, evenly split
 __host__ __device__ __forceinline__ int lmh_groups(int nrt) { return nrt >= 4 && nrt % 2 == 0 ? 2 : 1; }
 
-// STORE: 0 no logits, 1 bf16 logits, 2 fp32 logits (the bf16-rounded values widened)
-template <int STORE, bool X2, int NW>
-__device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
+// LDS of the GEMM workgroup, declared once in the kernel and shared by both load roles
+struct LmhLds {
+  int8_t* a[kNSA];  // activation stages
+  int8_t* b[kNSB];  // weight stages
+  float (*sc)[2][kBN];
+  uint32_t (*rkey)[kBM];
+};
+
+// STORE: 0 no logits, 1 bf16 logits, 2 fp32 logits (the bf16-rounded values widened).  ROLE: the
+// loads this wave issues (0: weights, waves 0-3; 1: activations, waves 4-7); everything else is the
+// same in both.  Each role is its own instantiation, so the compiler's wait counting sees only the
+// wave's own operand in flight.
+template <int STORE, bool X2, int NW, int ROLE>
+__device__ __forceinline__ void lmh_gemm_body(const LmhDev& d, const LmhLds& L) {
   // NW waves: two vocab halves (wn) x NW / 2 token groups (wm); a wave owns 128 vocab columns (VB = 4
   // blocks of 32) x TW tokens (TB blocks of 32)
   constexpr int WM = NW / 2, TW = kBM / WM, TB = TW / 32, VB = 4;
-  constexpr int CPW = 16 / NW;            // 1 KB chunk pairs (A and B) a wave loads per step
-  constexpr int LPS = 2 * CPW;            // its loads per step
+  static_assert(NW == 8, "eight waves: four load each operand");
+  constexpr int CPL = 16 / (NW / 2);      // 1 KB chunks a wave loads per step (its operand only)
+  constexpr int NS = ROLE == 0 ? kNSB : kNSA;  // stages of its operand's ring: loads go NS steps ahead
   constexpr int NRD = 2 * TB + 2 * VB;    // its fragment reads per step
   constexpr int NMF = 2 * TB * VB;        // its MFMAs per step
-  // one object per LDS stage: the compiler tracks the buffer-to-LDS loads of each object apart
-  __shared__ __align__(1024) int8_t a_s0[kBM * kBK], a_s1[kBM * kBK], a_s2[kBM * kBK], a_s3[kBM * kBK];
-  __shared__ __align__(1024) int8_t b_s0[kBN * kBK], b_s1[kBN * kBK], b_s2[kBN * kBK], b_s3[kBN * kBK];
-  __shared__ __align__(16) float sc_l[2][2][kBN];  // [tile parity][weight scales | row scales]
-  __shared__ uint32_t rkey[2][kBM];  // [column wave][row of the tile] (two terms: [token of the tile])
-  auto a_st = [&](auto st) -> int8_t* {
-    if constexpr (decltype(st)::value == 0) return a_s0;
-    else if constexpr (decltype(st)::value == 1) return a_s1;
-    else if constexpr (decltype(st)::value == 2) return a_s2;
-    else return a_s3;
-  };
-  auto b_st = [&](auto st) -> int8_t* {
-    if constexpr (decltype(st)::value == 0) return b_s0;
-    else if constexpr (decltype(st)::value == 1) return b_s1;
-    else if constexpr (decltype(st)::value == 2) return b_s2;
-    else return b_s3;
-  };
+  auto a_st = [&](auto st) -> int8_t* { return L.a[decltype(st)::value]; };
+  auto b_st = [&](auto st) -> int8_t* { return L.b[decltype(st)::value]; };
+  float (*sc_l)[2][kBN] = L.sc;
+  uint32_t (*rkey)[kBM] = L.rkey;
   const int nvt = (d.V + kBN - 1) / kBN, nrt = (d.Rs + kBM - 1) / kBM;
   const int xcd = blockIdx.x & 7, loc = blockIdx.x >> 3, nloc = gridDim.x >> 3;
   const int ngrp = lmh_groups(nrt), rpg = nrt / ngrp, vstep = 8 / ngrp;
@@ -217,9 +227,10 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1;  // token group, vocab half
   const int wv = __builtin_amdgcn_readfirstlane(wave);
-  // Load i of wave w fills 1 KB chunk q = CPW w + i of a stage (tile rows 16 q .. 16 q + 15); lane l
-  // writes bytes 16 l .. 16 l + 15 of the chunk, which bswz assigns to row 16 q + l / 4, logical
-  // 16-byte chunk (l % 4) ^ ((l / 8) % 4) ^ (l / 32).  Rows past R or V read as zero (buffer bounds).
+  // Load i of a loading wave fills 1 KB chunk q = CPL (w % 4) + i of its operand's stage (tile rows
+  // 16 q .. 16 q + 15); lane l writes bytes 16 l .. 16 l + 15 of the chunk, which bswz assigns to row
+  // 16 q + l / 4, logical 16-byte chunk (l % 4) ^ ((l / 8) % 4) ^ (l / 32).  Rows past R or V read as
+  // zero (buffer bounds).
   const int voff = (lane >> 2) * kLH + (((lane & 3) ^ ((lane >> 3) & 3) ^ (lane >> 5)) << 4);
   struct Tile {
     int r0, v0;
@@ -237,17 +248,19 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   };
   // The row offset rides in the VGPR offset, the K offset in the SGPR offset: the buffer range
   // check covers only the former, so rows past the tile's last valid row read zero.
-  int vrow[CPW];
+  int vrow[CPL];
 #pragma unroll
-  for (int i = 0; i < CPW; ++i) vrow[i] = voff + (CPW * wv + i) * 16 * kLH;
-  // Both operands with the default cache policy: the four workgroups of a row group read each weight
-  // line in turn, and a streaming hint on the weights (measured) lets lines go before the last reader.
-  auto issue_to = [&](const Tile& t, int ks, int8_t* as, int8_t* bs, int i) {
-    const int q = wv * CPW + i;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(t.a, as + q * 1024, 16, vrow[i], ks * kBK, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(t.b, bs + q * 1024, 16, vrow[i], ks * kBK, 0, 0);
+  for (int i = 0; i < CPL; ++i) vrow[i] = voff + (CPL * (wv & 3) + i) * 16 * kLH;
+  auto issue_to = [&](const Tile& t, int ks, int8_t* s, int i) {
+    const int q = (wv & 3) * CPL + i;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ROLE == 0 ? t.b : t.a, s + q * 1024, 16, vrow[i], ks * kBK, 0, 0);
   };
-  auto issue_step = [&](const Tile& t, int ks, auto st, int i) { issue_to(t, ks, a_st(st), b_st(st), i); };
+  // load i of step KS (its stage KS % NS of the wave's operand)
+  auto issue_one = [&](const Tile& t, auto ksc, int i) {
+    constexpr int KS = decltype(ksc)::value;
+    if constexpr (ROLE == 0) issue_to(t, KS, b_st(ic<KS % kNSB>{}), i);
+    else issue_to(t, KS, a_st(ic<KS % kNSA>{}), i);
+  };
   // the tile's weight and row scales (wave w < 4: entries 64 w .. 64 w + 63 of each; past V or R: zero)
   auto issue_scales = [&](const Tile& t, int par) {
     if (wv >= 4) return;
@@ -267,9 +280,10 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   const int fw0 = bswz(wn * 128 + l32, lh), fw1 = bswz(wn * 128 + l32, 2 + lh);
   v16i acc[VB][TB];     // [vocab block][token block]
   v4i fx[2][2][TB], fw[2][2][VB];  // [register set][half step][block]
-  auto read_one = [&](auto st, auto fb, int k) {  // fragment k (0..NRD-1) of a step
-    const int8_t* as = a_st(st);
-    const int8_t* bs = b_st(st);
+  auto read_one = [&](auto ksc, auto fb, int k) {  // fragment k (0..NRD-1) of step KS
+    constexpr int KS = decltype(ksc)::value;
+    const int8_t* as = a_st(ic<KS % kNSA>{});
+    const int8_t* bs = b_st(ic<KS % kNSB>{});
     constexpr int f = decltype(fb)::value;
     if (k < 2 * TB) {
       const int h = k / TB, t = k % TB;
@@ -285,71 +299,55 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     acc[vi][ti] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
         fw[f][h][vi], fx[f][h][ti], (decltype(first)::value && h == 0) ? v16i{} : acc[vi][ti], 0, 0, 0);
   };
-  // Step ks on register set FB (already read).  WAITN: this wave's loads allowed in flight once
-  // step ks + 1 has landed (16 in the steady state; 8 and 0 over the last steps, which load
-  // nothing).  LOADS: issue step ks + 4 into stage ks % 4.  NEXT: read step ks + 1 into the other set.
-  auto step = [&](const Tile& t, int ks, auto cur, auto fb, auto first, auto waitn, auto loads, auto next) {
-    wait_vm<decltype(waitn)::value>();
+  // Step KS on register set KS % 2 (read during step KS - 1).  At its top the wave waits for its own
+  // loads of step KS + 1: only those of steps KS + 2 .. KS + NS - 1 were issued after them (loads
+  // complete in order; the previous tile's epilogue stores and atomics still in flight only lengthen
+  // the wait), then one barrier makes every wave's loads of step KS + 1 visible and every wave's reads
+  // of step KS complete, so the loads of step KS + NS may overwrite the stage step KS used.
+  auto step = [&](const Tile& t, auto ksc) {
+    constexpr int KS = decltype(ksc)::value;
+    if constexpr (KS + 1 < kNK) {
+      constexpr int later = (KS + NS - 1 < kNK - 1 ? KS + NS - 1 : kNK - 1) - (KS + 1);
+      wait_vm<(later > 0 ? later : 0) * CPL>();
+    }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    using nb = ic<1 - decltype(fb)::value>;
-    using nst = ic<(decltype(cur)::value + 1) & 3>;
+    using fb = ic<KS & 1>;
+    using nb = ic<(KS + 1) & 1>;
+    using first = std::integral_constant<bool, KS == 0>;
 #pragma unroll
     for (int k = 0; k < NMF; ++k) {
-      mfma_one(fb, first, k);
-      if constexpr (decltype(next)::value)
-        if (k < NRD) read_one(nst{}, nb{}, k);
-      if constexpr (decltype(loads)::value)
-        if (k >= NMF / 2 && k < NMF / 2 + CPW) issue_step(t, ks + 4, cur, k - NMF / 2);
+      mfma_one(fb{}, first{}, k);
+      if constexpr (KS + 1 < kNK)
+        if (k < NRD) read_one(ic<KS + 1>{}, nb{}, k);
+      if constexpr (KS + NS < kNK)
+        if (k >= NMF / 2 && k < NMF / 2 + CPL) issue_one(t, ic<KS + NS>{}, k - NMF / 2);
       __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  auto prologue = [&](const Tile& t) {
+    for_steps([&](auto sc) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) issue_one(t, sc, i);
+    }, std::make_integer_sequence<int, NS>{});
   };
   int par = 0;
   Tile t = tile(j);
   issue_scales(t, 0);
-#pragma unroll
-  for (int i = 0; i < CPW; ++i) issue_step(t, 0, ic<0>{}, i);
-#pragma unroll
-  for (int i = 0; i < CPW; ++i) issue_step(t, 1, ic<1>{}, i);
-#pragma unroll
-  for (int i = 0; i < CPW; ++i) issue_step(t, 2, ic<2>{}, i);
-#pragma unroll
-  for (int i = 0; i < CPW; ++i) issue_step(t, 3, ic<3>{}, i);
-  using T_ = std::true_type;
-  using F_ = std::false_type;
+  prologue(t);
   for (;;) {
-    // step 0 of this tile: the oldest loads in flight but for its scales when they went out first
-    // (the epilogue's row atomic, and with two terms the scales, go out after steps 0-3, and the
-    // atomic may finish first: with at most 3 LPS - 1 left, every load of step 0 has landed)
-    if constexpr (STORE) wait_vm<0>(); else wait_vm<3 * LPS - 1>();
+    // step 0 of this tile has landed: only steps 1 .. NS - 1 of the wave's operand went out after it
+    wait_vm<(NS - 1) * CPL>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int k = 0; k < NRD; ++k) read_one(ic<0>{}, ic<0>{}, k);
-    using W2 = ic<2 * LPS>;
-    step(t, 0, ic<0>{}, ic<0>{}, T_{}, W2{}, T_{}, T_{});
-    step(t, 1, ic<1>{}, ic<1>{}, F_{}, W2{}, T_{}, T_{});
-    step(t, 2, ic<2>{}, ic<0>{}, F_{}, W2{}, T_{}, T_{});
-    step(t, 3, ic<3>{}, ic<1>{}, F_{}, W2{}, T_{}, T_{});
-    for (int ks = 4; ks < kNK - 4; ks += 4) {
-      step(t, ks, ic<0>{}, ic<0>{}, F_{}, W2{}, T_{}, T_{});
-      step(t, ks + 1, ic<1>{}, ic<1>{}, F_{}, W2{}, T_{}, T_{});
-      step(t, ks + 2, ic<2>{}, ic<0>{}, F_{}, W2{}, T_{}, T_{});
-      step(t, ks + 3, ic<3>{}, ic<1>{}, F_{}, W2{}, T_{}, T_{});
-    }
-    step(t, kNK - 4, ic<0>{}, ic<0>{}, F_{}, W2{}, F_{}, T_{});
-    step(t, kNK - 3, ic<1>{}, ic<1>{}, F_{}, ic<LPS>{}, F_{}, T_{});
-    step(t, kNK - 2, ic<2>{}, ic<0>{}, F_{}, ic<0>{}, F_{}, T_{});
-    // last step: once every wave has read the ring, the next tile's loads go out first
+    for_steps([&](auto sc) { step(t, sc); }, std::make_integer_sequence<int, kNK>{});
+    // every wave is past the last step's barrier: no wave reads the ring any more
     j += nloc;
     const bool more = vt_of(j) < nvt;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
     const Tile tn = more ? tile(j) : t;
-#pragma unroll
-    for (int k = 0; k < NMF; ++k) mfma_one(ic<1>{}, F_{}, k);
     // The lane's indices are derived afresh from the thread id here: values computed before the K
     // loop and kept across it were spilled (the loop holds 224 of the 256 registers), and their
     // reloads, queued behind the next tile's loads, held the epilogue until those loads landed.
@@ -382,14 +380,7 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
     }
     if (more) {
       if constexpr (kRegScales) issue_scales(tn, par ^ 1);
-#pragma unroll
-      for (int i = 0; i < CPW; ++i) issue_step(tn, 0, ic<0>{}, i);
-#pragma unroll
-      for (int i = 0; i < CPW; ++i) issue_step(tn, 1, ic<1>{}, i);
-#pragma unroll
-      for (int i = 0; i < CPW; ++i) issue_step(tn, 2, ic<2>{}, i);
-#pragma unroll
-      for (int i = 0; i < CPW; ++i) issue_step(tn, 3, ic<3>{}, i);
+      prologue(tn);
     }
     asm volatile("" ::: "memory");
     // Epilogue: lane l holds tokens r0 + wm*TW + 32 ti + l % 32 and, per token, vocab columns
@@ -472,16 +463,34 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d) {
   }
 }
 
+// The GEMM's LDS: kNSA activation and kNSB weight stages, the scales and the row keys
+#define LMH_GEMM_LDS                                                                                  \
+  __shared__ __align__(1024) int8_t a_s0[kBM * kBK], a_s1[kBM * kBK], a_s2[kBM * kBK];               \
+  __shared__ __align__(1024) int8_t b_s0[kBN * kBK], b_s1[kBN * kBK], b_s2[kBN * kBK], b_s3[kBN * kBK], \
+      b_s4[kBN * kBK], b_s5[kBN * kBK];                                                               \
+  __shared__ __align__(16) float sc_l[2][2][kBN];                                                     \
+  __shared__ uint32_t rkey[2][kBM];                                                                   \
+  static_assert(kNSA == 3 && kNSB == 6, "the stage arrays above");                                   \
+  const LmhLds L{{a_s0, a_s1, a_s2}, {b_s0, b_s1, b_s2, b_s3, b_s4, b_s5}, sc_l, rkey};
+
 template <bool X2>
 __global__ __launch_bounds__(64 * kLmhWaves) __attribute__((amdgpu_waves_per_eu(kLmhWaves / 4, kLmhWaves / 4))) void
 lmh_gemm_kernel(LmhDev d) {
-  lmh_gemm_body<0, X2, kLmhWaves>(d);
+  LMH_GEMM_LDS
+  if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) < kLmhWaves / 2)
+    lmh_gemm_body<0, X2, kLmhWaves, 0>(d, L);
+  else
+    lmh_gemm_body<0, X2, kLmhWaves, 1>(d, L);
 }
 // the same with the logits written out (F32: as fp32)
 template <bool X2, bool F32>
 __global__ __launch_bounds__(64 * kLmhWaves) __attribute__((amdgpu_waves_per_eu(kLmhWaves / 4, kLmhWaves / 4))) void
 lmh_gemm_logits_kernel(LmhDev d) {
-  lmh_gemm_body<F32 ? 2 : 1, X2, kLmhWaves>(d);
+  LMH_GEMM_LDS
+  if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) < kLmhWaves / 2)
+    lmh_gemm_body<F32 ? 2 : 1, X2, kLmhWaves, 0>(d, L);
+  else
+    lmh_gemm_body<F32 ? 2 : 1, X2, kLmhWaves, 1>(d, L);
 }
 
 __global__ __launch_bounds__(256) void lmh_ids_kernel(LmhDev d) {
