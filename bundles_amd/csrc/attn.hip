@@ -393,9 +393,11 @@ ks_gemm_kernel(GemmDev g) {
 // order (the weights as packed, the activations from act_quant's fragment mode).
 // Workgroup = one 128-row block (one weight scale per K block) x BT tokens, 8 waves, two a SIMD:
 // wave w owns row tiles 4 (w & 1) .. +3 and token tiles TTW (w >> 1) .. +TTW-1 (TTW = BT / 64).  K
-// goes in 128-byte steps (one K block, one MFMA deep) through a 4-stage LDS ring that buffer loads
-// fill straight from global memory, four steps ahead; a stage holds the block's 8 weight tiles and
-// BT / 16 token tiles, 2 KB each, exactly as they lie in memory.  The fragments (and scales) of step
+// goes in 128-byte steps (one K block, one MFMA deep) through two LDS rings that buffer loads fill
+// straight from global memory: the block's 8 weight tiles (6 stages, copied by waves 0-3 six steps
+// ahead) and the BT / 16 token tiles (3 stages, L2-resident, copied by waves 4-7), 2 KB a tile,
+// exactly as they lie in memory.  Vector-memory loads complete in order per wave, so one operand a
+// wave lets each ring have its own depth.  The fragments (and scales) of step
 // s + 1 are read while the MFMAs of step s run.  Per call every weight byte passes through L2
 // ceil(T / BT) times and every activation byte N / 128 times (the streaming GEMM's 16- or 32-token
 // groups re-read the weights T / 16 or T / 32 times).
@@ -413,29 +415,29 @@ template <typename F, int... KS>
 __device__ __forceinline__ void for_steps(F& f, std::integer_sequence<int, KS...>) {
   (f(ic<KS>{}), ...);
 }
+constexpr int kTileNSW = 6, kTileNSA = 3;  // LDS ring stages of the weight tiles and of the token tiles
 template <int BT, int NKB>
-__device__ __forceinline__ void tile_gemm_body(const GemmDev& g) {
-  constexpr int WB = 8 * 2048, AB = (BT / 16) * 2048;  // stage bytes: weight tiles, token tiles
-  constexpr int NCH = (WB + AB) / 1024, LPS = NCH / 8;  // 1 KB copies a stage, per wave
+struct TileLds {
+  static constexpr int WB = 8 * 2048, AB = (BT / 16) * 2048;  // stage bytes: weight tiles, token tiles
+  uint8_t* w[kTileNSW];
+  uint8_t* a[kTileNSA];
+  float* xs;  // [NKB][BT]
+  float* ws;  // [NKB]
+};
+// ROLE: the copies this wave issues (0: the weight tiles, waves 0-3; 1: the token tiles, waves 4-7);
+// everything else is the same in both.  Each role is its own instantiation, so the compiler's wait
+// counting sees only the wave's own operand in flight.
+template <int BT, int NKB, int ROLE>
+__device__ __forceinline__ void tile_gemm_body(const GemmDev& g, const TileLds<BT, NKB>& L) {
+  constexpr int WB = TileLds<BT, NKB>::WB, AB = TileLds<BT, NKB>::AB;
+  constexpr int CP = (ROLE == 0 ? WB : AB) / 1024 / 4;  // 1 KB copies a wave issues per step
+  constexpr int NS = ROLE == 0 ? kTileNSW : kTileNSA;  // stages of its operand's ring
   constexpr int TTW = BT / 64;
-  static_assert(NCH % 8 == 0 && NKB >= 4 && TTW >= 1, "tile shape");
-  // one object per stage and operand: the compiler tracks the buffer-to-LDS loads of each apart
-  __shared__ __align__(1024) uint8_t w_s0[WB], w_s1[WB], w_s2[WB], w_s3[WB];
-  __shared__ __align__(1024) uint8_t a_s0[AB], a_s1[AB], a_s2[AB], a_s3[AB];
-  __shared__ __align__(16) float xs_l[NKB * BT];  // [kb][token of the tile]
-  __shared__ float ws_l[NKB];
-  auto w_st = [&](auto st) -> uint8_t* {
-    if constexpr (decltype(st)::value == 0) return w_s0;
-    else if constexpr (decltype(st)::value == 1) return w_s1;
-    else if constexpr (decltype(st)::value == 2) return w_s2;
-    else return w_s3;
-  };
-  auto a_st = [&](auto st) -> uint8_t* {
-    if constexpr (decltype(st)::value == 0) return a_s0;
-    else if constexpr (decltype(st)::value == 1) return a_s1;
-    else if constexpr (decltype(st)::value == 2) return a_s2;
-    else return a_s3;
-  };
+  static_assert(CP >= 1 && NKB >= kTileNSW && TTW >= 1, "tile shape");
+  auto w_st = [&](auto st) -> uint8_t* { return L.w[decltype(st)::value]; };
+  auto a_st = [&](auto st) -> uint8_t* { return L.a[decltype(st)::value]; };
+  float* const xs_l = L.xs;
+  float* const ws_l = L.ws;
   // XCD-aware order: workgroup b runs on XCD b % 8, which owns the row blocks rb = xcd (mod 8) with
   // every token group of each, so a weight block is fetched into one L2 for all its token groups
   const int nrb = g.N / 128, ntg = (g.T + BT - 1) / BT;
@@ -452,21 +454,18 @@ __device__ __forceinline__ void tile_gemm_body(const GemmDev& g) {
       (void*)(g.W + (size_t)rb * 8 * NKB * 2048), (short)0, 8 * NKB * 2048, 0x00020000);
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(g.A + (size_t)(t0 >> 4) * NKB * 2048), (short)0, ntile * NKB * 2048, 0x00020000);
-  // copy i of this wave for step ks: 1 KB chunk q = LPS w + i of the stage (weight tile q / 2 half
-  // q % 2, then the token tiles' halves)
-  auto dma = [&](bool wpart, uint8_t* lds, int voff, int soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(wpart ? wrs : ars, lds, 16, voff, soff, 0, 0);
-  };
-  auto issue = [&](auto st, int ks) {
+  // copy i of step ks: 1 KB chunk q = CP (w % 4) + i of the wave's operand's stage (tile q / 2,
+  // half q % 2)
+  auto issue = [&](auto ksc) {
+    constexpr int ks = decltype(ksc)::value;
 #pragma unroll
-    for (int i = 0; i < LPS; ++i) {
-      const int q = wv * LPS + i;
-      if (q < 16) {
-        dma(true, w_st(st) + q * 1024, lane * 16 + (q >> 1) * NKB * 2048 + (q & 1) * 1024, ks * 2048);
-      } else {
-        const int qa = q - 16;
-        dma(false, a_st(st) + qa * 1024, lane * 16 + (qa >> 1) * NKB * 2048 + (qa & 1) * 1024, ks * 2048);
-      }
+    for (int i = 0; i < CP; ++i) {
+      const int q = (wv & 3) * CP + i;
+      const int voff = lane * 16 + (q >> 1) * NKB * 2048 + (q & 1) * 1024;
+      if constexpr (ROLE == 0)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, w_st(ic<ks % kTileNSW>{}) + q * 1024, 16, voff, ks * 2048, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, a_st(ic<ks % kTileNSA>{}) + q * 1024, 16, voff, ks * 2048, 0, 0);
     }
   };
   // the group's scales: activations [NKB][BT] and the block's weight scales, through registers
@@ -481,11 +480,9 @@ __device__ __forceinline__ void tile_gemm_body(const GemmDev& g) {
     xsr[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, off, 0, 0));
   }
   const float wsv = tid < NKB ? g.Ws[(size_t)rb * NKB + tid] : 0.f;
-  issue(ic<0>{}, 0);
-  issue(ic<1>{}, 1);
-  issue(ic<2>{}, 2);
-  issue(ic<3>{}, 3);
-  tg_wait_vm<3 * LPS>();  // the scales and step 0
+  auto issue_one = [&](auto sc) { issue(sc); };
+  for_steps(issue_one, std::make_integer_sequence<int, NS>{});
+  tg_wait_vm<(NS - 1) * CP>();  // the scales and step 0 (the wave's loads complete in order)
 #pragma unroll
   for (int q = 0; q < NXS; ++q) xs_l[tid + 512 * q] = xsr[q];
   if (tid < NKB) ws_l[tid] = wsv;
@@ -500,10 +497,10 @@ __device__ __forceinline__ void tile_gemm_body(const GemmDev& g) {
   v8i wf[2][4], af[2][TTW];
   float xw[2][TTW];
   const int lo = lane * 16;
-  auto read_frags = [&](auto st, auto fb, int ks) {
-    constexpr int f = decltype(fb)::value;
-    const uint8_t* wsp = w_st(st);
-    const uint8_t* asp = a_st(st);
+  auto read_frags = [&](auto ksc, auto fb) {
+    constexpr int ks = decltype(ksc)::value, f = decltype(fb)::value;
+    const uint8_t* wsp = w_st(ic<ks % kTileNSW>{});
+    const uint8_t* asp = a_st(ic<ks % kTileNSA>{});
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       const uint8_t* p = wsp + (4 * wr + rt) * 2048 + lo;
@@ -518,21 +515,20 @@ __device__ __forceinline__ void tile_gemm_body(const GemmDev& g) {
 #pragma unroll
     for (int tt = 0; tt < TTW; ++tt) xw[f][tt] = xs_l[ks * BT + (TTW * wt + tt) * 16 + (lane & 15)] * wsk;
   };
-  read_frags(ic<0>{}, ic<0>{}, 0);
+  read_frags(ic<0>{}, ic<0>{});
   auto step = [&](auto ksc) {
     constexpr int ks = decltype(ksc)::value, f = ks & 1;
-    // this wave's copies of step ks + 1 have landed (those of ks + 2 and ks + 3 may fly), its reads
-    // of step ks are done, and after the barrier every wave's are: stage ks % 4 is free
-    constexpr int ahead = NKB - 2 - ks;
-    tg_wait_vm<LPS * (ahead >= 2 ? 2 : ahead > 0 ? ahead : 0)>();
+    // this wave's copies of step ks + 1 have landed (only those of steps ks + 2 .. ks + NS - 1 went
+    // out after them), its reads of step ks are done, and after the barrier every wave's are: the
+    // stage step ks used is free
+    constexpr int later = (ks + NS - 1 < NKB - 1 ? ks + NS - 1 : NKB - 1) - (ks + 1);
+    tg_wait_vm<CP * (later > 0 ? later : 0)>();
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    using cur = ic<ks % 4>;
-    using nxt = ic<(ks + 1) % 4>;
     using nfb = ic<1 - f>;
-    if constexpr (ks + 4 < NKB) issue(cur{}, ks + 4);
-    if constexpr (ks + 1 < NKB) read_frags(nxt{}, nfb{}, ks + 1);
+    if constexpr (ks + NS < NKB) issue(ic<ks + NS>{});
+    if constexpr (ks + 1 < NKB) read_frags(ic<ks + 1>{}, nfb{});
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
@@ -572,7 +568,18 @@ __device__ __forceinline__ void tile_gemm_body(const GemmDev& g) {
 
 template <int BT, int NKB>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void tile_gemm_kernel(GemmDev g) {
-  tile_gemm_body<BT, NKB>(g);
+  // one object per stage and operand: the compiler tracks the buffer-to-LDS loads of each apart
+  constexpr int WB = TileLds<BT, NKB>::WB, AB = TileLds<BT, NKB>::AB;
+  static_assert(kTileNSW == 6 && kTileNSA == 3, "the stage arrays below");
+  __shared__ __align__(1024) uint8_t w_s0[WB], w_s1[WB], w_s2[WB], w_s3[WB], w_s4[WB], w_s5[WB];
+  __shared__ __align__(1024) uint8_t a_s0[AB], a_s1[AB], a_s2[AB];
+  __shared__ __align__(16) float xs_l[NKB * BT];  // [kb][token of the tile]
+  __shared__ float ws_l[NKB];
+  const TileLds<BT, NKB> L{{w_s0, w_s1, w_s2, w_s3, w_s4, w_s5}, {a_s0, a_s1, a_s2}, xs_l, ws_l};
+  if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) < 4)
+    tile_gemm_body<BT, NKB, 0>(g, L);
+  else
+    tile_gemm_body<BT, NKB, 1>(g, L);
 }
 
 // ------------------------------------------------------------------------------------------
