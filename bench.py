@@ -169,7 +169,9 @@ def bench_small(args, torch, dev):
       moe_m{1,4,8,16}   the fp8 MoE layer (config 2 shapes, Zipf router), 8 layers cycled in one graph
       dense8_*          the DENSE8 W8A16 projections of the recurrent block: in_proj [12352, 2048]
                         (12 copies cycled) and out_proj / o_proj [2048, 4096] (36 copies)
-      lmhead_w8a16      the int8 lm_head [151936, 2048] in its W8A16 form + argmax (2 copies)
+      lmhead_w8a16      the int8 lm_head [151936, 2048] in its W8A16 form + argmax (2 copies), the
+                        codes in the kernel's tile order as the logits node keeps them (us_row_major:
+                        the same calls on the row-major codes)
     Each dense / lm_head point is a graph of one call per copy, replayed; per call."""
     from bundles_amd import synth
     from bundles_amd.qwen36_layer import formats, glue
@@ -229,18 +231,23 @@ def bench_small(args, torch, dev):
     heads = []
     for c in range(2):
         d = synth.lmhead_inputs(32, V, dev, seed=50 + c)
-        heads.append(lmhead8.quantize_rows(d["w"]))
+        q, s = lmhead8.quantize_rows(d["w"])
+        heads.append((q, s, lmhead8.tile_rows_w16(q)))  # the logits node keeps the tile-order copy too
         del d["w"]
     wsl = lmhead8.Workspace(32, dev)
     pts = {}
     for R in (1, 4, 16, 32):
         h = torch.randn((R, 2048), generator=gen, device=dev).to(torch.bfloat16)
         ids = torch.empty(R, dtype=torch.int32, device=dev)
-        calls = [lambda q=q, s=s: lmhead8.w8a8_lmhead_argmax(h, q, s, wsl, ids=ids, w8a16=True) for q, s in heads]
+        calls = [lambda q=q, s=s, qt=qt: lmhead8.w8a8_lmhead_argmax(h, q, s, wsl, ids=ids, w8a16=True, q_w16=qt)
+                 for q, s, qt in heads]
         ms = graph_time(calls)
+        ms_rm = graph_time([lambda q=q, s=s: lmhead8.w8a8_lmhead_argmax(h, q, s, wsl, ids=ids, w8a16=True)
+                            for q, s, _ in heads])
         algo = V * 2048 + V * 4 + R * 2048 * 2 + R * 4
         pts[f"r{R}"] = dict(us=round(ms * 1e3, 2), bytes=algo, gbs=round(algo / (ms * 1e-3) / 1e9, 1),
-                            frac_hbm=round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+                            frac_hbm=round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                            us_row_major=round(ms_rm * 1e3, 2))
     res["lmhead_w8a16"] = dict(vocab=V, copies_cycled=2, **pts)
     print("bench: W8A16 lm_head done", file=sys.stderr, flush=True)
     del heads

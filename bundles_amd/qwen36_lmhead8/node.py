@@ -129,6 +129,7 @@ class HeadCopy:
     q: torch.Tensor        # int8 [V, 2048]
     scale: torch.Tensor    # fp32 [V]
     ident: tuple           # (storage pointer, shape, device, version) of the weight it was built from
+    q16: torch.Tensor | None = None  # q in the W8A16 kernel's tile order, made at the first W8A16 call
 
     @staticmethod
     def ident_of(w: torch.Tensor) -> tuple:
@@ -183,8 +184,11 @@ class LogitsNode:
         buf = self.out_buf
         out = (buf if buf is not None and rows >= LOGITS_BUF_MIN_ROWS and tuple(buf.shape) == (rows, vocab)
                and vocab == getattr(self.processor, "vocab_size", -1) and buf.device == weight.device else None)
+        if mode == "w8a16" and hc.q16 is None and not torch.cuda.is_current_stream_capturing():
+            hc.q16 = lmhead8.tile_rows_w16(hc.q)  # a second copy of the codes (V x 2048 bytes)
         ids, logits = lmhead8.w8a8_lmhead_argmax(h.contiguous(), hc.q, hc.scale, ws, want_logits=True, logits=out,
-                                                 two_term=mode == "two_term", w8a16=mode == "w8a16")
+                                                 two_term=mode == "two_term", w8a16=mode == "w8a16",
+                                                 q_w16=hc.q16 if mode == "w8a16" else None)
         self.last_ids = ids
         return logits
 

@@ -35,7 +35,7 @@ def test_every_declared_symbol_is_exported(L):
         assert hasattr(L, n), f"{n} declared in q36_abi.h but not exported"
     bound = {s[0] for s in _lib.SYMBOLS}
     assert set(names) <= bound, f"not bound in _lib.SYMBOLS: {set(names) - bound}"
-    assert L.q36_abi_version() == 6
+    assert L.q36_abi_version() == 7
 
 
 def test_struct_layouts_match_header(tmp_path):

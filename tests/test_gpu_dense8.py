@@ -104,6 +104,32 @@ def test_lmhead_w8a16_vs_oracle(mods, oracle_mod, dev, R, V, norm):
     assert agree >= 0.9, f"ids agree on {agree:.2f} of the rows"
 
 
+@pytest.mark.parametrize("R,V,norm", [(1, 151936, True), (16, 8192, False), (24, 8192, True), (37, 4128, True),
+                                      (64, 4096, False)])
+def test_lmhead_w8a16_tiled_copy_same_bits(mods, dev, R, V, norm):
+    """The W8A16 lm_head on the tile-order copy (tile_rows_w16, what the logits node keeps) gives the
+    row-major codes' ids and bf16 logits bit for bit, across the 32- and 64-row wave shapes; the copy
+    is the stated permutation (a torch reshape of the same definition); q_w16 is refused outside W8A16."""
+    from bundles_amd import synth
+    _, _, lmh = mods
+    print(f"lmhead W8A16 tiled R={R} V={V} norm={norm}", flush=True)
+    d = synth.lmhead_inputs(R, V, dev, seed=3 * R + V)
+    q, s = lmh.quantize_rows(d["w"])
+    qt = lmh.tile_rows_w16(q)
+    ws = lmh.Workspace(R, dev)
+    nw = d["norm_w"] if norm else None
+    ids, logits = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=nw, eps=1e-6, want_logits=True, w8a16=True)
+    ids2, logits2 = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=nw, eps=1e-6, want_logits=True, w8a16=True,
+                                           q_w16=qt)
+    torch.cuda.synchronize()
+    want = q.view(V // 16, 16, 2048 // 64, 4, 16).permute(0, 2, 3, 1, 4).reshape(V, 2048)
+    assert torch.equal(qt, want), "tile order"
+    assert torch.equal(ids, ids2)
+    assert torch.equal(logits.view(torch.int16), logits2.view(torch.int16))
+    with pytest.raises(ValueError):
+        lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, q_w16=qt)
+
+
 @pytest.mark.parametrize("T,N,K", [(1, 12352, 2048), (16, 2048, 4096), (37, 384, 2048)])
 def test_dense8_tiled_copy_same_bits(dev, T, N, K):
     """formats.tile_w16 is the stated permutation of the rows (checked against a torch reshape of the
