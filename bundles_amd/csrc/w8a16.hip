@@ -61,7 +61,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8a16_kernel(W16Dev d) {
   constexpr int RG = WAVES / KS;
   constexpr int RW = 16 * RT;      // rows per wave
   // steps in flight: weights, activations (and mode 1's group scales); four token tiles hold half as many
-  constexpr int D = NTT >= 4 ? kDepth / 2 : kDepth;
+  constexpr int D = NTT >= 4 || RT >= 8 ? kDepth / 2 : kDepth;
   constexpr int NACC = RT * NTT * 4;
   __shared__ float red[KS > 1 ? WAVES - RG : 1][KS > 1 ? NACC : 1][KS > 1 ? 64 : 1];
   __shared__ uint32_t rkey[MODE == 0 ? RG : 1][64];
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(64 * WAVES) void w8a16_kernel(W16Dev d) {
 
 // The launch shape: token tiles NTT (T <= 16 NTT), row tiles per wave RT, K split KS, waves per
 // workgroup WAVES.  Every shape the policy can pick is instantiated here.
-#define Q36_W16_SHAPES_0(X) X(1, 2, 1, 4) X(1, 4, 1, 2) X(2, 4, 1, 2) X(4, 2, 1, 4)
+#define Q36_W16_SHAPES_0(X) X(1, 2, 1, 4) X(1, 4, 1, 2) X(2, 2, 1, 4) X(2, 4, 1, 2) X(2, 8, 1, 2) X(4, 2, 1, 4) X(4, 4, 1, 2)
 #define Q36_W16_SHAPES_1(X) \
   X(1, 2, 4, 8) X(2, 2, 4, 8) X(4, 2, 4, 8) \
   X(1, 1, 8, 8) X(2, 1, 8, 8) X(4, 1, 8, 8)
@@ -281,16 +281,22 @@ struct W16Shape {
   int ntt, rt, ks, waves;
 };
 
-// Measured on MI355X over T = 4..64: the lm_head (N in the 100 000s) streams whole rows, 32 a wave in
-// four-wave workgroups up to 8 tokens; from 9 tokens on 64 a wave in two-wave workgroups, so each
-// activation fragment a wave reads from L2 serves twice the weight rows (16 tokens 95 -> 90 us, 32
-// tokens 125 -> 115 us; at 1-4 tokens the wider waves leave too few loads in flight: 77 -> 84 us).
+// Measured on MI355X (the lm_head, N = 151936, codes in the tile order, graph-timed): the lm_head
+// streams whole rows, 32 a wave in four-wave workgroups up to 8 tokens (61 us; 64-row waves 63 us,
+// too few loads in flight); from 9 tokens on the activation fragments each wave reads from L2 weigh
+// more, so wider waves serve more weight rows with each: 64 rows a wave in two-wave workgroups up to
+// 24 tokens (16: 62.7 against 66.1 us), 128 rows from 25 to 32 tokens (32: 73.6 against 78.0 us), and
+// 64 rows with four token tiles (48: 99 against 138 us for 32-row waves, 63: 112 against 160 us).
 // The projections split K so that every CU has waves: in quarters for the 9216- and 12352-row
 // in_proj / qkv, in eighths for the 2048-row o_proj / out_proj.
 W16Shape w16_shape(const W16Dev& d, int mode) {
   const int ntt = d.T <= 16 ? 1 : d.T <= 32 ? 2 : 4;
-  // (the wider waves need N % 64 == 0: a wave's rows are all in or all out)
-  if (mode == 0) return ntt == 4 || d.T <= 8 || d.N % 64 != 0 ? W16Shape{ntt, 2, 1, 4} : W16Shape{ntt, 4, 1, 2};
+  // (a wave's rows are all in or all out: 64-row waves need N % 64 == 0, 128-row waves N % 128 == 0)
+  if (mode == 0) {
+    if (d.T <= 8 || d.N % 64 != 0) return W16Shape{ntt, 2, 1, 4};
+    if (ntt == 2 && d.T > 24 && d.N % 128 == 0) return W16Shape{ntt, 8, 1, 2};
+    return W16Shape{ntt, 4, 1, 2};
+  }
   return d.N >= 8192 ? W16Shape{ntt, 2, 4, 8} : W16Shape{ntt, 1, 8, 8};
 }
 

@@ -76,9 +76,11 @@ def test_dense8_linear_rejects_bad_shapes(mods, dev):
         glue.dense8_linear(torch.zeros((4, 1024), dtype=torch.bfloat16, device=dev), q, s)
 
 
-# 1-8 rows take 32-row waves, 9-32 rows 64-row waves when V % 64 == 0 (4128 is not: 32-row waves)
+# 1-8 rows take 32-row waves; 9-24 rows and 33-64 rows 64-row waves when V % 64 == 0 (4128 is not:
+# 32-row waves); 25-32 rows 128-row waves when V % 128 == 0 (4160 is not: 64-row waves)
 @pytest.mark.parametrize("R,V,norm", [(1, 4096, True), (16, 151936, True), (24, 8192, True), (12, 4128, False),
-                                      (37, 8192, False), (64, 4096, True)])
+                                      (37, 8192, False), (64, 4096, True), (32, 8192, True), (29, 4160, False),
+                                      (48, 4128, True)])
 def test_lmhead_w8a16_vs_oracle(mods, oracle_mod, dev, R, V, norm):
     from bundles_amd import synth
     _, _, lmh = mods
@@ -105,10 +107,10 @@ def test_lmhead_w8a16_vs_oracle(mods, oracle_mod, dev, R, V, norm):
 
 
 @pytest.mark.parametrize("R,V,norm", [(1, 151936, True), (16, 8192, False), (24, 8192, True), (37, 4128, True),
-                                      (64, 4096, False)])
+                                      (64, 4096, False), (32, 151936, True), (48, 8192, False)])
 def test_lmhead_w8a16_tiled_copy_same_bits(mods, dev, R, V, norm):
     """The W8A16 lm_head on the tile-order copy (tile_rows_w16, what the logits node keeps) gives the
-    row-major codes' ids and bf16 logits bit for bit, across the 32- and 64-row wave shapes; the copy
+    row-major codes' ids and bf16 logits bit for bit, across the 32-, 64- and 128-row wave shapes; the copy
     is the stated permutation (a torch reshape of the same definition); q_w16 is refused outside W8A16."""
     from bundles_amd import synth
     _, _, lmh = mods
