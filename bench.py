@@ -239,7 +239,7 @@ def bench_small(args, torch, dev):
     for R in (1, 4, 16, 32):
         h = torch.randn((R, 2048), generator=gen, device=dev).to(torch.bfloat16)
         ids = torch.empty(R, dtype=torch.int32, device=dev)
-        calls = [lambda q=q, s=s, qt=qt: lmhead8.w8a8_lmhead_argmax(h, q, s, wsl, ids=ids, w8a16=True, q_w16=qt)
+        calls = [lambda s=s, qt=qt: lmhead8.w8a8_lmhead_argmax(h, None, s, wsl, ids=ids, w8a16=True, q_t=qt)
                  for q, s, qt in heads]
         ms = graph_time(calls)
         ms_rm = graph_time([lambda q=q, s=s: lmhead8.w8a8_lmhead_argmax(h, q, s, wsl, ids=ids, w8a16=True)
@@ -534,19 +534,26 @@ def bench_lmhead(args, torch, dev):
     R, V = 2048, 151936
     d = synth.lmhead_inputs(R, V, dev, seed=0)
     q, s = lmhead8.quantize_rows(d["w"])
+    qt = lmhead8.tile_rows_w16(q)  # the codes in the tile order, as the logits node keeps them
     del d["w"]
     ws = lmhead8.Workspace(R, dev)
     ids = torch.empty(R, dtype=torch.int32, device=dev)
 
     def step():
+        lmhead8.w8a8_lmhead_argmax(d["h"], None, s, ws, norm_w=d["norm_w"], eps=1e-6, ids=ids, q_t=qt)
+
+    def step_rm():
         lmhead8.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=d["norm_w"], eps=1e-6, ids=ids)
 
     for _ in range(max(1, args.warmup)):
         step()
+        step_rm()
     torch.cuda.synchronize()
     ms = events_time(step, max(5, args.steps // 2), torch)
+    ms_rm = events_time(step_rm, max(5, args.steps // 2), torch)
     ops = 2.0 * R * V * 2048
-    return dict(us_per_step=ms * 1e3, ops=ops, tops=ops / (ms * 1e-3) / 1e12, rows=R, vocab=V)
+    return dict(us_per_step=ms * 1e3, ops=ops, tops=ops / (ms * 1e-3) / 1e12, rows=R, vocab=V,
+                us_row_major=ms_rm * 1e3)
 
 
 def cpu_info() -> dict:

@@ -71,7 +71,7 @@ class OprojArgs(C.Structure):
 class LmheadArgs(C.Structure):
     _fields_ = [("R", I32), ("H", I32), ("V", I32), ("h", P), ("norm_w", P), ("eps", C.c_float), ("wq", P),
                 ("ws", P), ("ids", P), ("logits", P), ("workspace", P), ("workspace_bytes", SZ), ("mode", I32),
-                ("logits_f32", I32), ("wq_w16", P)]
+                ("logits_f32", I32), ("wq_t", P)]
 
 
 class LinearSeg(C.Structure):

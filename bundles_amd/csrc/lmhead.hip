@@ -203,7 +203,7 @@ struct LmhLds {
 // loads this wave issues (0: weights, waves 0-3; 1: activations, waves 4-7); everything else is the
 // same in both.  Each role is its own instantiation, so the compiler's wait counting sees only the
 // wave's own operand in flight.
-template <int STORE, bool X2, int NW, int ROLE>
+template <int STORE, bool X2, int NW, int ROLE, bool WT>
 __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d, const LmhLds& L) {
   // NW waves: two vocab halves (wn) x NW / 2 token groups (wm); a wave owns 128 vocab columns (VB = 4
   // blocks of 32) x TW tokens (TB blocks of 32)
@@ -250,10 +250,12 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d, const LmhLds& L) 
   // check covers only the former, so rows past the tile's last valid row read zero.
   int vrow[CPL];
 #pragma unroll
-  for (int i = 0; i < CPL; ++i) vrow[i] = voff + (CPL * (wv & 3) + i) * 16 * kLH;
+  for (int i = 0; i < CPL; ++i)
+    vrow[i] = ROLE == 0 && WT ? 16 * lane + (CPL * (wv & 3) + i) * 16 * kLH : voff + (CPL * (wv & 3) + i) * 16 * kLH;
   auto issue_to = [&](const Tile& t, int ks, int8_t* s, int i) {
     const int q = (wv & 3) * CPL + i;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ROLE == 0 ? t.b : t.a, s + q * 1024, 16, vrow[i], ks * kBK, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ROLE == 0 ? t.b : t.a, s + q * 1024, 16, vrow[i],
+                                             ROLE == 0 && WT ? ks * 1024 : ks * kBK, 0, 0);
   };
   // load i of step KS (its stage KS % NS of the wave's operand)
   auto issue_one = [&](const Tile& t, auto ksc, int i) {
@@ -277,7 +279,11 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d, const LmhLds& L) 
   // 8 (j / 4) + 4 (l / 32) + j % 4 of register j.
   const int l32 = lane & 31, lh = lane >> 5;
   const int fx0 = bswz(wm * TW + l32, lh), fx1 = bswz(wm * TW + l32, 2 + lh);  // + 32 kBK per t
-  const int fw0 = bswz(wn * 128 + l32, lh), fw1 = bswz(wn * 128 + l32, 2 + lh);
+  // WT (weights in the tile order, each 16-row x 64-byte piece 1 KB contiguous): the DMA puts lane l's
+  // 16 bytes (row 16 q + l % 16, K chunk l / 16 of the step) at 16 l of chunk q, and a fragment read's
+  // 16 lanes take 256 contiguous bytes
+  const int fw0 = WT ? ((wn * 128 + l32) >> 4) * 1024 + ((l32 & 15) + 16 * lh) * 16 : bswz(wn * 128 + l32, lh);
+  const int fw1 = WT ? fw0 + 512 : bswz(wn * 128 + l32, 2 + lh);
   v16i acc[VB][TB];     // [vocab block][token block]
   v4i fx[2][2][TB], fw[2][2][VB];  // [register set][half step][block]
   auto read_one = [&](auto ksc, auto fb, int k) {  // fragment k (0..NRD-1) of step KS
@@ -473,24 +479,25 @@ __device__ __forceinline__ void lmh_gemm_body(const LmhDev& d, const LmhLds& L) 
   static_assert(kNSA == 3 && kNSB == 6, "the stage arrays above");                                   \
   const LmhLds L{{a_s0, a_s1, a_s2}, {b_s0, b_s1, b_s2, b_s3, b_s4, b_s5}, sc_l, rkey};
 
-template <bool X2>
+// WT: the weights in the tile order (q36_lmhead_args.wq_t) instead of row-major
+template <bool X2, bool WT>
 __global__ __launch_bounds__(64 * kLmhWaves) __attribute__((amdgpu_waves_per_eu(kLmhWaves / 4, kLmhWaves / 4))) void
 lmh_gemm_kernel(LmhDev d) {
   LMH_GEMM_LDS
   if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) < kLmhWaves / 2)
-    lmh_gemm_body<0, X2, kLmhWaves, 0>(d, L);
+    lmh_gemm_body<0, X2, kLmhWaves, 0, WT>(d, L);
   else
-    lmh_gemm_body<0, X2, kLmhWaves, 1>(d, L);
+    lmh_gemm_body<0, X2, kLmhWaves, 1, WT>(d, L);
 }
 // the same with the logits written out (F32: as fp32)
-template <bool X2, bool F32>
+template <bool X2, bool F32, bool WT>
 __global__ __launch_bounds__(64 * kLmhWaves) __attribute__((amdgpu_waves_per_eu(kLmhWaves / 4, kLmhWaves / 4))) void
 lmh_gemm_logits_kernel(LmhDev d) {
   LMH_GEMM_LDS
   if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) < kLmhWaves / 2)
-    lmh_gemm_body<F32 ? 2 : 1, X2, kLmhWaves, 0>(d, L);
+    lmh_gemm_body<F32 ? 2 : 1, X2, kLmhWaves, 0, WT>(d, L);
   else
-    lmh_gemm_body<F32 ? 2 : 1, X2, kLmhWaves, 1>(d, L);
+    lmh_gemm_body<F32 ? 2 : 1, X2, kLmhWaves, 1, WT>(d, L);
 }
 
 __global__ __launch_bounds__(256) void lmh_ids_kernel(LmhDev d) {
@@ -545,9 +552,9 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
               "q36_lmhead_argmax: mode %d unknown", a->mode);
   Q36_REQUIRE(a->mode != Q36_LMH_W8A16 || (a->R <= 64 && a->V % 32 == 0),
               "q36_lmhead_argmax: the W8A16 form serves R <= 64 rows and V a multiple of 32 (R=%d V=%d)", a->R, a->V);
-  Q36_REQUIRE(a->h && a->wq && a->ws && a->ids && a->workspace, "q36_lmhead_argmax: a required pointer is null");
-  Q36_REQUIRE(!a->wq_w16 || a->mode == Q36_LMH_W8A16, "q36_lmhead_argmax: wq_w16 serves the W8A16 mode only");
-  Q36_REQUIRE(aligned16(a->h) && aligned16(a->wq) && aligned16(a->ws) && aligned16(a->norm_w) && aligned16(a->wq_w16) &&
+  Q36_REQUIRE(a->h && (a->wq || a->wq_t) && a->ws && a->ids && a->workspace,
+              "q36_lmhead_argmax: a required pointer is null");
+  Q36_REQUIRE(aligned16(a->h) && aligned16(a->wq) && aligned16(a->ws) && aligned16(a->norm_w) && aligned16(a->wq_t) &&
                   (reinterpret_cast<uintptr_t>(a->workspace) & 255u) == 0,
               "q36_lmhead_argmax: h, wq, ws, norm_w must be 16-byte and workspace 256-byte aligned");
   const LmhWs L = lmh_ws(a->R);
@@ -559,7 +566,7 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
   Q36_REQUIRE(aligned16(a->logits), "q36_lmhead_argmax: logits must be 16-byte aligned");
   const bool f32 = a->logits && a->logits_f32;
   LmhDev d{a->R, a->V, act_rows(a->R, x2), x2, w16, static_cast<const uint16_t*>(a->h), static_cast<const uint16_t*>(a->norm_w), a->eps,
-           static_cast<const int8_t*>(a->wq), a->ws, a->ids, f32 ? nullptr : static_cast<uint16_t*>(a->logits),
+           a->wq_t ? a->wq_t : static_cast<const int8_t*>(a->wq), a->ws, a->ids, f32 ? nullptr : static_cast<uint16_t*>(a->logits),
            f32 ? static_cast<float*>(a->logits) : nullptr, reinterpret_cast<int8_t*>(ws + L.xq), reinterpret_cast<float*>(ws + L.xs),
            reinterpret_cast<unsigned long long*>(ws + L.keys)};
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -572,8 +579,8 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
     g.x = reinterpret_cast<const uint16_t*>(d.xq);  // the prep's bf16 rows (2 R * H bytes fit in xq)
     // the codes in the tile order when the caller keeps that copy: each piece the kernel loads at once
     // is then 1 KB contiguous (1 row 77 -> 61 us, 32 rows 115 -> 79 us at V = 151936)
-    g.q = a->wq_w16 ? a->wq_w16 : d.wq;
-    g.tiled = a->wq_w16 != nullptr;
+    g.q = d.wq;
+    g.tiled = a->wq_t != nullptr;
     g.ws = d.ws;
     g.logits = d.logits;
     g.logits32 = d.logits32;
@@ -587,18 +594,27 @@ extern "C" int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream) 
   // busiest XCD's tiles
   const int ngrp = lmh_groups(nrt), vstep = 8 / ngrp;
   const int blocks = 8 * std::max(1, std::min(lmh_cus() / 8, ((nvt + vstep - 1) / vstep) * (nrt / ngrp)));
-  if (d.logits32 && x2)
-    lmh_gemm_logits_kernel<true, true><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
-  else if (d.logits32)
-    lmh_gemm_logits_kernel<false, true><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
-  else if (d.logits && x2)
-    lmh_gemm_logits_kernel<true, false><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
-  else if (d.logits)
-    lmh_gemm_logits_kernel<false, false><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
-  else if (x2)
-    lmh_gemm_kernel<true><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+  // the weights' tile order: their DMA reads 1 KB contiguous pieces (2048 rows 697-702 -> 674-683 us,
+  // 256 rows two terms 171-178 -> 164-166 us against the row-major codes)
+  auto go = [&](auto wt) {
+    constexpr bool WT = decltype(wt)::value;
+    if (d.logits32 && x2)
+      lmh_gemm_logits_kernel<true, true, WT><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+    else if (d.logits32)
+      lmh_gemm_logits_kernel<false, true, WT><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+    else if (d.logits && x2)
+      lmh_gemm_logits_kernel<true, false, WT><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+    else if (d.logits)
+      lmh_gemm_logits_kernel<false, false, WT><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+    else if (x2)
+      lmh_gemm_kernel<true, WT><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+    else
+      lmh_gemm_kernel<false, WT><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+  };
+  if (a->wq_t)
+    go(std::true_type{});
   else
-    lmh_gemm_kernel<false><<<blocks, 64 * kLmhWaves, 0, st>>>(d);
+    go(std::false_type{});
   lmh_ids_kernel<<<(a->R + 255) / 256, 256, 0, st>>>(d);
   return check_launch("q36_lmhead_argmax");
 }

@@ -67,9 +67,10 @@ class Layer:
 class HybridWeights:
     layers: list
     final_norm_w: torch.Tensor
-    lm_q: torch.Tensor
+    lm_q: torch.Tensor   # int8 [V, 2048] row-major (the reference layout; what the oracle checks read)
     lm_s: torch.Tensor
     E: int
+    lm_qt: torch.Tensor | None = None  # the same codes in the tile order (what the lm_head reads)
     eps: float = 1e-6
 
 
@@ -116,7 +117,7 @@ def make_weights(device, seed: int = 0, E: int = synth.E, V: int = 151936, zipf:
     lw = synth.randn((V, HIDDEN), g, device, 0.02)
     lm_q, lm_s = lmhead8.quantize_rows(lw)
     del lw
-    return HybridWeights(layers, synth.randn((HIDDEN,), g, device, 0.1), lm_q, lm_s, E)
+    return HybridWeights(layers, synth.randn((HIDDEN,), g, device, 0.1), lm_q, lm_s, E, lmhead8.tile_rows_w16(lm_q))
 
 
 def _ring_pools(B: int, T: int, device, g, wp: int) -> dict:
@@ -295,7 +296,8 @@ def forward(x: torch.Tensor, w: HybridWeights, st: HybridState, ws: HybridWorksp
         keep(f"L{i}.res_out", res)
     keep("final", h)
     mode = lm_mode(M, w.lm_q.shape[0])
-    lmhead8.w8a8_lmhead_argmax(h, w.lm_q, w.lm_s, ws.lmhead, norm_w=None, eps=w.eps, ids=b["ids"], stream=stream,
+    lmhead8.w8a8_lmhead_argmax(h, w.lm_q if w.lm_qt is None else None, w.lm_s, ws.lmhead, norm_w=None, eps=w.eps,
+                               ids=b["ids"], q_t=w.lm_qt, stream=stream,
                                two_term=mode == "two_term", w8a16=mode == "w8a16")
     keep("ids", b["ids"])
     return b["ids"]

@@ -36,9 +36,9 @@ class Workspace:
 
 
 def tile_rows_w16(q: torch.Tensor, stream=None) -> torch.Tensor:
-    """The int8 head [V, 2048] reordered into the W8A16 kernel's tile order (q36_tile_w16): each
-    16-row x 64-column piece that kernel loads at once becomes 1 KB contiguous.  w8a8_lmhead_argmax
-    (..., w8a16=True, q_w16=...) reads it with the same bits out."""
+    """The int8 head [V, 2048] reordered into the tile order (q36_tile_w16): each 16-row x 64-column
+    piece becomes 1 KB contiguous.  w8a8_lmhead_argmax(..., q_t=...) reads it in every mode, with the
+    same bits out."""
     V, H = q.shape
     if q.dtype != torch.int8 or not q.is_contiguous() or V % 16 or H % 64:
         raise ValueError("tile_rows_w16: q must be contiguous int8 [V, H], V % 16 == 0, H % 64 == 0")
@@ -48,19 +48,22 @@ def tile_rows_w16(q: torch.Tensor, stream=None) -> torch.Tensor:
 
 
 def w8a8_lmhead_argmax(h, q, scale, ws: Workspace, norm_w=None, eps: float = 1e-6, want_logits: bool = False,
-                       ids=None, stream=None, two_term: bool = False, logits=None, w8a16: bool = False, q_w16=None):
+                       ids=None, stream=None, two_term: bool = False, logits=None, w8a16: bool = False, q_t=None):
     """h bf16 [R, 2048] -> ids int32 [R] (and bf16 logits [R, V] when want_logits, into `logits` when
     given: bf16, or fp32 receiving the same bf16-rounded values, as the reference writes stock's fp32
     next_token_logits_buffer, H/node.py:68-88,136-149).  two_term: the reference's two-term activation
     form (H/w8a8.py:25-37); w8a16: the bf16 rows times the int8 weights unquantized (H/lmhead8.py:57-91;
-    R <= 64, V a multiple of 32); q_w16 (w8a16 only, optional): tile_rows_w16(q), read instead of q
-    (the same bits, 20-30 % faster)."""
+    R <= 64, V a multiple of 32); q_t (optional): tile_rows_w16(q), read instead of q by every form, q
+    may then be None (the same bits; 3-5 % faster for W8A8, 20-30 % for W8A16)."""
     R, H = h.shape
-    V = q.shape[0]
+    if q is None and q_t is None:
+        raise ValueError("w8a8_lmhead_argmax: q or q_t is required")
+    V = (q if q is not None else q_t).shape[0]
     if R > ws.R_max:
         raise ValueError(f"w8a8_lmhead_argmax: {R} rows exceed the workspace's {ws.R_max}")
-    for name, t, dt in (("h", h, torch.bfloat16), ("q", q, torch.int8), ("scale", scale, torch.float32)):
-        if t.dtype != dt or not t.is_contiguous():
+    for name, t, dt in (("h", h, torch.bfloat16), ("q", q, torch.int8), ("scale", scale, torch.float32),
+                        ("q_t", q_t, torch.int8)):
+        if t is not None and (t.dtype != dt or not t.is_contiguous()):
             raise ValueError(f"w8a8_lmhead_argmax: {name} must be contiguous {dt}")
     ids = torch.empty(R, dtype=torch.int32, device=h.device) if ids is None else ids
     if want_logits and logits is None:
@@ -68,12 +71,11 @@ def w8a8_lmhead_argmax(h, q, scale, ws: Workspace, norm_w=None, eps: float = 1e-
     if logits is not None and (logits.dtype not in (torch.bfloat16, torch.float32) or tuple(logits.shape) != (R, V)
                                or not logits.is_contiguous()):
         raise ValueError(f"w8a8_lmhead_argmax: logits must be contiguous bf16 or fp32 [{R}, {V}]")
-    if q_w16 is not None and (not w8a16 or q_w16.dtype != torch.int8 or tuple(q_w16.shape) != tuple(q.shape)
-                              or not q_w16.is_contiguous()):
-        raise ValueError("w8a8_lmhead_argmax: q_w16 is tile_rows_w16(q), for the w8a16 form only")
+    if q_t is not None and (tuple(q_t.shape) != (V, H) or (q is not None and tuple(q.shape) != (V, H))):
+        raise ValueError(f"w8a8_lmhead_argmax: q_t is tile_rows_w16(q), int8 [{V}, {H}]")
     a = LmheadArgs(R, H, V, ptr(h), ptr(norm_w), eps, ptr(q), ptr(scale), ptr(ids), ptr(logits), ptr(ws.buf),
                    ws.buf.numel(),
                    _lib.Q36_LMH_W8A16 if w8a16 else _lib.Q36_LMH_W8A8X2 if two_term else _lib.Q36_LMH_W8A8,
-                   int(logits is not None and logits.dtype == torch.float32), ptr(q_w16))
+                   int(logits is not None and logits.dtype == torch.float32), ptr(q_t))
     check(_lib.lib().q36_lmhead_argmax(C.byref(a), _lib.stream_handle(stream)), "q36_lmhead_argmax")
     return (ids, logits) if (want_logits or logits is not None) else ids

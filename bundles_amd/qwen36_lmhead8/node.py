@@ -126,10 +126,9 @@ def _version(w: torch.Tensor):
 
 @dataclass
 class HeadCopy:
-    q: torch.Tensor        # int8 [V, 2048]
+    q: torch.Tensor        # int8 [V, 2048] codes in the tile order (lmhead8.tile_rows_w16), what every form reads
     scale: torch.Tensor    # fp32 [V]
     ident: tuple           # (storage pointer, shape, device, version) of the weight it was built from
-    q16: torch.Tensor | None = None  # q in the W8A16 kernel's tile order, made at the first W8A16 call
 
     @staticmethod
     def ident_of(w: torch.Tensor) -> tuple:
@@ -157,6 +156,7 @@ class LogitsNode:
         self.copy = None  # free the stale copy before building the new one
         with torch.no_grad():
             q, s = lmhead8.quantize_rows(w.contiguous())
+            q = lmhead8.tile_rows_w16(q)  # the row-major codes are freed: one copy of V x 2048 bytes
         self.copy = HeadCopy(q, s, ident)
         return self.copy
 
@@ -184,11 +184,8 @@ class LogitsNode:
         buf = self.out_buf
         out = (buf if buf is not None and rows >= LOGITS_BUF_MIN_ROWS and tuple(buf.shape) == (rows, vocab)
                and vocab == getattr(self.processor, "vocab_size", -1) and buf.device == weight.device else None)
-        if mode == "w8a16" and hc.q16 is None and not torch.cuda.is_current_stream_capturing():
-            hc.q16 = lmhead8.tile_rows_w16(hc.q)  # a second copy of the codes (V x 2048 bytes)
-        ids, logits = lmhead8.w8a8_lmhead_argmax(h.contiguous(), hc.q, hc.scale, ws, want_logits=True, logits=out,
-                                                 two_term=mode == "two_term", w8a16=mode == "w8a16",
-                                                 q_w16=hc.q16 if mode == "w8a16" else None)
+        ids, logits = lmhead8.w8a8_lmhead_argmax(h.contiguous(), None, hc.scale, ws, want_logits=True, logits=out,
+                                                 two_term=mode == "two_term", w8a16=mode == "w8a16", q_t=hc.q)
         self.last_ids = ids
         return logits
 

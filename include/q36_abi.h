@@ -499,7 +499,7 @@ typedef struct q36_lmhead_args {
   const void* h;
   const void* norm_w;
   float eps;
-  const int8_t* wq;
+  const int8_t* wq; /* row-major, or NULL with wq_t */
   const float* ws;
   int32_t* ids;
   void* logits;
@@ -507,10 +507,10 @@ typedef struct q36_lmhead_args {
   size_t workspace_bytes;
   int32_t mode; /* Q36_LMH_W8A8, Q36_LMH_W8A8X2 or Q36_LMH_W8A16 */
   int32_t logits_f32; /* 0: logits is bf16 [R, V]; nonzero: fp32 [R, V] (bf16-rounded values) */
-  /* Optional, mode Q36_LMH_W8A16 only (no reference counterpart): wq's codes in q36_tile_w16's order,
-   * read instead of wq (each 16-row x 64-column piece the kernel loads at once is 1 KB contiguous);
-   * the same bits out.  NULL: wq row-major. */
-  const int8_t* wq_w16;
+  /* Optional (no reference counterpart): wq's codes in q36_tile_w16's order (each 16-row x 64-column
+   * piece 1 KB contiguous, V % 16 == 0), read instead of wq by every mode, which may then be NULL; the
+   * same bits out, faster (the weight loads read contiguous 1 KB pieces).  NULL: wq row-major. */
+  const int8_t* wq_t;
 } q36_lmhead_args;
 size_t q36_lmhead_workspace_bytes(int32_t R);
 int q36_lmhead_argmax(const q36_lmhead_args* a, q36_stream_t stream);

@@ -1,5 +1,6 @@
 """GPU parity of the W8A16 GEMM (libq36 through the C-ABI) against the CPU oracle: the DENSE8 linear
-(q36_dense8_linear) and the lm_head's W8A16 form (q36_lmhead_argmax, Q36_LMH_W8A16).
+(q36_dense8_linear) and the lm_head's W8A16 form (q36_lmhead_argmax, Q36_LMH_W8A16); and the lm_head on
+the tile-order copy of its codes (q36_lmhead_args.wq_t) against the row-major codes, in every form.
 
 Bar: the GPU sums the bf16 x int8 products (each exact in fp32) in fp32 in its MFMA order, the oracle
 sums each 128-column group exactly and rounds once, so outputs agree within the bf16 bar (worst row
@@ -111,7 +112,7 @@ def test_lmhead_w8a16_vs_oracle(mods, oracle_mod, dev, R, V, norm):
 def test_lmhead_w8a16_tiled_copy_same_bits(mods, dev, R, V, norm):
     """The W8A16 lm_head on the tile-order copy (tile_rows_w16, what the logits node keeps) gives the
     row-major codes' ids and bf16 logits bit for bit, across the 32-, 64- and 128-row wave shapes; the copy
-    is the stated permutation (a torch reshape of the same definition); q_w16 is refused outside W8A16."""
+    is the stated permutation (a torch reshape of the same definition)."""
     from bundles_amd import synth
     _, _, lmh = mods
     print(f"lmhead W8A16 tiled R={R} V={V} norm={norm}", flush=True)
@@ -121,15 +122,51 @@ def test_lmhead_w8a16_tiled_copy_same_bits(mods, dev, R, V, norm):
     ws = lmh.Workspace(R, dev)
     nw = d["norm_w"] if norm else None
     ids, logits = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=nw, eps=1e-6, want_logits=True, w8a16=True)
-    ids2, logits2 = lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, norm_w=nw, eps=1e-6, want_logits=True, w8a16=True,
-                                           q_w16=qt)
+    ids2, logits2 = lmh.w8a8_lmhead_argmax(d["h"], None, s, ws, norm_w=nw, eps=1e-6, want_logits=True, w8a16=True,
+                                           q_t=qt)
     torch.cuda.synchronize()
     want = q.view(V // 16, 16, 2048 // 64, 4, 16).permute(0, 2, 3, 1, 4).reshape(V, 2048)
     assert torch.equal(qt, want), "tile order"
     assert torch.equal(ids, ids2)
     assert torch.equal(logits.view(torch.int16), logits2.view(torch.int16))
+
+
+# the W8A8 GEMM forms on the tile-order copy: one term (ids only, bf16 and f32 logits) and two terms
+@pytest.mark.parametrize("R,V,two_term,logits", [(256, 151936, False, None), (64, 4096, False, "bf16"),
+                                                 (300, 8192, True, None), (128, 4160, False, "f32"),
+                                                 (256, 8192, True, "bf16"), (2048, 4096, False, None)])
+def test_lmhead_w8a8_tiled_copy_same_bits(mods, dev, R, V, two_term, logits):
+    """Every W8A8 form reads the tile-order copy (q_t) in place of the row-major codes and gives the same ids
+    and logits bit for bit (the same products summed in the same MFMA order); a copy of the wrong shape is
+    refused before anything is launched."""
+    from bundles_amd import synth
+    _, _, lmh = mods
+    print(f"lmhead W8A8 tiled R={R} V={V} two_term={two_term} logits={logits}", flush=True)
+    d = synth.lmhead_inputs(R, V, dev, seed=5 * R + V)
+    q, s = lmh.quantize_rows(d["w"])
+    qt = lmh.tile_rows_w16(q)
+    ws = lmh.Workspace(R, dev)
+
+    def run(qq, qtt):
+        out = None
+        if logits is not None:
+            out = torch.full((R, V), -3.0, device=dev,
+                             dtype=torch.float32 if logits == "f32" else torch.bfloat16)
+        ids = torch.full((R,), -1, dtype=torch.int32, device=dev)
+        lmh.w8a8_lmhead_argmax(d["h"], qq, s, ws, norm_w=d["norm_w"], eps=1e-6, ids=ids, two_term=two_term,
+                               logits=out, q_t=qtt)
+        return ids, out
+
+    ids, out = run(q, None)
+    ids2, out2 = run(None, qt)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids2), "ids"
+    assert int(ids.min()) >= 0
+    if logits is not None:
+        iv = torch.int32 if logits == "f32" else torch.int16
+        assert torch.equal(out.view(iv), out2.view(iv)), "logits"
     with pytest.raises(ValueError):
-        lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, q_w16=qt)
+        lmh.w8a8_lmhead_argmax(d["h"], q, s, ws, q_t=qt[: V - 32])
 
 
 @pytest.mark.parametrize("T,N,K", [(1, 12352, 2048), (16, 2048, 4096), (37, 384, 2048)])
