@@ -56,7 +56,9 @@ def test_quant_blocks_e4m3_matches_oracle(q36, oracle_mod, dev):
         assert np.array_equal(np_(s[i]).view(np.uint32), so.view(np.uint32))
 
 
-ROUTE_CASES = [(1, False, False), (8, False, False), (64, True, False), (64, True, True), (256, False, True)]
+# past 128 rows the router takes eight experts a wave: 129 rows end in a partial 8-token group, 200 rows pad
+ROUTE_CASES = [(1, False, False), (8, False, False), (64, True, False), (64, True, True), (256, False, True),
+               (129, True, False), (200, True, True), (256, True, False)]
 
 
 @pytest.mark.parametrize("M,zipf,padded", ROUTE_CASES)
@@ -312,13 +314,13 @@ def test_moe_fused_add_norm(q36, oracle_mod, dev, dtype):
     assert np.array_equal(bits16(y_got), hn) and np.array_equal(bits16(r_got), res)
 
 
-@pytest.mark.parametrize("dtype,M", [(1, 1), (1, 2), (0, 5), (1, 24), (1, 40), (0, 64), (1, 256)])
+@pytest.mark.parametrize("dtype,M", [(1, 1), (1, 2), (0, 5), (1, 24), (1, 40), (0, 64), (1, 256), (0, 131)])
 def test_moe_input_add_norm(q36, oracle_mod, dev, dtype, M):
     """This block's own input add-norm run by the route kernel (pre_norm) gives the same bits as
     q36_add_rmsnorm followed by the block: the normed rows, the new residual, the block output (padding
     rows included), and with the next block's add-norm fused into the combine too, the hybrid node's
     form; the old residual is left as it was, and the oracle's add-norm agrees.  M covers every router
-    shape (1, 2, 4 and 8 tokens a workgroup, two and four experts a wave)."""
+    shape (1, 2, 4 and 8 tokens a workgroup, two, four and eight experts a wave)."""
     from bundles_amd import synth
     from bundles_amd.qwen36_layer import glue
     O = oracle_mod
