@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import statistics
 import os
 import sys
 import time
@@ -549,8 +550,14 @@ def bench_lmhead(args, torch, dev):
         step()
         step_rm()
     torch.cuda.synchronize()
-    ms = events_time(step, max(5, args.steps // 2), torch)
-    ms_rm = events_time(step_rm, max(5, args.steps // 2), torch)
+    # the two forms in alternating rounds of a few calls, the order swapped every round (the clock
+    # drifts over a run), medians of the rounds
+    n_per, rounds = 3, max(4, args.steps // 3)
+    t_tiled, t_rm = [], []
+    for r in range(rounds):
+        for f, acc in ((step, t_tiled), (step_rm, t_rm))[:: 1 if r % 2 == 0 else -1]:
+            acc.append(events_time(f, n_per, torch))
+    ms, ms_rm = statistics.median(t_tiled), statistics.median(t_rm)
     ops = 2.0 * R * V * 2048
     return dict(us_per_step=ms * 1e3, ops=ops, tops=ops / (ms * 1e-3) / 1e12, rows=R, vocab=V,
                 us_row_major=ms_rm * 1e3)
