@@ -1115,22 +1115,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W + ((size_t)(n0 >> 4) * NSTG << 11)), (short)0, kDnCT * NSTG << 11, 0x00020000);
   v4i B[kDnCT][NSTG][2];
-  auto issue_weights = [&](auto c0c) {  // the tile pair c0, c0 + 1
-    constexpr int C0 = decltype(c0c)::value;
+  // K stages [S0, S1) of the tile pair c0, c0 + 1
+  auto issue_weights = [&](auto c0c, auto s0c, auto s1c) {
+    constexpr int C0 = decltype(c0c)::value, S0 = decltype(s0c)::value, S1 = decltype(s1c)::value;
 #pragma unroll
     for (int ct = C0; ct < C0 + 2; ++ct)
 #pragma unroll
-      for (int s = 0; s < NSTG; ++s) {
+      for (int s = S0; s < S1; ++s) {
         B[ct][s][0] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, (ct * NSTG + s) << 11, 2);
         B[ct][s][1] = __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, ((ct * NSTG + s) << 11) + 1024, 2);
       }
   };
-  // the token list is requested and the first tile pair's weights go out as soon as the expert is
-  // known, then the first group's h rows, then the second pair: the rows' quantization waits for
-  // the first pair only and overlaps the second (vector loads complete in issue order)
+  // the token list is requested and the first tile pair's first two K stages go out as soon as the
+  // expert is known, then the first group's h rows, then the rest of the weights: the rows'
+  // quantization waits for those 8 KB a wave only (vector loads complete in issue order) and overlaps
+  // the remaining 24 KB (with the whole first pair, 16 KB, ahead of the rows the batch-64 layer was
+  // 0.5 us slower)
+  constexpr int kDnEarly = 2;
+  static_assert(kDnEarly < NSTG, "the rest of the first pair goes out after the rows");
   const SlotReq req = slots_request(d, unit, e);
   __builtin_amdgcn_sched_barrier(0);
-  issue_weights(std::integral_constant<int, 0>{});
+  issue_weights(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, kDnEarly>{});
   __builtin_amdgcn_sched_barrier(0);
   const int cnt = slots_finish(d, unit, e, req, slots, wtot, nullptr);
   if (cnt <= g0) return;
@@ -1167,7 +1172,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (!shared)
         wv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(trs, wok ? slots[g0 + tid] * 4 : tbytes, 0, 0));
       if constexpr (FIRST) {
-        issue_weights(std::integral_constant<int, 2>{});
+        issue_weights(std::integral_constant<int, 0>{}, std::integral_constant<int, kDnEarly>{}, std::integral_constant<int, NSTG>{});
+        issue_weights(std::integral_constant<int, 2>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, NSTG>{});
         if constexpr (DT != Q36_MOE_FP8) sn[tid] = snv;
       }
 #pragma unroll
