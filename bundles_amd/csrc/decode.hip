@@ -300,8 +300,11 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
         for (int dg = 0; dg < 16; dg += 4) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
+            // taken from the AGPRs here (an opaque redefinition: a VGPR copy made before the branch
+            // would be stale), scaled, and put back (no VGPR copy across the join)
+            asm volatile("" : "+a"(o[rt][dg + i]));
             o[rt][dg + i] *= al;
-            asm volatile("" : "+a"(o[rt][dg + i]));  // back into AGPRs (no VGPR copy across the join)
+            asm volatile("" : "+a"(o[rt][dg + i]));
           }
           __builtin_amdgcn_sched_barrier(0);
         }
