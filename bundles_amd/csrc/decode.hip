@@ -21,7 +21,8 @@
 //                   f16 16x16x32 MFMA, V^T read from LDS with the transpose read (V rows staged by
 //                   buffer DMA in the key order the lane's weights are in), P^T the lane's own
 //                   weights rounded to f16.  Keys, values and page-table entries stream through a
-//                   4-stage per-wave pipeline with no workgroup barrier; the output is rescaled only
+//                   per-wave pipeline (2 stages at two waves a SIMD for one row tile, 4 at one wave
+//                   a SIMD for two) with no workgroup barrier; the output is rescaled only
 //                   when a row max grows by more than 2^8 (weights up to 2^8 are exact in f16).
 //   decode_combine  the splits' partials weighted by exp2(m_s - M) / L (with one split the split
 //                   kernel writes the output itself).
@@ -37,9 +38,14 @@ namespace {
 
 constexpr int kQH = 16, kKVH = 2, kDD = 256, kGQ = kQH / kKVH, kDNT = 4, kDRows = kGQ * kDNT;
 constexpr int kST = 32;              // keys per wave step
-constexpr int kNS = 3;               // key / value stages per wave (steps in flight + 1)
-constexpr int kPTD = 2 * kNS;        // page-table lookahead in steps
+// NS (kernel template): key / value stages per wave (steps in flight + 1); the page-table entries run
+// 2 NS steps ahead, so an entry's DMA is older than every key and value load a wait leaves in flight
 constexpr int kPTR = 8;              // page-table ring entries per wave (one step each)
+// The two forms' shapes (alternating builds on one box, three rounds): the one-row-tile form (decode,
+// NT <= 2) with 2 stages fits 224 registers and 77 KB of LDS, so two workgroups share a CU (two waves
+// a SIMD): decode 189.9 -> 182.7 us against 3 stages at one wave a SIMD; the two-row-tile form
+// (verify) keeps one wave a SIMD and runs 4 stages (456 registers, 145 KB): 62.0 -> 60.6 us.
+constexpr int kDecNS1 = 2, kDecWPE1 = 2, kDecNS2 = 4;
 constexpr int kVG = 4 * kDD + 64;    // a group of 4 value rows in LDS (64 bytes of padding)
 constexpr int kVW = 8 * kVG;         // one wave's 32 value rows
 constexpr int kVS = 4 * kVW;         // one stage of the four waves' value rows
@@ -48,9 +54,8 @@ constexpr float kLazy = 8.f;
 // inside the hybrid node (after a GDN verify has left ~0.5 GB of snapshot writes dirty in the
 // caches) the plain reads ran at half speed, evicting that data; measured 111 -> 63 us per call.
 constexpr int kKVAux = 2;         // rescale when a row max grows past the reference by 2^8
-static_assert(kPTR >= kPTD && (kPTR & (kPTR - 1)) == 0, "page-table ring");
+static_assert((kPTR & (kPTR - 1)) == 0, "page-table ring");
 static_assert(kVS >= 2 * 16 * kDD * 4, "a stage holds two waves' fp32 output of one row tile at the merge");
-static_assert(kNS == 3, "the stage arrays and the prologue are written out for three stages");
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
@@ -126,11 +131,17 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(const uint8_t* k8, cons
   *reinterpret_cast<v4i*>((isv ? vc : kc) + dst) = *reinterpret_cast<const v4i*>((isv ? v8 : k8) + src);
 }
 
-template <int RT>
-__global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
+template <int RT, int NS, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void decode_split_kernel(DecodeDev d) {
+  constexpr int PTD = 2 * NS;
+  static_assert(NS >= 2 && NS <= 4, "the prologue and the step loop are written out for 2 to 4 stages");
+  static_assert(kPTR >= PTD, "the ring holds the entries of every step in flight");
+  // one object per stage: the compiler then sees that a stage's DMA does not write what another
+  // stage's reads read (in one array it waits for every DMA in flight before each read)
   __shared__ __align__(16) uint8_t vs0[kVS];
   __shared__ __align__(16) uint8_t vs1[kVS];
-  __shared__ __align__(16) uint8_t vs2[kVS];
+  __shared__ __align__(16) uint8_t vs2[NS >= 3 ? kVS : 16];
+  __shared__ __align__(16) uint8_t vs3[NS >= 4 ? kVS : 16];
   __shared__ __align__(16) int32_t ptl[4][kPTR][64];
   __shared__ float mw[4][kDRows], lwv[4][kDRows], rowM[kDRows], rowL[kDRows];
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z, S = d.splits;
@@ -142,7 +153,7 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
   const int st0 = s * per + min(s, rem), nst = per + (s < rem ? 1 : 0);
   const int ws0 = st0 + (wave * nst) / 4, ws1 = st0 + ((wave + 1) * nst) / 4;
   const int kbeg = ws0 * kST, kend = min(ws1 * kST, nk);  // the wave's keys [kbeg, kend)
-  const int npad = (ws1 - ws0 + kNS - 1) / kNS * kNS;     // steps run (a multiple of the stages)
+  const int npad = (ws1 - ws0 + NS - 1) / NS * NS;        // steps run (a multiple of the stages)
   const int kfull = min(kend - 1, npre);  // keys up to here are visible to every query row
   const int grp = (b * kKVH + h) * S + s;
   // query fragments (score operand B): column 16 rt + l16 = query row (token row / 8, head
@@ -190,10 +201,10 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
   // (one DMA call, 1 KB) starts at m * (1 KB + 64 B) and 16-byte piece p of its row i sits at position
   // p ^ i: the eight rows a lane group reads for one dim tile fall on eight distinct 16-byte bank
   // slots, and only the low two bits of a piece's position depend on the lane.
-  v4i kf[kNS][2][4];
+  v4i kf[NS][2][4];
   auto stage = [&](auto qc) -> uint8_t* {
     constexpr int Q = decltype(qc)::value;
-    return (Q == 0 ? vs0 : Q == 1 ? vs1 : vs2) + wave * kVW;
+    return (Q == 0 ? vs0 : Q == 1 ? vs1 : Q == 2 ? vs2 : vs3) + wave * kVW;
   };
   auto fetch = [&](int j, auto qc) {
     constexpr int Q = decltype(qc)::value;
@@ -237,9 +248,9 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
   const int vri = (l16 >> 1) & 3, vbase = (2 * lg + (l16 >> 3)) * kVG + vri * kDD + 8 * (l16 & 1);
   auto compute = [&](int j, auto qc) {
     constexpr int Q = decltype(qc)::value;
-    // this stage's values have landed (newer: one page-table DMA and kNS - 1 steps' requests); all
+    // this stage's values have landed (newer: NS page-table DMAs and NS - 1 steps' requests); all
     // sixteen transposed reads are issued now and complete under the scores and the softmax
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(1 + (kNS - 1) * 17) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NS + (NS - 1) * 16) : "memory");
     const uint8_t* vb = stage(qc) + vbase;
     v2i vraw[16];
 #pragma unroll
@@ -329,26 +340,33 @@ __global__ __launch_bounds__(256, 1) void decode_split_kernel(DecodeDev d) {
       for (int rt = 0; rt < RT; ++rt) o[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pb[rt], o[rt][dt], 0, 0, 0);
     }
   };
-  // prologue: entries of steps 0 .. kPTD - kNS, then the first kNS - 1 steps' requests, each
-  // followed by the page-table DMA kPTD steps ahead (the order every step keeps)
-  for (int j = 0; j <= kPTD - kNS; ++j) pt_dma(j);
+  // prologue: entries of steps 0 .. PTD - NS, then the first NS - 1 steps' requests, each
+  // followed by the page-table DMA PTD steps ahead (the order every step keeps)
+  for (int j = 0; j <= PTD - NS; ++j) pt_dma(j);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   fetch(0, std::integral_constant<int, 0>{});
-  pt_dma(kPTD - kNS + 1);
-  fetch(1, std::integral_constant<int, 1>{});
-  pt_dma(kPTD - kNS + 2);
+  pt_dma(PTD - NS + 1);
+  if constexpr (NS >= 3) {
+    fetch(1, std::integral_constant<int, 1>{});
+    pt_dma(PTD - NS + 2);
+  }
+  if constexpr (NS == 4) {
+    fetch(2, std::integral_constant<int, 2>{});
+    pt_dma(PTD - NS + 3);
+  }
   auto step = [&](int j, auto qc) {
     constexpr int Q = decltype(qc)::value;
-    fetch(j + kNS - 1, std::integral_constant<int, (Q + kNS - 1) % kNS>{});
-    pt_dma(j + kPTD);
+    fetch(j + NS - 1, std::integral_constant<int, (Q + NS - 1) % NS>{});
+    pt_dma(j + PTD);
     __builtin_amdgcn_sched_barrier(0);  // requests first: the compute below waits for step j's data
     compute(j, qc);
     __builtin_amdgcn_sched_barrier(0);  // and the next step's requests stay after it
   };
-  for (int j = 0; j < npad; j += kNS) {
+  for (int j = 0; j < npad; j += NS) {
     step(j, std::integral_constant<int, 0>{});
     step(j + 1, std::integral_constant<int, 1>{});
-    step(j + 2, std::integral_constant<int, 2>{});
+    if constexpr (NS >= 3) step(j + 2, std::integral_constant<int, 2>{});
+    if constexpr (NS == 4) step(j + 3, std::integral_constant<int, 3>{});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   // merge the four waves: M = max of the waves' maxima, L = sum of exp2(m_w - M) l_w; per row
@@ -500,9 +518,9 @@ extern "C" int q36_attn_decode(const q36_decode_args* a, q36_stream_t stream) {
               static_cast<uint16_t*>(a->out), static_cast<const uint16_t*>(a->gate), static_cast<uint8_t*>(a->oq),
               a->oqs};
   if (a->NT <= 2)
-    decode_split_kernel<1><<<dim3(S, kKVH, a->B), 256, 0, st>>>(d);
+    decode_split_kernel<1, kDecNS1, kDecWPE1><<<dim3(S, kKVH, a->B), 256, 0, st>>>(d);
   else
-    decode_split_kernel<2><<<dim3(S, kKVH, a->B), 256, 0, st>>>(d);
+    decode_split_kernel<2, kDecNS2, 1><<<dim3(S, kKVH, a->B), 256, 0, st>>>(d);
   if (S > 1) decode_combine_kernel<<<(a->B * a->NT * kQH * (kDD / 4) + 255) / 256, 256, 0, st>>>(d);
   return check_launch("q36_attn_decode");
 }
