@@ -341,22 +341,29 @@ __global__ __launch_bounds__(256) void route_logits_kernel(MoeDev d, int n_route
   }
   if (wave == 0 && d.gate_w != nullptr) {
     float xe[kRouteH / 512][8];
-    v4i gg[kRouteH / 512];
+    v4i gg[kRouteH / 512], xg[kRouteH / 512];
+    // every load first, none under a branch (the compiler waits for a load at the join of the branch
+    // it sits in: four round trips one after another).  The x chunks go through a buffer resource
+    // that is empty when the row comes from the LDS tile (reads of it return zeros, touch nothing).
+    const bool tile = d.in_norm_w != nullptr;
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(tile ? reinterpret_cast<const void*>(d.gate_w) : reinterpret_cast<const void*>(d.x)), (short)0,
+        tile ? 0 : d.M * kRouteH * 2, 0x00020000);
 #pragma unroll
     for (int j = 0; j < kRouteH / 512; ++j) {
       const int c = lane + 64 * j;
       gg[j] = ldg16(reinterpret_cast<const uint8_t*>(d.gate_w + 8 * c));
-      if (d.in_norm_w) {
-        const float4 lo = xlo[0][c], hi = xhi[0][c];
-        xe[j][0] = lo.x, xe[j][1] = lo.y, xe[j][2] = lo.z, xe[j][3] = lo.w;
-        xe[j][4] = hi.x, xe[j][5] = hi.y, xe[j][6] = hi.z, xe[j][7] = hi.w;
-      } else {
-        const v4i xg = ldg16(reinterpret_cast<const uint8_t*>(d.x + (size_t)t * kRouteH + 8 * c));
+      xg[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (t * kRouteH + 8 * c) * 2, 0, 0);
+    }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          xe[j][2 * q] = bf_lo((uint32_t)xg[q]);
-          xe[j][2 * q + 1] = bf_hi((uint32_t)xg[q]);
-        }
+    for (int j = 0; j < kRouteH / 512; ++j) {
+      const int c = lane + 64 * j;
+      const float4 lo = xlo[0][c], hi = xhi[0][c];  // the tile row (read either way, used with it)
+      const float tv[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        xe[j][2 * q] = tile ? tv[2 * q] : bf_lo((uint32_t)xg[j][q]);
+        xe[j][2 * q + 1] = tile ? tv[2 * q + 1] : bf_hi((uint32_t)xg[j][q]);
       }
     }
     float acc = 0.f;
