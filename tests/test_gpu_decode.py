@@ -77,6 +77,9 @@ def _check(out, ref, what):
     (4, [4, 5, 67, 128, 1000], 64),
     (2, [2, 130, 777], 0),
     (3, [3, 64, 129], 5),
+    # the one-row-tile form (NT <= 2, two stages) with splits: waves of zero, one or a few steps
+    (1, [1, 2, 33, 97, 2049], 7),
+    (2, [2, 3, 65, 4096], 64),
 ])
 def test_decode_parity(attn, oracle_mod, dev, NT, seqlens, splits):
     print(f"attn_decode NT={NT} seqlens={seqlens} splits={splits}", flush=True)
@@ -92,6 +95,16 @@ def test_decode_peaked_softmax(attn, oracle_mod, dev):
     h = _make(2, 4, [2000, 3001], seed=11, qscale=4.0)
     out, _ = _run(attn, h, 4, dev)
     _check(out, _oracle(oracle_mod, h, 4), "decode peaked")
+
+
+def test_decode_peaked_softmax_one_row_tile(attn, oracle_mod, dev):
+    """The peaked case in the one-row-tile form (NT = 1 and 2: two waves a SIMD, two stages), whose
+    lazy rescale runs on its own accumulators."""
+    for NT, seqlens in ((1, [1500, 2500, 4096]), (2, [700, 3001])):
+        print(f"attn_decode peaked NT={NT}", flush=True)
+        h = _make(len(seqlens), NT, seqlens, seed=13 + NT, qscale=4.0)
+        out, _ = _run(attn, h, NT, dev)
+        _check(out, _oracle(oracle_mod, h, NT), f"decode peaked NT={NT}")
 
 
 def test_decode_bench_shape(attn, oracle_mod, dev):
