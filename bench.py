@@ -9,9 +9,13 @@ unskewed router (about 470 of 512 experts active), the roofline of the dominant 
 up-projection, HBM-bound), the other nodes' step times, and the CPU oracle timed on this host's
 cores on every node's workload.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-ms MS] [--no-cpu]
                 [--only moe,moe_high_u,gdn,gdn_ring,lmhead,attn,decode,hybrid]
                 [--copy-calib]
+
+Every timed region is preceded by W warm-up steps and then by --settle-ms (default 500) of untimed
+repeats of the same work, so the shader clock has left its idle state; the timed region itself is
+exactly the K steps (settle_ms is reported in the line; --settle-ms 0 turns it off).
 """
 from __future__ import annotations
 
@@ -39,6 +43,28 @@ def measured_traffic(kernel: str):
         return int(t["traffic_bytes"])
     except (OSError, KeyError, ValueError):
         return None
+
+
+SETTLE_MS = 500.0  # --settle-ms: untimed repeats of a leg's work before its timed region
+
+
+def settle(fn, torch, ms=None):
+    """Untimed repeats of fn for SETTLE_MS of wall time right before a timed region.  The shader clock
+    ramps up under load; a timed region of a few milliseconds straight after a leg's setup (CPU work,
+    allocations, an idle GPU) would measure part of that ramp instead of the kernels.  The work is the
+    timed region's own; the line reports the setting as settle_ms."""
+    ms = SETTLE_MS if ms is None else ms
+    if ms <= 0:
+        return
+    t0, n = time.perf_counter(), 0
+    while True:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= ms:
+                break
+    torch.cuda.synchronize()
 
 
 def events_time(fn, steps, torch):
@@ -114,6 +140,7 @@ def bench_moe(args, torch, dev, n_layers=1, zipf=1.1, seed0=0, prebuilt=None, M=
     for _ in range(max(1, args.warmup)):
         g.replay()
     torch.cuda.synchronize()
+    settle(g.replay, torch)
     reps = max(1, args.steps // n_layers)
     t0 = time.perf_counter()
     for _ in range(reps):
@@ -200,6 +227,7 @@ def bench_small(args, torch, dev):
                 c()
         g.replay()
         torch.cuda.synchronize()
+        settle(g.replay, torch, SETTLE_MS / 5)
         reps = max(3, args.steps // 4)
         return events_time(g.replay, reps, torch) / len(calls)
 
@@ -275,6 +303,7 @@ def bench_gdn(args, torch, dev):
     for _ in range(max(1, args.warmup)):
         step()
     torch.cuda.synchronize()
+    settle(step, torch)
     ms = events_time(step, args.steps, torch)
     R = B * T
     state = B * 32 * 128 * 128 * 4
@@ -318,6 +347,7 @@ def bench_gdn_ring(args, torch, dev):
     torch.cuda.current_stream().wait_stream(s)
     graph.replay()
     torch.cuda.synchronize()
+    settle(graph.replay, torch)
     ms = events_time(graph.replay, max(2, args.steps // 5), torch) / (REP * SETS)
     R = B * T
     # checkpoint rows read; committed ring entries read (k and d high parts, g); window entries
@@ -352,6 +382,7 @@ def bench_attn(args, torch, dev):
         proj()
         oproj()
     torch.cuda.synchronize()
+    settle(proj, torch)
     ms_p = events_time(proj, args.steps, torch)
     ms_o = events_time(oproj, args.steps, torch)
     # as in the engine's captured verify step: the calls inside one graph (no per-call graph launch),
@@ -365,6 +396,7 @@ def bench_attn(args, torch, dev):
         for _ in range(inner):
             oproj()
     torch.cuda.synchronize()
+    settle(gp.replay, torch, SETTLE_MS / 5)
     ms_pg = events_time(gp.replay, max(1, args.steps // inner), torch) / inner
     ms_og = events_time(go.replay, max(1, args.steps // inner), torch) / inner
     # the node's form: x quantized by the add-norm that writes it, the o_proj input by the attention's
@@ -409,6 +441,7 @@ def bench_attn(args, torch, dev):
             for _ in range(inner):
                 fn()
         torch.cuda.synchronize()
+        settle(g.replay, torch, SETTLE_MS / 5)
         return events_time(g.replay, max(1, args.steps // inner), torch) / inner
 
     ms_pq, ms_oq = graph_ms(proj_q), graph_ms(oproj_q)
@@ -449,6 +482,7 @@ def bench_decode(args, torch, dev):
         for _ in range(max(1, args.warmup)):
             step()
         torch.cuda.synchronize()
+        settle(step, torch)
         ms = events_time(step, args.steps, torch)
         # algorithmic bytes: every cached key's K and V row of both KV heads, the page-table
         # entries, the queries and the outputs
@@ -512,6 +546,7 @@ def _hybrid_form(args, torch, dev, hybrid, synth, w, B, T, ctx, form):
         torch.cuda.synchronize()
         if not torch.equal(ws.bufs["ids"], ids_eager):
             raise RuntimeError(f"hybrid node ({form}): a graph replay's ids differ from the eager step's")
+    settle(graph.replay, torch)
     ms = events_time(graph.replay, args.steps, torch)
     del st, ws
     return dict(us_per_step=ms * 1e3, us_eager=ms_eager * 1e3, rows=B * T, tokens_per_s=B * T / (ms * 1e-3),
@@ -550,6 +585,7 @@ def bench_lmhead(args, torch, dev):
         step()
         step_rm()
     torch.cuda.synchronize()
+    settle(lambda: (step(), step_rm()), torch)
     # the two forms in alternating rounds of a few calls, the order swapped every round (the clock
     # drifts over a run), medians of the rounds
     n_per, rounds = 3, max(4, args.steps // 3)
@@ -679,10 +715,13 @@ def cpu_baselines(moe_res, seconds):
 
 
 def main():
+    global SETTLE_MS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="untimed repeats of each leg's work (ms of wall time) before its timed region")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="moe,moe_high_u,gdn,gdn_ring,lmhead,attn,decode,hybrid,small",
@@ -691,6 +730,7 @@ def main():
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 256 MiB device copy (the reference kernel for HBM counters)")
     args = ap.parse_args()
+    SETTLE_MS = max(0.0, args.settle_ms)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the MoE, GDN and lm_head nodes are measured on one "
                                    "MI355X; multi-GPU sharding is a design note only"}))
@@ -758,7 +798,7 @@ def main():
     if moe_res is None:
         # a run of single legs (--only without moe, e.g. under a profiler): no headline
         line = {"metric": "per-leg run (no headline: --only without moe)", "value": None, "n_gpus": 1,
-                "legs": sorted(only)}
+                "legs": sorted(only), "settle_ms": SETTLE_MS}
         legs = {"lmhead": lmh_res, "attn": attn_res, "decode": dec_res, "hybrid": hyb_res, "gdn": gdn_res,
                 "gdn_ring": ring_res, "small": small_res}
         for k, v in legs.items():
@@ -780,6 +820,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": SETTLE_MS,
         "ms_per_step": round(moe_res["ms_graph"], 4),
         "higher_is_better": True,
         "scaling": "weak",
