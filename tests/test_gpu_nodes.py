@@ -374,3 +374,42 @@ def test_lmhead_node_writes_the_fp32_logits_buffer(dev, R):
     meta_x = types.SimpleNamespace(forward_mode=_Mode("extend"), next_token_logits_buffer=None)
     out_x = node.forward(prepared, None, h, head, meta_x)
     assert out_x.dtype == torch.bfloat16 and torch.equal(out_x, ref)
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")  # the decision capture launches nothing
+def test_lmhead_node_under_graph_capture(dev):
+    """Under capture the node builds neither its int8 copy nor its workspace (both allocate and launch
+    work of their own), so a batch captured before any eager call goes to the stock product.  Once an
+    eager call has made them, a captured call runs the int8 path, and its replays give the eager
+    logits and ids."""
+    from bundles_amd.qwen36_lmhead8 import node
+    R, V = 100, 4096
+    g = torch.Generator(device=dev).manual_seed(77)
+    h = torch.randn((R, 2048), generator=g, device=dev).to(torch.bfloat16)
+    head = _Holder(weight=(torch.randn((V, 2048), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+    prepared = node.prepare(_Processor())
+    print("lmhead node under capture: decisions", flush=True)
+    empty = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(empty):  # nothing is launched inside: only the decisions are checked
+        no_copy = prepared.copy_for(head.weight)
+        no_ws = prepared.workspace_for(h.device)
+    assert no_copy is None and no_ws is None
+    assert prepared.copy is None and prepared.workspace is None
+    del empty
+    print("lmhead node under capture: int8 path", flush=True)
+    ref = node.forward(prepared, None, h, head).clone()
+    ids = prepared.last_ids.clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = node.forward(prepared, None, h, head)
+    got_ids = prepared.last_ids
+    for _ in range(3):
+        out.fill_(0)
+        got_ids.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+        assert torch.equal(got_ids, ids)
+        node.forward(prepared, None, torch.randn((R, 2048), device=dev).to(torch.bfloat16), head)
+        torch.cuda.synchronize()
