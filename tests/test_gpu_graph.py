@@ -190,3 +190,29 @@ def test_graph_gdn_verify_ring(lib, dev):
                                          1e-6, d["scale"], T=T)
 
     _check_replays("gdn ring B=8 T=5", call, lambda r: [r], restore=restore, state=[d[k] for k in pools])
+
+
+@pytest.mark.parametrize("form", ["snapshot", "ring"])
+def test_graph_hybrid_step(lib, dev, form):
+    """The whole hybrid verify step (3 GDN + 1 attention layer, each with its MoE, the add-norms, the
+    final norm and the int8 lm_head), captured as the bench runs it: with the KV cache, conv states and
+    ring pools restored before each replay, every replay gives the eager step's ids and state."""
+    from bundles_amd import synth
+    from bundles_amd.qwen36_layer import hybrid
+    B, T, CTX, E, V = 2, 4, 40, 64, 4096
+    w = hybrid.make_weights(dev, seed=3, E=E, V=V)
+    st = hybrid.make_state(B, T, CTX, dev, seed=4, gdn_form=form)
+    ws = hybrid.HybridWorkspace(B, T, E, dev)
+    x = synth.randn((B * T, 2048), synth.gen(dev, 5), dev)
+    x2 = synth.randn((B * T, 2048), synth.gen(dev, 6), dev)
+    state = [st.k_cache, st.v_cache] + list(st.conv_state) + list(st.S)
+    for r in st.ring or []:
+        state += [t for t in r.values() if isinstance(t, torch.Tensor)]
+    saved = [t.clone() for t in state]
+
+    def restore():
+        for t, s in zip(state, saved):
+            t.copy_(s)
+
+    _check_replays(f"hybrid step {form}", lambda: hybrid.forward(x, w, st, ws), lambda r: [r],
+                   other=lambda: hybrid.forward(x2, w, st, ws), restore=restore, state=state)
