@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_bf16_close, bits16, bits8, np_
+from helpers import assert_bf16_close, bits16, bits8, elementwise_rel, np_
 
 pytestmark = pytest.mark.gpu
 
@@ -146,7 +146,10 @@ def _run_moe(q36, O, dev, M, E, dtype, seed, zipf=None, padded=False, debug=True
     return out, ws.views(M), dbg, r, pos
 
 
-MOE_CASES = [(1, 64, 0), (8, 64, 0), (37, 128, 0), (64, 64, 0), (1, 64, 1), (8, 64, 1), (37, 128, 1), (64, 64, 1)]
+MOE_CASES = [(1, 64, 0), (8, 64, 0), (37, 128, 0), (64, 64, 0), (1, 64, 1), (8, 64, 1), (37, 128, 1), (64, 64, 1),
+             # int8 (bit-exact end to end) one token past the 16-, 32- and 64-token block edges of the expert
+             # work items; the fp8 forms of such ragged batches are checked stage by stage below
+             (17, 64, 0), (33, 128, 0), (65, 64, 0), (97, 64, 0)]
 
 
 @pytest.mark.parametrize("M,E,dtype", MOE_CASES)
@@ -240,11 +243,24 @@ def test_moe_config2_fp8_stages(q36, oracle_mod, dev, seed):
     the down stage fed the GPU's own h (teacher forcing) each within the bf16 bar, with elementwise
     errors and the number of re-quantization group scales that differ reported; the combine fed the
     GPU's own weighted expert rows bit-exact; and the block end to end."""
+    _fp8_stages(q36, oracle_mod, dev, 64, 512, seed, zipf=1.1, e2e=True)
+
+
+@pytest.mark.parametrize("M,E,seed", [(33, 128, 133), (97, 64, 197), (17, 512, 5)])
+def test_moe_fp8_stages_ragged(q36, oracle_mod, dev, M, E, seed):
+    """Ragged fp8 batches (one token past a work item's 16-, 32- or 64-token edge), stage by stage with the
+    same bars as config 2.  The end-to-end error is reported, not asserted: the down stage re-quantizes h
+    to e4m3 per 128-group, so a one-ulp difference in h (2 % of its elements, from the MFMA's summation
+    order) can move a 3-bit mantissa code or a group scale, and a row whose output nearly cancels then
+    shows that step as a large relative error (33 x 128 experts, seed 133: 1.3e-2 end to end, while each
+    stage alone is within its bar)."""
+    _fp8_stages(q36, oracle_mod, dev, M, E, seed, zipf=None, e2e=False)
+
+
+def _fp8_stages(q36, O, dev, M, E, seed, zipf, e2e):
     from bundles_amd import synth
-    O = oracle_mod
-    M, E = 64, 512
-    print(f"moe config2 stages seed={seed}", flush=True)
-    d = synth.moe_inputs(M, dev, seed=seed, E=E, zipf=1.1)
+    print(f"moe fp8 stages M={M} E={E} seed={seed}", flush=True)
+    d = synth.moe_inputs(M, dev, seed=seed, E=E, zipf=zipf)
     ew = q36.prepare_experts(d["w13"], d["w2"], d["sw13"], d["sw2"], q36.Q36_MOE_FP8)
     ws = q36.Workspace(E, 2048, 512, 10, q36.Q36_MOE_FP8, dev)
     S = M * 10
@@ -256,7 +272,7 @@ def test_moe_config2_fp8_stages(q36, oracle_mod, dev, seed):
     hw = _host_weights(ew)
     args = (1, bits16(d["x"]), bits16(d["router_w"]), hw["w13"], hw["s13"], hw["w2"], hw["s2"], hw["sw13"],
             hw["ss13"], hw["sw2"], hw["ss2"], bits16(d["gate_w"]), 10)
-    kw = dict(bias=np_(d["router_bias"]), debug=True)
+    kw = dict(bias=None if d["router_bias"] is None else np_(d["router_bias"]), debug=True)
     r = O.moe(*args, **kw)
     assert np.array_equal(np_(v["ids"]), r["ids"])
     # x quantization: e4m3 codes and per-(token, 128-group) scales
@@ -275,7 +291,12 @@ def test_moe_config2_fp8_stages(q36, oracle_mod, dev, seed):
     # combine fed the GPU's y: the same fp32 sums in the same order
     rc = O.moe(*args, **kw, y_in=y_gpu)
     assert np.array_equal(bits16(out), rc["out"]), "combine (teacher forced) must be bit-exact"
-    e2e = assert_bf16_close(bits16(out), r["out"], 1e-2, "config 2 out")
+    if e2e:
+        e2e = assert_bf16_close(bits16(out), r["out"], 1e-2, "config 2 out")
+    else:
+        g2, r2 = O.bf16_to_f32(bits16(out)).astype(np.float64), O.bf16_to_f32(r["out"]).astype(np.float64)
+        row = np.linalg.norm(g2 - r2, axis=-1) / np.maximum(np.linalg.norm(r2, axis=-1), 1e-30)
+        e2e = (float(row.max()), elementwise_rel(g2, r2), float(np.mean(bits16(out) == r["out"])))
     print(f"seed {seed}: h exact {up[2]:.4f} row {up[0]:.2e} elem {up[1]:.2e}; group scales differing "
           f"{n_scale}/{hs_ref.size}; down(tf) row {dn[0]:.2e} elem {dn[1]:.2e} exact {dn[2]:.4f}; "
           f"end-to-end row {e2e[0]:.2e} elem {e2e[1]:.2e} exact {e2e[2]:.4f}", flush=True)
